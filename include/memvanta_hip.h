@@ -1,0 +1,128 @@
+/*
+ * memvanta_hip.h -- C ABI of the MI355X (gfx950) backend for MemVanta's
+ * quantized-matmul + paged F16 attention hot path.
+ *
+ * Plain C: pointers, sizes and int status codes; no exceptions or C++/torch
+ * types cross it.  Every call returns MVH_OK (0) or an MVH_E_* code and leaves
+ * a message in mvh_last_error() (thread-local) that carries the same text the
+ * reference throws (e.g. "Q4_0 matrix row not block aligned: <tensor>").
+ *
+ * Weights are uploaded once in their native GGUF block layout (Q4_0 18-byte,
+ * Q8_0 34-byte, Q6_K 210-byte blocks; GGML order ne0 = cols, ne1 = rows) and
+ * are never repacked.  Activation/result pointers are host memory
+ * (MVH_HOST: the call stages, launches and synchronises) or device memory
+ * (MVH_DEVICE: the call only enqueues on the context's stream).
+ *
+ * Reference interfaces replaced (MemVanta file:line):
+ *   mvh_matvec            tensor_matvec            include/memvanta/gguf_kernels.hpp:26,
+ *                                                  src/gguf_kernels.cpp:244-253
+ *   mvh_matmul_batch      tensor_matmul_batch      gguf_kernels.hpp:27, src/gguf_kernels.cpp:255-259
+ *   mvh_matmul_batch_v06  tensor_matmul_batch_v06  gguf_kernels.hpp:30, src/gguf_kernels.cpp:261-271
+ *   mvh_read_row_f32      tensor_read_row_f32      gguf_kernels.hpp:25, src/gguf_kernels.cpp:226
+ *   mvh_quantize_q8       quantize_q8 / quantize_activations_q8 (file-local)
+ *                                                  src/gguf_kernels.cpp:160-178
+ *   mvh_fp32_to_fp16      fp32_to_fp16             gguf_kernels.hpp:34, src/gguf_kernels.cpp:242
+ *   mvh_fp16_to_fp32      fp16_to_fp32             include/memvanta/gguf.hpp:80, src/gguf.cpp:110-119
+ *   mvh_kv_*              PagedKVCache             include/memvanta/llama_model.hpp:32-52,
+ *                                                  src/llama_model.cpp:18-56
+ *   mvh_attn_decode       the per-head dot_key/softmax/add_value loop of
+ *                         LlamaModel::forward      src/llama_model.cpp:256
+ *   mvh_tensor_upload     GgufFile::tensor_data    include/memvanta/gguf.hpp:57, src/gguf.cpp:139
+ *                         (the bytes it returns are copied to HBM once)
+ */
+#ifndef MEMVANTA_HIP_H
+#define MEMVANTA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define MVH_OK 0
+#define MVH_E_INVALID 1  /* null handle / bad argument */
+#define MVH_E_SHAPE 2    /* shape or block-alignment error */
+#define MVH_E_TYPE 3     /* unsupported GGML tensor type */
+#define MVH_E_DEVICE 4   /* HIP runtime error */
+#define MVH_E_RANGE 5    /* position / row / layer out of range, missing KV page */
+#define MVH_E_NOMEM 6    /* device allocation failed */
+
+/* where activation / result pointers live */
+#define MVH_HOST 0
+#define MVH_DEVICE 1
+
+/* numerics of the batched (prefill) matmul, tensor_matmul_batch_v06 */
+#define MVH_ACT_REF 0 /* default: fp32 activations, 4/8-token blocking (q4/q8_row_batch4_fp32) */
+#define MVH_ACT_Q8 1  /* MEMVANTA_FORCE_Q8_ACT=1: per-token Q8 activations; Q4_0 on int8 MFMA */
+
+/* GGML type ids accepted by mvh_tensor_upload */
+#define MVH_TYPE_F32 0
+#define MVH_TYPE_F16 1
+#define MVH_TYPE_Q4_0 2
+#define MVH_TYPE_Q8_0 8
+#define MVH_TYPE_Q6_K 14
+
+typedef struct mvh_context mvh_context;
+typedef struct mvh_tensor mvh_tensor;
+typedef struct mvh_kv_cache mvh_kv_cache;
+
+/* ---- library / context ---- */
+const char* mvh_last_error(void);
+int mvh_version(void);
+int mvh_device_count(int* count);
+/* one context = one device + one HIP stream (default priority) */
+int mvh_context_create(int device, mvh_context** out);
+int mvh_context_destroy(mvh_context* ctx);
+/* the hipStream_t every call of this context is enqueued on */
+int mvh_context_stream(mvh_context* ctx, void** stream);
+int mvh_context_synchronize(mvh_context* ctx);
+
+/* ---- weights (GgufFile::tensor_data bytes, uploaded once) ---- */
+int mvh_tensor_upload(mvh_context* ctx, const char* name, uint32_t ggml_type, uint64_t ne0, uint64_t ne1,
+                      const void* host_bytes, uint64_t nbytes, mvh_tensor** out);
+/* borrow device memory the caller owns (already in the native layout) */
+int mvh_tensor_wrap(mvh_context* ctx, const char* name, uint32_t ggml_type, uint64_t ne0, uint64_t ne1,
+                    const void* device_bytes, uint64_t nbytes, mvh_tensor** out);
+int mvh_tensor_free(mvh_tensor* t);
+int mvh_tensor_info(const mvh_tensor* t, uint32_t* ggml_type, uint64_t* ne0, uint64_t* ne1, uint64_t* nbytes,
+                    const void** device_bytes);
+
+/* ---- kernels ---- */
+/* quantize_activations_q8: x[batch][cols] -> q[batch][cols] int8 + d[batch][cols/32] f32 */
+int mvh_quantize_q8(mvh_context* ctx, const float* x, size_t batch, size_t cols, int8_t* q, float* d, int ptr_kind);
+/* tensor_matvec: y[ne1] = W . x[ne0] */
+int mvh_matvec(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, int ptr_kind);
+/* tensor_matmul_batch: y[b*ne1 + r] = row r . x[b*ne0 ..], fp32 activations */
+int mvh_matmul_batch(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, size_t batch, int ptr_kind);
+/* tensor_matmul_batch_v06 with its fallbacks; act_mode MVH_ACT_REF or MVH_ACT_Q8.  As in the
+ * reference, tensors named *.ffn_gate.* / *.ffn_up.* / *.ffn_down.* use 8-token blocking (it changes
+ * which tokens of a batch fall in the unblocked tail). */
+int mvh_matmul_batch_v06(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, size_t batch,
+                         int act_mode, int ptr_kind);
+/* tensor_read_row_f32 (embedding row) */
+int mvh_read_row_f32(mvh_context* ctx, const mvh_tensor* w, size_t row, float* out, int ptr_kind);
+/* fp32_to_fp16 (the reference's rounding, bit for bit) and the exact fp16_to_fp32 */
+int mvh_fp32_to_fp16(mvh_context* ctx, const float* x, uint16_t* out, size_t n, int ptr_kind);
+int mvh_fp16_to_fp32(mvh_context* ctx, const uint16_t* h, float* out, size_t n, int ptr_kind);
+
+/* ---- paged F16 KV cache: all layers of one model on one device ---- */
+int mvh_kv_create(mvh_context* ctx, size_t n_layer, size_t kv_dim, size_t page_tokens, size_t max_tokens,
+                  mvh_kv_cache** out);
+int mvh_kv_destroy(mvh_kv_cache* kv);
+int mvh_kv_reset(mvh_kv_cache* kv);
+int mvh_kv_bytes_allocated(const mvh_kv_cache* kv, size_t* bytes);
+/* PagedKVCache::write for n_tokens consecutive positions pos..pos+n-1; k/v are [n][kv_dim] fp32 */
+int mvh_kv_write(mvh_context* ctx, mvh_kv_cache* kv, size_t layer, size_t pos, size_t n_tokens, const float* k,
+                 const float* v, int ptr_kind);
+/* copy the stored fp16 row of (layer, pos): which = 0 for K, 1 for V; out is host memory [kv_dim] */
+int mvh_kv_read_row(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, size_t pos, int which, uint16_t* out);
+/* decode attention of one layer over positions 0..pos: q[n_head*hd] -> out[n_head*hd] */
+int mvh_attn_decode(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos,
+                    size_t n_head, size_t n_head_kv, size_t head_dim, float* out, int ptr_kind);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MEMVANTA_HIP_H */

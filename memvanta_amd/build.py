@@ -1,0 +1,56 @@
+"""Build the gfx950 HIP library (and, on request, the CPU checker libraries).
+
+    python -m memvanta_amd.build            # libmemvanta_hip.so
+    python -m memvanta_amd.build --all      # + oracle/liboracle.so (+ oracle/_ref when the reference exists)
+"""
+from __future__ import annotations
+
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB = os.path.join(HERE, "libmemvanta_hip.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# -ffp-contract=off: every FMA in the kernels is written out, nothing else fuses.
+# -packed-fp32-ops off: no v_pk_*_f32 in the generated code.
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _run(cmd, cwd=ROOT):
+    p = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in p.stdout.splitlines() if "packed-fp32-ops' is not a recognized feature" not in l
+                    and "warning: feature flag" not in l)
+    if p.returncode != 0:
+        raise RuntimeError(f"command failed ({p.returncode}): {' '.join(cmd)}\n{out}")
+    return out
+
+
+def build_hip(verbose: bool = False) -> str:
+    srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(HERE, 'csrc')}", "-o", tmp, *srcs]
+    out = _run(cmd)
+    os.replace(tmp, LIB)
+    if verbose and out.strip():
+        print(out)
+    return LIB
+
+
+def build_oracle(with_ref: bool | None = None) -> None:
+    targets = ["oracle"]
+    if with_ref is None:
+        with_ref = os.path.isdir("/root/reference/src")
+    if with_ref:
+        targets.append("ref")
+    _run(["make", "-C", os.path.join(ROOT, "oracle"), "-j4", *targets])
+
+
+if __name__ == "__main__":
+    print(build_hip(verbose=True))
+    if "--all" in sys.argv:
+        build_oracle()
+        print("oracle built")

@@ -1,0 +1,284 @@
+"""ctypes binding of the C ABI in include/memvanta_hip.h (libmemvanta_hip.so).
+
+There is no fallback: if the HIP library is missing or a call fails, an
+exception is raised.  Host arrays are numpy; device buffers are anything with
+an integer device address (torch tensors' ``data_ptr()``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmemvanta_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "memvanta_hip.h")
+
+MVH_HOST, MVH_DEVICE = 0, 1
+MVH_ACT_REF, MVH_ACT_Q8 = 0, 1
+STATUS = {0: "MVH_OK", 1: "MVH_E_INVALID", 2: "MVH_E_SHAPE", 3: "MVH_E_TYPE", 4: "MVH_E_DEVICE",
+          5: "MVH_E_RANGE", 6: "MVH_E_NOMEM"}
+
+
+class MvhError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+        self.code = code
+        self.msg = msg
+
+
+def header_functions(path: str = HEADER) -> list[str]:
+    """Names of every function the C header declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mvh_[a-z0-9_]+)\s*\(", text)))
+
+
+_vp, _sz, _u32, _u64, _int = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_int
+_SIGS = {
+    "mvh_last_error": (C.c_char_p, []),
+    "mvh_version": (_int, []),
+    "mvh_device_count": (_int, [C.POINTER(_int)]),
+    "mvh_context_create": (_int, [_int, C.POINTER(_vp)]),
+    "mvh_context_destroy": (_int, [_vp]),
+    "mvh_context_stream": (_int, [_vp, C.POINTER(_vp)]),
+    "mvh_context_synchronize": (_int, [_vp]),
+    "mvh_tensor_upload": (_int, [_vp, C.c_char_p, _u32, _u64, _u64, _vp, _u64, C.POINTER(_vp)]),
+    "mvh_tensor_wrap": (_int, [_vp, C.c_char_p, _u32, _u64, _u64, _vp, _u64, C.POINTER(_vp)]),
+    "mvh_tensor_free": (_int, [_vp]),
+    "mvh_tensor_info": (_int, [_vp, C.POINTER(_u32), C.POINTER(_u64), C.POINTER(_u64), C.POINTER(_u64),
+                               C.POINTER(_vp)]),
+    "mvh_quantize_q8": (_int, [_vp, _vp, _sz, _sz, _vp, _vp, _int]),
+    "mvh_matvec": (_int, [_vp, _vp, _vp, _vp, _int]),
+    "mvh_matmul_batch": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
+    "mvh_matmul_batch_v06": (_int, [_vp, _vp, _vp, _vp, _sz, _int, _int]),
+    "mvh_read_row_f32": (_int, [_vp, _vp, _sz, _vp, _int]),
+    "mvh_fp32_to_fp16": (_int, [_vp, _vp, _vp, _sz, _int]),
+    "mvh_fp16_to_fp32": (_int, [_vp, _vp, _vp, _sz, _int]),
+    "mvh_kv_create": (_int, [_vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]),
+    "mvh_kv_destroy": (_int, [_vp]),
+    "mvh_kv_reset": (_int, [_vp]),
+    "mvh_kv_bytes_allocated": (_int, [_vp, C.POINTER(_sz)]),
+    "mvh_kv_write": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
+    "mvh_kv_read_row": (_int, [_vp, _vp, _sz, _sz, _int, _vp]),
+    "mvh_attn_decode": (_int, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _vp, _int]),
+}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"HIP backend not built: {path} is missing (run __graft_entry__.build())")
+    lib = C.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _ptr(a) -> int | None:
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        if not a.flags["C_CONTIGUOUS"]:
+            raise ValueError("host array must be C-contiguous")
+        return a.ctypes.data
+    if hasattr(a, "data_ptr"):
+        return a.data_ptr()
+    return int(a)
+
+
+def _kind(*arrs) -> int:
+    dev = [not isinstance(a, np.ndarray) for a in arrs if a is not None]
+    if all(dev):
+        return MVH_DEVICE
+    if not any(dev):
+        return MVH_HOST
+    raise ValueError("mix of host and device buffers in one call")
+
+
+class Context:
+    """One device + one HIP stream (mvh_context)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = _vp()
+        self._check(self.lib.mvh_context_create(device, C.byref(h)))
+        self.h = h.value
+        self.device = device
+
+    def _check(self, rc: int):
+        if rc != 0:
+            raise MvhError(rc, self.lib.mvh_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.mvh_context_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        s = _vp()
+        self._check(self.lib.mvh_context_stream(self.h, C.byref(s)))
+        return s.value
+
+    def synchronize(self):
+        self._check(self.lib.mvh_context_synchronize(self.h))
+
+    # -- weights --
+    def upload(self, name: str, ggml_type: int, ne0: int, ne1: int, data: np.ndarray) -> "Tensor":
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        t = _vp()
+        self._check(self.lib.mvh_tensor_upload(self.h, name.encode(), ggml_type, ne0, ne1, data.ctypes.data,
+                                               data.nbytes, C.byref(t)))
+        return Tensor(self, t.value, name, ggml_type, ne0, ne1)
+
+    def wrap(self, name: str, ggml_type: int, ne0: int, ne1: int, dev_ptr: int, nbytes: int) -> "Tensor":
+        t = _vp()
+        self._check(self.lib.mvh_tensor_wrap(self.h, name.encode(), ggml_type, ne0, ne1, dev_ptr, nbytes,
+                                             C.byref(t)))
+        return Tensor(self, t.value, name, ggml_type, ne0, ne1)
+
+    # -- kernels (host numpy in/out, or device pointers) --
+    def quantize_q8(self, x, q=None, d=None):
+        if isinstance(x, np.ndarray):
+            x = np.ascontiguousarray(x, np.float32)
+            m = 1 if x.ndim == 1 else x.shape[0]
+            k = x.shape[-1]
+            q = np.empty(x.shape, np.int8)
+            d = np.empty(x.shape[:-1] + (k // 32,), np.float32)
+            self._check(self.lib.mvh_quantize_q8(self.h, x.ctypes.data, m, k, q.ctypes.data, d.ctypes.data, MVH_HOST))
+            return q, d
+        m = 1 if x.dim() == 1 else x.shape[0]
+        k = x.shape[-1]
+        self._check(self.lib.mvh_quantize_q8(self.h, _ptr(x), m, k, _ptr(q), _ptr(d), MVH_DEVICE))
+        return q, d
+
+    def matvec(self, w: "Tensor", x, y=None):
+        if y is None:
+            y = np.empty(w.ne1, np.float32)
+            x = np.ascontiguousarray(x, np.float32)
+        self._check(self.lib.mvh_matvec(self.h, w.h, _ptr(x), _ptr(y), _kind(x, y)))
+        return y
+
+    def matmul_batch(self, w: "Tensor", x, y=None):
+        b = x.shape[0]
+        if y is None:
+            x = np.ascontiguousarray(x, np.float32)
+            y = np.empty((b, w.ne1), np.float32)
+        self._check(self.lib.mvh_matmul_batch(self.h, w.h, _ptr(x), _ptr(y), b, _kind(x, y)))
+        return y
+
+    def matmul_batch_v06(self, w: "Tensor", x, act_mode: int = MVH_ACT_REF, y=None):
+        b = x.shape[0]
+        if y is None:
+            x = np.ascontiguousarray(x, np.float32)
+            y = np.empty((b, w.ne1), np.float32)
+        self._check(self.lib.mvh_matmul_batch_v06(self.h, w.h, _ptr(x), _ptr(y), b, act_mode, _kind(x, y)))
+        return y
+
+    def read_row(self, w: "Tensor", row: int, out=None):
+        if out is None:
+            out = np.empty(w.ne0, np.float32)
+        self._check(self.lib.mvh_read_row_f32(self.h, w.h, row, _ptr(out), _kind(out)))
+        return out
+
+    def fp32_to_fp16(self, x, out=None):
+        if out is None:
+            x = np.ascontiguousarray(x, np.float32).ravel()
+            out = np.empty(x.size, np.uint16)
+        n = x.size if isinstance(x, np.ndarray) else x.numel()
+        self._check(self.lib.mvh_fp32_to_fp16(self.h, _ptr(x), _ptr(out), n, _kind(x, out)))
+        return out
+
+    def fp16_to_fp32(self, h, out=None):
+        if out is None:
+            h = np.ascontiguousarray(h, np.uint16).ravel()
+            out = np.empty(h.size, np.float32)
+        n = h.size if isinstance(h, np.ndarray) else h.numel()
+        self._check(self.lib.mvh_fp16_to_fp32(self.h, _ptr(h), _ptr(out), n, _kind(h, out)))
+        return out
+
+    def kv_cache(self, n_layer: int, kv_dim: int, page_tokens: int = 128, max_tokens: int = 2048) -> "KVCache":
+        return KVCache(self, n_layer, kv_dim, page_tokens, max_tokens)
+
+
+class Tensor:
+    def __init__(self, ctx: Context, h: int, name: str, ggml_type: int, ne0: int, ne1: int):
+        self.ctx, self.h, self.name, self.type, self.ne0, self.ne1 = ctx, h, name, ggml_type, ne0, ne1
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.mvh_tensor_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def info(self):
+        ty, n0, n1, nb, dp = _u32(), _u64(), _u64(), _u64(), _vp()
+        self.ctx._check(self.ctx.lib.mvh_tensor_info(self.h, C.byref(ty), C.byref(n0), C.byref(n1), C.byref(nb),
+                                                     C.byref(dp)))
+        return ty.value, n0.value, n1.value, nb.value, dp.value
+
+
+class KVCache:
+    def __init__(self, ctx: Context, n_layer, kv_dim, page_tokens, max_tokens):
+        self.ctx, self.kv_dim = ctx, kv_dim
+        h = _vp()
+        ctx._check(ctx.lib.mvh_kv_create(ctx.h, n_layer, kv_dim, page_tokens, max_tokens, C.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.ctx.lib.mvh_kv_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def reset(self):
+        self.ctx._check(self.ctx.lib.mvh_kv_reset(self.h))
+
+    def bytes_allocated(self) -> int:
+        n = _sz()
+        self.ctx._check(self.ctx.lib.mvh_kv_bytes_allocated(self.h, C.byref(n)))
+        return n.value
+
+    def write(self, layer, pos, k, v):
+        if isinstance(k, np.ndarray):
+            k = np.ascontiguousarray(k, np.float32)
+            v = np.ascontiguousarray(v, np.float32)
+            n = k.size // self.kv_dim
+        else:
+            n = k.numel() // self.kv_dim
+        self.ctx._check(self.ctx.lib.mvh_kv_write(self.ctx.h, self.h, layer, pos, n, _ptr(k), _ptr(v), _kind(k, v)))
+
+    def read_row(self, layer, pos, which):
+        out = np.empty(self.kv_dim, np.uint16)
+        self.ctx._check(self.ctx.lib.mvh_kv_read_row(self.ctx.h, self.h, layer, pos, which, out.ctypes.data))
+        return out
+
+    def attn_decode(self, layer, q, pos, n_head, n_head_kv, head_dim, out=None):
+        if out is None:
+            q = np.ascontiguousarray(q, np.float32)
+            out = np.empty(n_head * head_dim, np.float32)
+        self.ctx._check(self.ctx.lib.mvh_attn_decode(self.ctx.h, self.h, layer, _ptr(q), pos, n_head, n_head_kv,
+                                                     head_dim, _ptr(out), _kind(q, out)))
+        return out

@@ -1,0 +1,635 @@
+// mvh_capi.hip -- the C ABI declared in include/memvanta_hip.h.
+//
+// Host-side dispatch mirrors the reference's branches and error texts
+// (src/gguf_kernels.cpp:244-271); all arithmetic runs in the gfx950 kernels.
+#include "memvanta_hip.h"
+#include "mvh_kernels.hpp"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+struct mvh_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    struct Buf {
+        void* p = nullptr;
+        size_t cap = 0;
+    };
+    Buf act;      // Q8 activations: q | d | s
+    Buf xin;      // host-pointer staging of inputs
+    Buf yout;     // host-pointer staging of outputs
+    Buf scratch;  // attention scores
+};
+
+struct mvh_tensor {
+    mvh_context* ctx = nullptr;
+    std::string name;
+    uint32_t type = 0;
+    uint64_t ne0 = 0, ne1 = 0, nbytes = 0;
+    void* d = nullptr;
+    bool owned = false;
+};
+
+struct mvh_kv_cache {
+    mvh_context* ctx = nullptr;
+    size_t n_layer = 0, kv_dim = 0, page_tokens = 0, max_tokens = 0, max_pages = 0;
+    std::vector<uint16_t*> hk, hv;  // host mirror of the page tables, [layer*max_pages + page]
+    uint16_t** dk = nullptr;        // device page tables
+    uint16_t** dv = nullptr;
+    std::vector<uint16_t*> pool;    // released page slabs (K page followed by V page)
+    size_t live_pages = 0;
+    size_t page_elems() const { return page_tokens * kv_dim; }
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define MVH_HIP(expr)                                                                       \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return fail(MVH_E_DEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+const char* type_name(uint32_t t) {
+    switch (t) {
+        case MVH_TYPE_F32: return "F32";
+        case MVH_TYPE_F16: return "F16";
+        case MVH_TYPE_Q4_0: return "Q4_0";
+        case MVH_TYPE_Q8_0: return "Q8_0";
+        case MVH_TYPE_Q6_K: return "Q6_K";
+    }
+    return "type-?";
+}
+
+// ggml_tensor_nbytes (src/gguf.cpp:82-105) for the accepted types; 0 = invalid
+uint64_t tensor_nbytes(uint32_t t, uint64_t n) {
+    switch (t) {
+        case MVH_TYPE_F32: return n * 4;
+        case MVH_TYPE_F16: return n * 2;
+        case MVH_TYPE_Q4_0: return n % 32 ? 0 : n / 32 * 18;
+        case MVH_TYPE_Q8_0: return n % 32 ? 0 : n / 32 * 34;
+        case MVH_TYPE_Q6_K: return n % 256 ? 0 : n / 256 * 210;
+    }
+    return 0;
+}
+
+// is_ffn_tensor (src/gguf_kernels.cpp:50-54)
+bool is_ffn(const std::string& n) {
+    return n.find(".ffn_gate.") != std::string::npos || n.find(".ffn_up.") != std::string::npos ||
+           n.find(".ffn_down.") != std::string::npos;
+}
+
+int grow(mvh_context* c, mvh_context::Buf& b, size_t bytes) {
+    if (bytes <= b.cap) return MVH_OK;
+    if (b.p) {
+        MVH_HIP(hipStreamSynchronize(c->stream));
+        MVH_HIP(hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    const size_t cap = std::max(bytes, static_cast<size_t>(1) << 20);
+    if (hipMalloc(&b.p, cap) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(MVH_E_NOMEM, "device allocation of %zu bytes failed", cap);
+    }
+    b.cap = cap;
+    return MVH_OK;
+}
+
+size_t up16(size_t n) { return (n + 15) & ~static_cast<size_t>(15); }
+
+// Device view of an input: either the caller's device pointer or a staged copy.
+int stage_in(mvh_context* c, mvh_context::Buf& b, const void* src, size_t bytes, int kind, const void** out) {
+    if (kind == MVH_DEVICE) {
+        *out = src;
+        return MVH_OK;
+    }
+    if (kind != MVH_HOST) return fail(MVH_E_INVALID, "ptr_kind must be MVH_HOST or MVH_DEVICE");
+    if (int rc = grow(c, b, bytes)) return rc;
+    MVH_HIP(hipMemcpyAsync(b.p, src, bytes, hipMemcpyHostToDevice, c->stream));
+    *out = b.p;
+    return MVH_OK;
+}
+
+int finish_out(mvh_context* c, void* host_dst, const void* dev_src, size_t bytes, int kind) {
+    if (kind == MVH_DEVICE) return MVH_OK;
+    MVH_HIP(hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost, c->stream));
+    MVH_HIP(hipStreamSynchronize(c->stream));
+    return MVH_OK;
+}
+
+// Q8 activation scratch: q [rows][cols] | d [rows][cols/32] | s [rows][cols/32]
+struct ActView {
+    int8_t* q;
+    float* d;
+    int* s;
+};
+int act_buffers(mvh_context* c, size_t rows, size_t cols, ActView* v) {
+    const size_t nq = up16(rows * cols), nd = up16(rows * (cols / 32) * 4);
+    if (int rc = grow(c, c->act, nq + 2 * nd)) return rc;
+    auto* base = static_cast<uint8_t*>(c->act.p);
+    v->q = reinterpret_cast<int8_t*>(base);
+    v->d = reinterpret_cast<float*>(base + nq);
+    v->s = reinterpret_cast<int*>(base + nq + nd);
+    return MVH_OK;
+}
+
+#define CHECK_CTX(c)                                                   \
+    do {                                                               \
+        if (!(c)) return fail(MVH_E_INVALID, "null context");          \
+        MVH_HIP(hipSetDevice((c)->device));                            \
+    } while (0)
+
+// Per-(token, row) fp32-activation dots with tensor_matmul_batch's dispatch.
+int fp32_rows(mvh_context* c, const mvh_tensor* w, const float* xd, float* yd, size_t batch, const char* what) {
+    const size_t cols = w->ne0, rows = w->ne1;
+    const auto* W = static_cast<const uint8_t*>(w->d);
+    switch (w->type) {
+        case MVH_TYPE_Q4_0:
+            if (cols % 32) return fail(MVH_E_SHAPE, "Q4_0 %s row not block aligned: %s", what, w->name.c_str());
+            MVH_HIP(mvh::launch_gemv_q4_0_f32act(W, xd, yd, rows, cols, batch, c->stream));
+            return MVH_OK;
+        case MVH_TYPE_Q8_0:
+            if (cols % 32) return fail(MVH_E_SHAPE, "Q8_0 %s row not block aligned: %s", what, w->name.c_str());
+            MVH_HIP(mvh::launch_gemv_q8_0(W, xd, yd, rows, cols, batch, c->stream));
+            return MVH_OK;
+        case MVH_TYPE_Q6_K:
+            if (cols % 256) return fail(MVH_E_SHAPE, "Q6_K %s row not block aligned: %s", what, w->name.c_str());
+            MVH_HIP(mvh::launch_gemv_q6_k(W, xd, yd, rows, cols, batch, c->stream));
+            return MVH_OK;
+    }
+    return fail(MVH_E_TYPE, "unsupported %s tensor type %s: %s", what, type_name(w->type), w->name.c_str());
+}
+
+int check_kv(const mvh_kv_cache* kv, size_t layer) {
+    if (!kv) return fail(MVH_E_INVALID, "null KV cache");
+    if (layer >= kv->n_layer) return fail(MVH_E_RANGE, "KV layer %zu out of range", layer);
+    return MVH_OK;
+}
+
+int ensure_page(mvh_kv_cache* kv, size_t layer, size_t p) {
+    const size_t slot = layer * kv->max_pages + p;
+    if (kv->hk[slot]) return MVH_OK;
+    uint16_t* slab = nullptr;
+    if (!kv->pool.empty()) {
+        slab = kv->pool.back();
+        kv->pool.pop_back();
+    } else if (hipMalloc(&slab, 2 * kv->page_elems() * sizeof(uint16_t)) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(MVH_E_NOMEM, "KV page allocation failed");
+    }
+    kv->hk[slot] = slab;
+    kv->hv[slot] = slab + kv->page_elems();
+    ++kv->live_pages;
+    MVH_HIP(hipMemcpy(kv->dk + slot, &kv->hk[slot], sizeof(uint16_t*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dv + slot, &kv->hv[slot], sizeof(uint16_t*), hipMemcpyHostToDevice));
+    return MVH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mvh_last_error(void) { return g_err.c_str(); }
+int mvh_version(void) { return 1; }
+
+int mvh_device_count(int* count) {
+    if (!count) return fail(MVH_E_INVALID, "null count");
+    MVH_HIP(hipGetDeviceCount(count));
+    return MVH_OK;
+}
+
+int mvh_context_create(int device, mvh_context** out) {
+    if (!out) return fail(MVH_E_INVALID, "null out");
+    *out = nullptr;
+    MVH_HIP(hipSetDevice(device));
+    auto* c = new (std::nothrow) mvh_context;
+    if (!c) return fail(MVH_E_NOMEM, "host allocation failed");
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fail(MVH_E_DEVICE, "hipStreamCreate failed");
+    }
+    *out = c;
+    return MVH_OK;
+}
+
+int mvh_context_destroy(mvh_context* c) {
+    if (!c) return MVH_OK;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (auto* b : {&c->act, &c->xin, &c->yout, &c->scratch})
+        if (b->p) (void)hipFree(b->p);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return MVH_OK;
+}
+
+int mvh_context_stream(mvh_context* c, void** stream) {
+    if (!c || !stream) return fail(MVH_E_INVALID, "null argument");
+    *stream = c->stream;
+    return MVH_OK;
+}
+
+int mvh_context_synchronize(mvh_context* c) {
+    CHECK_CTX(c);
+    MVH_HIP(hipStreamSynchronize(c->stream));
+    return MVH_OK;
+}
+
+static int make_tensor(mvh_context* c, const char* name, uint32_t type, uint64_t ne0, uint64_t ne1, uint64_t nbytes,
+                       mvh_tensor** out) {
+    if (!out) return fail(MVH_E_INVALID, "null out");
+    *out = nullptr;
+    const uint64_t want = tensor_nbytes(type, ne0 * ne1);
+    if (type != MVH_TYPE_F32 && type != MVH_TYPE_F16 && type != MVH_TYPE_Q4_0 && type != MVH_TYPE_Q8_0 &&
+        type != MVH_TYPE_Q6_K)
+        return fail(MVH_E_TYPE, "unsupported GGML type %u: %s", type, name ? name : "");
+    if (!want || want != nbytes)
+        return fail(MVH_E_SHAPE, "tensor byte size %llu does not match %s [%llu x %llu]: %s",
+                    static_cast<unsigned long long>(nbytes), type_name(type), static_cast<unsigned long long>(ne1),
+                    static_cast<unsigned long long>(ne0), name ? name : "");
+    auto* t = new (std::nothrow) mvh_tensor;
+    if (!t) return fail(MVH_E_NOMEM, "host allocation failed");
+    t->ctx = c;
+    t->name = name ? name : "";
+    t->type = type;
+    t->ne0 = ne0;
+    t->ne1 = ne1;
+    t->nbytes = nbytes;
+    *out = t;
+    return MVH_OK;
+}
+
+int mvh_tensor_upload(mvh_context* c, const char* name, uint32_t type, uint64_t ne0, uint64_t ne1,
+                      const void* host_bytes, uint64_t nbytes, mvh_tensor** out) {
+    CHECK_CTX(c);
+    if (!host_bytes && nbytes) return fail(MVH_E_INVALID, "null tensor bytes");
+    mvh_tensor* t = nullptr;
+    if (int rc = make_tensor(c, name, type, ne0, ne1, nbytes, &t)) return rc;
+    if (hipMalloc(&t->d, std::max<uint64_t>(nbytes, 16)) != hipSuccess) {
+        (void)hipGetLastError();
+        delete t;
+        return fail(MVH_E_NOMEM, "device allocation of %llu bytes failed: %s", static_cast<unsigned long long>(nbytes),
+                    name ? name : "");
+    }
+    t->owned = true;
+    if (nbytes && hipMemcpy(t->d, host_bytes, nbytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(t->d);
+        delete t;
+        return fail(MVH_E_DEVICE, "tensor upload failed: %s", name ? name : "");
+    }
+    *out = t;
+    return MVH_OK;
+}
+
+int mvh_tensor_wrap(mvh_context* c, const char* name, uint32_t type, uint64_t ne0, uint64_t ne1,
+                    const void* device_bytes, uint64_t nbytes, mvh_tensor** out) {
+    CHECK_CTX(c);
+    if (!device_bytes) return fail(MVH_E_INVALID, "null device bytes");
+    if (reinterpret_cast<uintptr_t>(device_bytes) & 15) return fail(MVH_E_INVALID, "device bytes must be 16-byte aligned");
+    mvh_tensor* t = nullptr;
+    if (int rc = make_tensor(c, name, type, ne0, ne1, nbytes, &t)) return rc;
+    t->d = const_cast<void*>(device_bytes);
+    t->owned = false;
+    *out = t;
+    return MVH_OK;
+}
+
+int mvh_tensor_free(mvh_tensor* t) {
+    if (!t) return MVH_OK;
+    if (t->owned && t->d) {
+        (void)hipSetDevice(t->ctx->device);
+        (void)hipStreamSynchronize(t->ctx->stream);
+        (void)hipFree(t->d);
+    }
+    delete t;
+    return MVH_OK;
+}
+
+int mvh_tensor_info(const mvh_tensor* t, uint32_t* type, uint64_t* ne0, uint64_t* ne1, uint64_t* nbytes,
+                    const void** device_bytes) {
+    if (!t) return fail(MVH_E_INVALID, "null tensor");
+    if (type) *type = t->type;
+    if (ne0) *ne0 = t->ne0;
+    if (ne1) *ne1 = t->ne1;
+    if (nbytes) *nbytes = t->nbytes;
+    if (device_bytes) *device_bytes = t->d;
+    return MVH_OK;
+}
+
+int mvh_quantize_q8(mvh_context* c, const float* x, size_t batch, size_t cols, int8_t* q, float* d, int kind) {
+    CHECK_CTX(c);
+    if (cols % 32) return fail(MVH_E_SHAPE, "Q8 activation quantization requires cols multiple of 32");
+    if (!batch || !cols) return MVH_OK;
+    if (!x || !q || !d) return fail(MVH_E_INVALID, "null argument");
+    const void* xd = nullptr;
+    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
+    ActView a;
+    if (int rc = act_buffers(c, batch, cols, &a)) return rc;
+    int8_t* qd = kind == MVH_DEVICE ? q : a.q;
+    float* dd = kind == MVH_DEVICE ? d : a.d;
+    MVH_HIP(mvh::launch_quantize_q8(static_cast<const float*>(xd), qd, dd, a.s, batch, cols, c->stream));
+    if (kind == MVH_HOST) {
+        MVH_HIP(hipMemcpyAsync(q, a.q, batch * cols, hipMemcpyDeviceToHost, c->stream));
+        MVH_HIP(hipMemcpyAsync(d, a.d, batch * (cols / 32) * 4, hipMemcpyDeviceToHost, c->stream));
+        MVH_HIP(hipStreamSynchronize(c->stream));
+    }
+    return MVH_OK;
+}
+
+int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, int kind) {
+    CHECK_CTX(c);
+    if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
+    const size_t cols = w->ne0, rows = w->ne1;
+    if (!rows) return MVH_OK;
+    const void* xd = nullptr;
+    if (int rc = stage_in(c, c->xin, x, cols * 4, kind, &xd)) return rc;
+    float* yd = y;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, rows * 4)) return rc;
+        yd = static_cast<float*>(c->yout.p);
+    }
+    const auto* W = static_cast<const uint8_t*>(w->d);
+    switch (w->type) {
+        case MVH_TYPE_Q4_0: {
+            if (cols % 32) return fail(MVH_E_SHAPE, "Q4_0 matrix row not block aligned: %s", w->name.c_str());
+            ActView a;
+            if (int rc = act_buffers(c, 1, cols, &a)) return rc;
+            MVH_HIP(mvh::launch_quantize_q8(static_cast<const float*>(xd), a.q, a.d, a.s, 1, cols, c->stream));
+            MVH_HIP(mvh::launch_gemv_q4_0(W, a.q, a.d, a.s, yd, rows, cols, c->stream));
+            break;
+        }
+        case MVH_TYPE_Q8_0:
+        case MVH_TYPE_Q6_K:
+            if (int rc = fp32_rows(c, w, static_cast<const float*>(xd), yd, 1, "matrix")) return rc;
+            break;
+        default:
+            return fail(MVH_E_TYPE, "unsupported matvec tensor type %s: %s", type_name(w->type), w->name.c_str());
+    }
+    return finish_out(c, y, yd, rows * 4, kind);
+}
+
+int mvh_matmul_batch(mvh_context* c, const mvh_tensor* w, const float* x, float* y, size_t batch, int kind) {
+    CHECK_CTX(c);
+    if (!w) return fail(MVH_E_INVALID, "null tensor");
+    const size_t cols = w->ne0, rows = w->ne1;
+    if (!batch || !rows) return MVH_OK;
+    if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
+    const void* xd = nullptr;
+    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
+    float* yd = y;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
+        yd = static_cast<float*>(c->yout.p);
+    }
+    if (int rc = fp32_rows(c, w, static_cast<const float*>(xd), yd, batch, "batch matrix")) return rc;
+    return finish_out(c, y, yd, batch * rows * 4, kind);
+}
+
+int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, float* y, size_t batch, int act_mode,
+                         int kind) {
+    CHECK_CTX(c);
+    if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (act_mode != MVH_ACT_REF && act_mode != MVH_ACT_Q8) return fail(MVH_E_INVALID, "bad act_mode %d", act_mode);
+    const size_t cols = w->ne0, rows = w->ne1;
+    // fallback conditions of src/gguf_kernels.cpp:263
+    if (batch < 2 || (w->type != MVH_TYPE_Q4_0 && w->type != MVH_TYPE_Q8_0) || cols % 32)
+        return mvh_matmul_batch(c, w, x, y, batch, kind);
+    if (!rows) return MVH_OK;
+    if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
+    const void* xv = nullptr;
+    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xv)) return rc;
+    const auto* xd = static_cast<const float*>(xv);
+    float* yd = y;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
+        yd = static_cast<float*>(c->yout.p);
+    }
+    const auto* W = static_cast<const uint8_t*>(w->d);
+    const size_t nb = cols / 32;
+    if (act_mode == MVH_ACT_Q8) {
+        if (w->type == MVH_TYPE_Q4_0) {
+            ActView a;
+            if (int rc = act_buffers(c, batch, cols, &a)) return rc;
+            MVH_HIP(mvh::launch_quantize_q8(xd, a.q, a.d, a.s, batch, cols, c->stream));
+            for (size_t b = 0; b < batch; ++b)
+                MVH_HIP(mvh::launch_gemv_q4_0(W, a.q + b * cols, a.d + b * nb, a.s + b * nb, yd + b * rows, rows, cols,
+                                              c->stream));
+        } else {
+            MVH_HIP(mvh::launch_gemv_q8_0(W, xd, yd, rows, cols, batch, c->stream));
+        }
+    } else {
+        // FFN tensors block 8 tokens (two batch4 calls), others 4; the tail
+        // tokens use the per-token fp32 dot (src/gguf_kernels.cpp:268)
+        const size_t step = is_ffn(w->name) ? 8 : 4;
+        const size_t blocked = batch / step * step;
+        MVH_HIP(mvh::launch_batch4_f32act(w->type, W, xd, yd, rows, cols, blocked, c->stream));
+        if (blocked < batch) {
+            if (int rc = fp32_rows(c, w, xd + blocked * cols, yd + blocked * rows, batch - blocked, "batch matrix"))
+                return rc;
+        }
+    }
+    return finish_out(c, y, yd, batch * rows * 4, kind);
+}
+
+int mvh_read_row_f32(mvh_context* c, const mvh_tensor* w, size_t row, float* out, int kind) {
+    CHECK_CTX(c);
+    if (!w || !out) return fail(MVH_E_INVALID, "null argument");
+    if (row >= w->ne1) return fail(MVH_E_RANGE, "tensor row shape mismatch: %s", w->name.c_str());
+    if (w->type == MVH_TYPE_Q6_K && w->ne0 % 256)
+        return fail(MVH_E_SHAPE, "Q6_K embedding row not block aligned: %s", w->name.c_str());
+    float* od = out;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, w->ne0 * 4)) return rc;
+        od = static_cast<float*>(c->yout.p);
+    }
+    MVH_HIP(mvh::launch_read_row(w->type, static_cast<const uint8_t*>(w->d), w->ne0, row, od, c->stream));
+    return finish_out(c, out, od, w->ne0 * 4, kind);
+}
+
+int mvh_fp32_to_fp16(mvh_context* c, const float* x, uint16_t* out, size_t n, int kind) {
+    CHECK_CTX(c);
+    if (!n) return MVH_OK;
+    if (!x || !out) return fail(MVH_E_INVALID, "null argument");
+    const void* xd = nullptr;
+    if (int rc = stage_in(c, c->xin, x, n * 4, kind, &xd)) return rc;
+    uint16_t* od = out;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, n * 2)) return rc;
+        od = static_cast<uint16_t*>(c->yout.p);
+    }
+    MVH_HIP(mvh::launch_f2h(static_cast<const float*>(xd), od, n, c->stream));
+    return finish_out(c, out, od, n * 2, kind);
+}
+
+int mvh_fp16_to_fp32(mvh_context* c, const uint16_t* h, float* out, size_t n, int kind) {
+    CHECK_CTX(c);
+    if (!n) return MVH_OK;
+    if (!h || !out) return fail(MVH_E_INVALID, "null argument");
+    const void* hd = nullptr;
+    if (int rc = stage_in(c, c->xin, h, n * 2, kind, &hd)) return rc;
+    float* od = out;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, n * 4)) return rc;
+        od = static_cast<float*>(c->yout.p);
+    }
+    MVH_HIP(mvh::launch_h2f(static_cast<const uint16_t*>(hd), od, n, c->stream));
+    return finish_out(c, out, od, n * 4, kind);
+}
+
+int mvh_kv_create(mvh_context* c, size_t n_layer, size_t kv_dim, size_t page_tokens, size_t max_tokens,
+                  mvh_kv_cache** out) {
+    CHECK_CTX(c);
+    if (!out) return fail(MVH_E_INVALID, "null out");
+    *out = nullptr;
+    if (!page_tokens) page_tokens = 128;  // PagedKVCache default (src/llama_model.cpp:19)
+    if (!n_layer || !kv_dim || !max_tokens) return fail(MVH_E_INVALID, "KV cache needs layers, kv_dim and max_tokens");
+    if (kv_dim % 8) return fail(MVH_E_SHAPE, "kv_dim must be a multiple of 8");
+    if (max_tokens > 16000) return fail(MVH_E_RANGE, "max_tokens above 16000 is not supported");
+    auto* kv = new (std::nothrow) mvh_kv_cache;
+    if (!kv) return fail(MVH_E_NOMEM, "host allocation failed");
+    kv->ctx = c;
+    kv->n_layer = n_layer;
+    kv->kv_dim = kv_dim;
+    kv->page_tokens = page_tokens;
+    kv->max_tokens = max_tokens;
+    kv->max_pages = (max_tokens + page_tokens - 1) / page_tokens;
+    const size_t n = n_layer * kv->max_pages;
+    kv->hk.assign(n, nullptr);
+    kv->hv.assign(n, nullptr);
+    if (hipMalloc(&kv->dk, n * sizeof(uint16_t*)) != hipSuccess || hipMalloc(&kv->dv, n * sizeof(uint16_t*)) != hipSuccess) {
+        (void)hipGetLastError();
+        if (kv->dk) (void)hipFree(kv->dk);
+        delete kv;
+        return fail(MVH_E_NOMEM, "KV page table allocation failed");
+    }
+    MVH_HIP(hipMemcpy(kv->dk, kv->hk.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dv, kv->hv.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
+    *out = kv;
+    return MVH_OK;
+}
+
+int mvh_kv_reset(mvh_kv_cache* kv) {
+    if (!kv) return fail(MVH_E_INVALID, "null KV cache");
+    MVH_HIP(hipSetDevice(kv->ctx->device));
+    MVH_HIP(hipStreamSynchronize(kv->ctx->stream));
+    for (size_t i = 0; i < kv->hk.size(); ++i)
+        if (kv->hk[i]) {
+            kv->pool.push_back(kv->hk[i]);
+            kv->hk[i] = kv->hv[i] = nullptr;
+        }
+    kv->live_pages = 0;
+    const size_t n = kv->hk.size();
+    MVH_HIP(hipMemcpy(kv->dk, kv->hk.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dv, kv->hv.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
+    return MVH_OK;
+}
+
+int mvh_kv_destroy(mvh_kv_cache* kv) {
+    if (!kv) return MVH_OK;
+    (void)hipSetDevice(kv->ctx->device);
+    (void)hipStreamSynchronize(kv->ctx->stream);
+    for (auto* p : kv->hk)
+        if (p) (void)hipFree(p);
+    for (auto* p : kv->pool) (void)hipFree(p);
+    (void)hipFree(kv->dk);
+    (void)hipFree(kv->dv);
+    delete kv;
+    return MVH_OK;
+}
+
+int mvh_kv_bytes_allocated(const mvh_kv_cache* kv, size_t* bytes) {
+    if (!kv || !bytes) return fail(MVH_E_INVALID, "null argument");
+    *bytes = kv->live_pages * 2 * kv->page_elems() * sizeof(uint16_t);
+    return MVH_OK;
+}
+
+int mvh_kv_write(mvh_context* c, mvh_kv_cache* kv, size_t layer, size_t pos, size_t n_tokens, const float* k,
+                 const float* v, int kind) {
+    CHECK_CTX(c);
+    if (int rc = check_kv(kv, layer)) return rc;
+    if (!n_tokens) return MVH_OK;
+    if (!k || !v) return fail(MVH_E_INVALID, "null k/v");
+    if (pos + n_tokens > kv->max_tokens) return fail(MVH_E_RANGE, "context exhausted");
+    for (size_t p = pos / kv->page_tokens; p <= (pos + n_tokens - 1) / kv->page_tokens; ++p)
+        if (int rc = ensure_page(kv, layer, p)) return rc;
+    const size_t bytes = n_tokens * kv->kv_dim * 4;
+    const void* kd = nullptr;
+    const void* vd = nullptr;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->xin, 2 * bytes)) return rc;
+        MVH_HIP(hipMemcpyAsync(c->xin.p, k, bytes, hipMemcpyHostToDevice, c->stream));
+        MVH_HIP(hipMemcpyAsync(static_cast<uint8_t*>(c->xin.p) + bytes, v, bytes, hipMemcpyHostToDevice, c->stream));
+        kd = c->xin.p;
+        vd = static_cast<uint8_t*>(c->xin.p) + bytes;
+    } else {
+        kd = k;
+        vd = v;
+    }
+    const size_t base = layer * kv->max_pages;
+    MVH_HIP(mvh::launch_kv_write(kv->dk + base, kv->dv + base, static_cast<const float*>(kd),
+                                 static_cast<const float*>(vd), pos, n_tokens, kv->kv_dim, kv->page_tokens, c->stream));
+    if (kind == MVH_HOST) MVH_HIP(hipStreamSynchronize(c->stream));
+    return MVH_OK;
+}
+
+int mvh_kv_read_row(mvh_context* c, const mvh_kv_cache* kv, size_t layer, size_t pos, int which, uint16_t* out) {
+    CHECK_CTX(c);
+    if (int rc = check_kv(kv, layer)) return rc;
+    if (!out) return fail(MVH_E_INVALID, "null out");
+    if (pos >= kv->max_tokens) return fail(MVH_E_RANGE, "KV position out of range");
+    const size_t slot = layer * kv->max_pages + pos / kv->page_tokens;
+    const uint16_t* page = which ? kv->hv[slot] : kv->hk[slot];
+    if (!page) return fail(MVH_E_RANGE, which ? "KV value page missing" : "KV key page missing");
+    MVH_HIP(hipStreamSynchronize(c->stream));
+    MVH_HIP(hipMemcpy(out, page + (pos % kv->page_tokens) * kv->kv_dim, kv->kv_dim * 2, hipMemcpyDeviceToHost));
+    return MVH_OK;
+}
+
+int mvh_attn_decode(mvh_context* c, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos, size_t n_head,
+                    size_t n_head_kv, size_t head_dim, float* out, int kind) {
+    CHECK_CTX(c);
+    if (int rc = check_kv(kv, layer)) return rc;
+    if (!q || !out) return fail(MVH_E_INVALID, "null q/out");
+    if (!n_head || !n_head_kv || n_head % n_head_kv || !head_dim)
+        return fail(MVH_E_SHAPE, "invalid Llama head configuration");
+    if (head_dim % 8 || n_head_kv * head_dim > kv->kv_dim)
+        return fail(MVH_E_SHAPE, "head_dim must be a multiple of 8 and n_head_kv*head_dim <= kv_dim");
+    if (pos >= kv->max_tokens) return fail(MVH_E_RANGE, "context exhausted");
+    for (size_t p = 0; p <= pos / kv->page_tokens; ++p)
+        if (!kv->hk[layer * kv->max_pages + p]) return fail(MVH_E_RANGE, "KV key page missing");
+    const size_t qn = n_head * head_dim;
+    const void* qd = nullptr;
+    if (int rc = stage_in(c, c->xin, q, qn * 4, kind, &qd)) return rc;
+    float* od = out;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, qn * 4)) return rc;
+        od = static_cast<float*>(c->yout.p);
+    }
+    if (int rc = grow(c, c->scratch, n_head * (pos + 1) * 4)) return rc;
+    const size_t base = layer * kv->max_pages;
+    MVH_HIP(mvh::launch_attn_decode(kv->dk + base, kv->dv + base, static_cast<const float*>(qd),
+                                    static_cast<float*>(c->scratch.p), od, pos, n_head, n_head_kv, head_dim,
+                                    kv->kv_dim, kv->page_tokens, c->stream));
+    return finish_out(c, out, od, qn * 4, kind);
+}
+
+}  // extern "C"

@@ -1,0 +1,105 @@
+// mvh_device.hpp -- device helpers shared by the gfx950 kernels.
+//
+// All HIP sources are compiled with -ffp-contract=off: every fused
+// multiply-add is written as fmaf()/fma(), every other product rounds on its
+// own, so each kernel reproduces the reference's operation order exactly.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace mvh {
+
+constexpr int kWave = 64;
+
+// ---- fp16 ------------------------------------------------------------------
+
+// Exact binary16 -> binary32 (v_cvt_f32_f16; f16 denormals are kept, as in
+// fp16_to_fp32, src/gguf.cpp:110-119).
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+// The reference's binary32 -> binary16 routine (src/gguf_kernels.cpp:242):
+// ties away from zero, and a mantissa carry is OR-ed (not added) into the
+// exponent field.  The F16 KV cache must hold exactly these bits, so this is
+// integer code, not v_cvt_f16_f32.
+__device__ __forceinline__ uint16_t f2h_ref(float f) {
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u, mant = x & 0x7fffffu;
+    int e = static_cast<int>((x >> 23) & 0xffu) - 112;  // -127 + 15
+    if (e <= 0) {
+        if (e < -10) return static_cast<uint16_t>(sign);
+        mant = (mant | 0x800000u) >> (1 - e);
+        return static_cast<uint16_t>(sign + ((mant + 0x1000u) >> 13));
+    }
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | ((mant + 0x1000u) >> 13));
+}
+
+// ---- cross-lane --------------------------------------------------------------
+
+// ds_swizzle in bit-mask mode (offset[15]=0): lane' = ((lane & and) | or) ^ xor
+// inside each group of 32 lanes.  No LDS memory is touched.
+template <int XOR>
+__device__ __forceinline__ int swz_xor(int v) {
+    return __builtin_amdgcn_ds_swizzle(v, (XOR << 10) | 0x1f);
+}
+template <int XOR>
+__device__ __forceinline__ float swz_xor(float v) {
+    return __int_as_float(swz_xor<XOR>(__float_as_int(v)));
+}
+template <int XOR>
+__device__ __forceinline__ double swz_xor(double v) {
+    int lo = __double2loint(v), hi = __double2hiint(v);
+    return __hiloint2double(swz_xor<XOR>(hi), swz_xor<XOR>(lo));
+}
+
+// Reductions over aligned groups of N lanes (N = 2..32), result in every lane.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (N >= 32) v = fmaxf(v, swz_xor<16>(v));
+    if constexpr (N >= 16) v = fmaxf(v, swz_xor<8>(v));
+    if constexpr (N >= 8) v = fmaxf(v, swz_xor<4>(v));
+    if constexpr (N >= 4) v = fmaxf(v, swz_xor<2>(v));
+    if constexpr (N >= 2) v = fmaxf(v, swz_xor<1>(v));
+    return v;
+}
+template <int N>
+__device__ __forceinline__ int group_sum(int v) {
+    if constexpr (N >= 32) v += swz_xor<16>(v);
+    if constexpr (N >= 16) v += swz_xor<8>(v);
+    if constexpr (N >= 8) v += swz_xor<4>(v);
+    if constexpr (N >= 4) v += swz_xor<2>(v);
+    if constexpr (N >= 2) v += swz_xor<1>(v);
+    return v;
+}
+// Double sum over the full wave (xor butterfly inside 32-lane halves, then the
+// two halves through a DPP row broadcast-free readlane pair).
+__device__ __forceinline__ double wave_sum(double v) {
+    v += swz_xor<16>(v);
+    v += swz_xor<8>(v);
+    v += swz_xor<4>(v);
+    v += swz_xor<2>(v);
+    v += swz_xor<1>(v);
+    int lo = __double2loint(v), hi = __double2hiint(v);
+    double other = __hiloint2double(__builtin_amdgcn_readlane(hi, 32), __builtin_amdgcn_readlane(lo, 32));
+    double mine = __hiloint2double(__builtin_amdgcn_readlane(hi, 0), __builtin_amdgcn_readlane(lo, 0));
+    return mine + other;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (weights are read once per call: nontemporal hint).
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Bytes [2*sel, 2*sel+4) of the 8-byte value hi:lo (v_alignbyte_b32).
+__device__ __forceinline__ uint32_t align16(uint32_t hi, uint32_t lo) {
+    return __builtin_amdgcn_alignbyte(hi, lo, 2);
+}
+
+}  // namespace mvh

@@ -1,0 +1,433 @@
+// mvh_gemv.hip -- decode GEMVs over weights in native GGUF block layout.
+//
+// Q4_0 x Q8 (tensor_matvec Q4_0 branch, src/gguf_kernels.cpp:246 + dot_q4_q8
+// :189): per row the reference runs sum = fma(d_w*d_a, float(isum_b), sum)
+// over blocks b in order.  The kernels split that into two phases:
+//   1. every lane turns whole 18-byte blocks into (p_b = d_w*d_a, f_b =
+//      float(isum_b)) pairs -- integer dots with v_dot4_i32_i8, exact;
+//   2. one lane per row folds the pairs in block order with v_fma_f32.
+// Phase 2 is the reference's own chain, so y is bit-identical.
+//
+// Weight units are groups of 8 blocks (144 bytes = 9 x 16 B, so every unit
+// starts 16-byte aligned when K % 256 == 0); other K take a 1-block path.
+#include "mvh_kernels.hpp"
+
+namespace mvh {
+namespace {
+
+constexpr int kActPitch = 272;     // LDS bytes per 8-block activation group (256 + 16 pad)
+constexpr int kXPitchF = 260;      // LDS floats per 8-block fp32 activation group (256 + 4 pad)
+constexpr int kGemvThreads = 128;
+
+__device__ __forceinline__ int dot_nibbles(const uint32_t (&qs)[4], const uint4 a0, const uint4 a1) {
+    // qs byte i holds element i (low nibble) and element 16+i (high nibble).
+    constexpr uint32_t M = 0x0f0f0f0fu;
+    int s = 0;
+    s = __builtin_amdgcn_sdot4(static_cast<int>(qs[0] & M), static_cast<int>(a0.x), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(qs[1] & M), static_cast<int>(a0.y), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(qs[2] & M), static_cast<int>(a0.z), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(qs[3] & M), static_cast<int>(a0.w), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((qs[0] >> 4) & M), static_cast<int>(a1.x), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((qs[1] >> 4) & M), static_cast<int>(a1.y), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((qs[2] >> 4) & M), static_cast<int>(a1.z), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((qs[3] >> 4) & M), static_cast<int>(a1.w), s, false);
+    return s;
+}
+
+// Fold the per-block pairs of `rows` rows in block order (phase 2).
+__device__ __forceinline__ void fold_pairs(const float2* s_pair, int pitch, int rows, int nb, float* y) {
+    for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+        const float2* pr = s_pair + r * pitch;
+        float sum = 0.0f;
+        int b = 0;
+        for (; b + 8 <= nb; b += 8) {
+            float2 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = pr[b + j];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sum = fmaf(v[j].x, v[j].y, sum);
+        }
+        for (; b < nb; ++b) sum = fmaf(pr[b].x, pr[b].y, sum);
+        y[r] = sum;
+    }
+}
+
+template <int G>
+__global__ __launch_bounds__(kGemvThreads) void gemv_q4_0_kernel(const uint8_t* __restrict__ W,
+                                                                  const int8_t* __restrict__ aq,
+                                                                  const float* __restrict__ ad,
+                                                                  const int* __restrict__ as, float* __restrict__ y,
+                                                                  int N, int nb, int rows_per_wg) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int ngrp = (nb + 7) >> 3;
+    uint8_t* s_aq = smem;
+    float* s_ad = reinterpret_cast<float*>(smem + ngrp * kActPitch);
+    int* s_as = reinterpret_cast<int*>(s_ad + nb);
+    float2* s_pair = reinterpret_cast<float2*>(s_as + nb);
+    const int pitch = nb + 1;
+
+    // stage the Q8 activation (all rows of this tile share it)
+    const int K = nb * 32;
+    for (int c = threadIdx.x; c < K / 16; c += blockDim.x)
+        *reinterpret_cast<uint4*>(s_aq + (c >> 4) * kActPitch + (c & 15) * 16) = reinterpret_cast<const uint4*>(aq)[c];
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+        s_ad[b] = ad[b];
+        s_as[b] = as[b];
+    }
+    __syncthreads();
+
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int rows = min(rows_per_wg, N - r0);
+    const int upr = nb / G;
+    const int nunits = rows * upr;
+    const uint8_t* tile = W + static_cast<size_t>(r0) * nb * 18;
+
+    for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
+        const int row = u / upr;
+        const int b0 = (u - row * upr) * G;
+        float2* pout = s_pair + row * pitch + b0;
+        if constexpr (G == 8) {
+            uint32_t w[36];
+            const uint4* src = reinterpret_cast<const uint4*>(tile + static_cast<size_t>(u) * 144);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                const uint4 v = ld_stream16(src + k);
+                w[4 * k] = v.x;
+                w[4 * k + 1] = v.y;
+                w[4 * k + 2] = v.z;
+                w[4 * k + 3] = v.w;
+            }
+            const uint8_t* agrp = s_aq + (b0 >> 3) * kActPitch;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int o = 18 * j;  // byte offset of block j inside the unit
+                uint32_t dbits, qs[4];
+                if ((j & 1) == 0) {
+                    dbits = w[o / 4] & 0xffffu;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) qs[k] = align16(w[o / 4 + k + 1], w[o / 4 + k]);
+                } else {
+                    dbits = w[o / 4] >> 16;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) qs[k] = w[(o + 2) / 4 + k];
+                }
+                const uint4* a = reinterpret_cast<const uint4*>(agrp + j * 32);
+                const int b = b0 + j;
+                const int isum = dot_nibbles(qs, a[0], a[1]) - 8 * s_as[b];
+                pout[j] = make_float2(h2f(dbits) * s_ad[b], static_cast<float>(isum));
+            }
+        } else {
+            const uint16_t* src = reinterpret_cast<const uint16_t*>(tile + static_cast<size_t>(u) * 18);
+            uint32_t h[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) h[k] = src[k];
+            const uint32_t qs[4] = {h[1] | (h[2] << 16), h[3] | (h[4] << 16), h[5] | (h[6] << 16), h[7] | (h[8] << 16)};
+            const uint4* a = reinterpret_cast<const uint4*>(s_aq + (b0 >> 3) * kActPitch + (b0 & 7) * 32);
+            const int isum = dot_nibbles(qs, a[0], a[1]) - 8 * s_as[b0];
+            pout[0] = make_float2(h2f(h[0]) * s_ad[b0], static_cast<float>(isum));
+        }
+    }
+    __syncthreads();
+    fold_pairs(s_pair, pitch, rows, nb, y + r0);
+}
+
+// fp32-activation block dots (dot_q4_0_fp32 :93-109, dot_q8_0_fp32 :111-120,
+// src/gguf_kernels.cpp): per block, lane j of 8 accumulates elements j, 8+j,
+// 16+j, 24+j by fma from zero, s = 0+t0+..+t7; then sum = fma(d, s, sum) over
+// blocks.  Phase 1 produces (d_b, s_b) per block, phase 2 folds them per row.
+// blockIdx.y = token (tensor_matmul_batch's y[b*rows + r]).
+template <uint32_t TYPE>
+struct Blk;
+template <>
+struct Blk<kQ4_0> {
+    static constexpr int kBytes = 18, kQdw = 4;
+    // element e: low nibble of byte e (e < 16) or high nibble of byte e-16, minus 8
+    static __device__ __forceinline__ int value(const uint32_t (&qs)[kQdw], int e) {
+        const int byte = e & 15;
+        const uint32_t b = (qs[byte >> 2] >> (8 * (byte & 3))) & 0xffu;
+        return static_cast<int>(e < 16 ? (b & 15u) : (b >> 4)) - 8;
+    }
+};
+template <>
+struct Blk<kQ8_0> {
+    static constexpr int kBytes = 34, kQdw = 8;
+    static __device__ __forceinline__ int value(const uint32_t (&qs)[kQdw], int e) {
+        return static_cast<int>(static_cast<int8_t>(qs[e >> 2] >> (8 * (e & 3))));
+    }
+};
+
+template <uint32_t TYPE>
+__device__ __forceinline__ float f32act_block_sum(const uint32_t (&qs)[Blk<TYPE>::kQdw], const float* xb) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k += 8) {
+        const float4 x0 = *reinterpret_cast<const float4*>(xb + k);
+        const float4 x1 = *reinterpret_cast<const float4*>(xb + k + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = fmaf(static_cast<float>(Blk<TYPE>::value(qs, k + j)), xv[j], t[j]);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = s + t[j];
+    return s;
+}
+
+// Block j of an 8-block unit held in registers w[]: scale bits and quant dwords.
+template <uint32_t TYPE>
+__device__ __forceinline__ void unit_block(const uint32_t* w, int j, uint32_t& dbits,
+                                           uint32_t (&qs)[Blk<TYPE>::kQdw]) {
+    const int o = Blk<TYPE>::kBytes * j;
+    if ((o & 3) == 0) {
+        dbits = w[o / 4] & 0xffffu;
+#pragma unroll
+        for (int k = 0; k < Blk<TYPE>::kQdw; ++k) qs[k] = align16(w[o / 4 + k + 1], w[o / 4 + k]);
+    } else {
+        dbits = w[o / 4] >> 16;
+#pragma unroll
+        for (int k = 0; k < Blk<TYPE>::kQdw; ++k) qs[k] = w[(o + 2) / 4 + k];
+    }
+}
+
+template <uint32_t TYPE, int G>
+__global__ __launch_bounds__(kGemvThreads) void gemv_f32act_kernel(const uint8_t* __restrict__ W,
+                                                                    const float* __restrict__ x,
+                                                                    float* __restrict__ y, int N, int nb,
+                                                                    int rows_per_wg) {
+    constexpr int BB = Blk<TYPE>::kBytes;
+    constexpr int UNIT16 = 8 * BB / 16;  // 16-byte loads per 8-block unit
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int ngrp = (nb + 7) >> 3;
+    float* s_x = reinterpret_cast<float*>(smem);
+    float2* s_pair = reinterpret_cast<float2*>(smem + static_cast<size_t>(ngrp) * kXPitchF * 4);
+    const int pitch = nb + 1;
+    const int K = nb * 32;
+    const float* xt = x + static_cast<size_t>(blockIdx.y) * K;
+    for (int c = threadIdx.x; c < K / 4; c += blockDim.x)
+        *reinterpret_cast<float4*>(s_x + (c >> 6) * kXPitchF + (c & 63) * 4) = reinterpret_cast<const float4*>(xt)[c];
+    __syncthreads();
+
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int rows = min(rows_per_wg, N - r0);
+    const int upr = nb / G;
+    const int nunits = rows * upr;
+    const uint8_t* tile = W + static_cast<size_t>(r0) * nb * BB;
+    for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
+        const int row = u / upr;
+        const int b0 = (u - row * upr) * G;
+        float2* pout = s_pair + row * pitch + b0;
+        if constexpr (G == 8) {
+            uint32_t w[4 * UNIT16];
+            const uint4* src = reinterpret_cast<const uint4*>(tile + static_cast<size_t>(u) * 8 * BB);
+#pragma unroll
+            for (int k = 0; k < UNIT16; ++k) {
+                const uint4 v = ld_stream16(src + k);
+                w[4 * k] = v.x;
+                w[4 * k + 1] = v.y;
+                w[4 * k + 2] = v.z;
+                w[4 * k + 3] = v.w;
+            }
+            const float* xg = s_x + (b0 >> 3) * kXPitchF;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                uint32_t dbits, qs[Blk<TYPE>::kQdw];
+                unit_block<TYPE>(w, j, dbits, qs);
+                pout[j] = make_float2(h2f(dbits), f32act_block_sum<TYPE>(qs, xg + j * 32));
+            }
+        } else {
+            const uint16_t* src = reinterpret_cast<const uint16_t*>(tile + static_cast<size_t>(u) * BB);
+            uint32_t qs[Blk<TYPE>::kQdw];
+#pragma unroll
+            for (int k = 0; k < Blk<TYPE>::kQdw; ++k)
+                qs[k] = src[1 + 2 * k] | (static_cast<uint32_t>(src[2 + 2 * k]) << 16);
+            pout[0] = make_float2(h2f(src[0]),
+                                  f32act_block_sum<TYPE>(qs, s_x + (b0 >> 3) * kXPitchF + (b0 & 7) * 32));
+        }
+    }
+    __syncthreads();
+    fold_pairs(s_pair, pitch, rows, nb, y + static_cast<size_t>(blockIdx.y) * N + r0);
+}
+
+// Default batched prefill numerics (q4_row_batch4_fp32 / q8_row_batch4_fp32,
+// src/gguf_kernels.cpp:191-209; batch8 = two batch4, :211-216): per
+// (row, token) eight lane accumulators run over ALL blocks without reset,
+// term = fma(float(q)*d, x, acc) with the product float(q)*d rounded first;
+// result = t0+t1+..+t7.  One thread per (row, token); blockIdx.y = token.
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void batch4_f32act_kernel(const uint8_t* __restrict__ W,
+                                                             const float* __restrict__ x, float* __restrict__ y,
+                                                             int N, int nb) {
+    constexpr int BB = Blk<TYPE>::kBytes;
+    extern __shared__ __align__(16) float s_xt[];
+    const int K = nb * 32;
+    const float* xt = x + static_cast<size_t>(blockIdx.y) * K;
+    for (int c = threadIdx.x; c < K / 4; c += blockDim.x)
+        reinterpret_cast<float4*>(s_xt)[c] = reinterpret_cast<const float4*>(xt)[c];
+    __syncthreads();
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= N) return;
+    const uint8_t* rowp = W + static_cast<size_t>(r) * nb * BB;
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(rowp + static_cast<size_t>(b) * BB);
+        uint32_t qs[Blk<TYPE>::kQdw];
+#pragma unroll
+        for (int k = 0; k < Blk<TYPE>::kQdw; ++k)
+            qs[k] = src[1 + 2 * k] | (static_cast<uint32_t>(src[2 + 2 * k]) << 16);
+        const float d = h2f(src[0]);
+        const float* xb = s_xt + b * 32;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float q = static_cast<float>(Blk<TYPE>::value(qs, e)) * d;
+            t[e & 7] = fmaf(q, xb[e], t[e & 7]);
+        }
+    }
+    float s = t[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) s = s + t[j];
+    y[static_cast<size_t>(blockIdx.y) * N + r] = s;
+}
+
+// Q6_K with fp32 activations (dot_q6_k_fp32, src/gguf_kernels.cpp:138-146):
+// w = (d*sc[i/16])*q in f32, exact products summed in double.  One wave per
+// row; each lane owns 64 elements of one half super-block and keeps its own
+// double partial, the wave adds the partials as a tree and rounds to f32 once.
+// The double sum order differs from the reference's element order, so a row
+// can differ from it only when the exact sum lies within ~1e-13 (relative) of
+// an f32 rounding boundary.
+constexpr int kQ6Threads = 256;
+constexpr int kQ6RowsPerWg = 8;
+
+__global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __restrict__ W,
+                                                               const float* __restrict__ x, float* __restrict__ y,
+                                                               int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* s_x = reinterpret_cast<float*>(smem);
+    const float* xt = x + static_cast<size_t>(blockIdx.y) * K;
+    for (int c = threadIdx.x; c < K / 4; c += blockDim.x)
+        reinterpret_cast<float4*>(s_x)[c] = reinterpret_cast<const float4*>(xt)[c];
+    __syncthreads();
+    const int nsb = K / 256;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * kQ6RowsPerWg;
+    for (int rr = wave; rr < kQ6RowsPerWg; rr += kQ6Threads / 64) {
+        const int row = r0 + rr;
+        if (row >= N) break;
+        const uint8_t* rb = W + static_cast<size_t>(row) * nsb * 210;
+        double acc = 0.0;
+        for (int u = lane; u < 4 * nsb; u += 64) {
+            const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
+            const uint8_t* b = rb + static_cast<size_t>(sb) * 210;
+            const uint16_t* qla = reinterpret_cast<const uint16_t*>(b + g * 64 + h * 16);
+            const uint16_t* qlb = reinterpret_cast<const uint16_t*>(b + g * 64 + 32 + h * 16);
+            const uint16_t* qh = reinterpret_cast<const uint16_t*>(b + 128 + g * 32 + h * 16);
+            const float d = h2f(*reinterpret_cast<const uint16_t*>(b + 208));
+            const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + g * 8 + h);
+            float dsc[4];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) dsc[l] = d * static_cast<float>(sc[2 * l]);
+            const float* xb = s_x + sb * 256 + g * 128 + h * 16;
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const uint32_t a = qla[p], bb = qlb[p], hh = qh[p];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int jj = 2 * p + e;
+                    const uint32_t la = (a >> (8 * e)) & 0xffu, lb = (bb >> (8 * e)) & 0xffu, hb = (hh >> (8 * e)) & 0xffu;
+                    const int lo[4] = {static_cast<int>(la & 15), static_cast<int>(lb & 15), static_cast<int>(la >> 4),
+                                       static_cast<int>(lb >> 4)};
+#pragma unroll
+                    for (int l = 0; l < 4; ++l) {
+                        const int q = (lo[l] | static_cast<int>(((hb >> (2 * l)) & 3u) << 4)) - 32;
+                        const float wv = dsc[l] * static_cast<float>(q);
+                        acc = fma(static_cast<double>(wv), static_cast<double>(xb[l * 32 + jj]), acc);
+                    }
+                }
+            }
+        }
+        const double tot = wave_sum(acc);
+        if (lane == 0) y[static_cast<size_t>(blockIdx.y) * N + row] = static_cast<float>(tot);
+    }
+}
+
+int pick_rows_per_wg(size_t rows, size_t nb, size_t pair_budget) {
+    // enough rows per workgroup that every lane owns at least one 8-block
+    // unit, capped by the LDS budget of the pair buffer
+    int r = static_cast<int>((kGemvThreads * 8 + nb - 1) / nb);
+    if (r < 1) r = 1;
+    const int cap = static_cast<int>(pair_budget / ((nb + 1) * sizeof(float2)));
+    if (r > cap) r = cap;
+    if (r < 1) r = 1;
+    (void)rows;
+    return r;
+}
+
+}  // namespace
+
+hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, const int* as, float* y,
+                            size_t rows, size_t cols, hipStream_t st) {
+    const int nb = static_cast<int>(cols / 32);
+    const int ngrp = (nb + 7) / 8;
+    const size_t fixed = static_cast<size_t>(ngrp) * kActPitch + 8u * nb;
+    const int rpw = pick_rows_per_wg(rows, nb, 60 * 1024 - fixed);
+    const size_t lds = fixed + static_cast<size_t>(rpw) * (nb + 1) * sizeof(float2);
+    const unsigned grid = static_cast<unsigned>((rows + rpw - 1) / rpw);
+    if (nb % 8 == 0)
+        gemv_q4_0_kernel<8><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, as, y, static_cast<int>(rows), nb, rpw);
+    else
+        gemv_q4_0_kernel<1><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, as, y, static_cast<int>(rows), nb, rpw);
+    return hipGetLastError();
+}
+
+template <uint32_t TYPE>
+static hipError_t launch_f32act(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                                hipStream_t st) {
+    if (!rows || !batch) return hipSuccess;
+    const int nb = static_cast<int>(cols / 32);
+    const int ngrp = (nb + 7) / 8;
+    const size_t fixed = static_cast<size_t>(ngrp) * kXPitchF * 4;
+    const int rpw = pick_rows_per_wg(rows, nb, 60 * 1024 - fixed);
+    const size_t lds = fixed + static_cast<size_t>(rpw) * (nb + 1) * sizeof(float2);
+    const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw), static_cast<unsigned>(batch));
+    if (nb % 8 == 0)
+        gemv_f32act_kernel<TYPE, 8><<<grid, kGemvThreads, lds, st>>>(W, x, y, static_cast<int>(rows), nb, rpw);
+    else
+        gemv_f32act_kernel<TYPE, 1><<<grid, kGemvThreads, lds, st>>>(W, x, y, static_cast<int>(rows), nb, rpw);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_q8_0(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                            hipStream_t st) {
+    return launch_f32act<kQ8_0>(W, x, y, rows, cols, batch, st);
+}
+
+hipError_t launch_gemv_q4_0_f32act(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                                   hipStream_t st) {
+    return launch_f32act<kQ4_0>(W, x, y, rows, cols, batch, st);
+}
+
+hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,
+                                size_t batch, hipStream_t st) {
+    if (!rows || !batch) return hipSuccess;
+    const int nb = static_cast<int>(cols / 32);
+    const dim3 grid(static_cast<unsigned>((rows + 255) / 256), static_cast<unsigned>(batch));
+    if (type == kQ4_0)
+        batch4_f32act_kernel<kQ4_0><<<grid, 256, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows), nb);
+    else
+        batch4_f32act_kernel<kQ8_0><<<grid, 256, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows), nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                            hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>((rows + kQ6RowsPerWg - 1) / kQ6RowsPerWg), static_cast<unsigned>(batch));
+    gemv_q6_k_kernel<<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
+                                                                     static_cast<int>(cols));
+    return hipGetLastError();
+}
+
+}  // namespace mvh

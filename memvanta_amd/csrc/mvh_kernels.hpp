@@ -1,0 +1,40 @@
+// mvh_kernels.hpp -- launchers of the gfx950 kernels (host-callable).
+#pragma once
+#include "mvh_device.hpp"
+
+namespace mvh {
+
+// GGML type ids used on the device side.
+enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ6_K = 14 };
+
+// ---- activation quantization / conversions (mvh_quant.hip) ----
+hipError_t launch_quantize_q8(const float* x, int8_t* q, float* d, int* s, size_t rows, size_t cols, hipStream_t st);
+hipError_t launch_f2h(const float* x, uint16_t* out, size_t n, hipStream_t st);
+hipError_t launch_f2h_bits(uint32_t first, uint16_t* out, size_t n, hipStream_t st);
+hipError_t launch_h2f(const uint16_t* h, float* out, size_t n, hipStream_t st);
+hipError_t launch_read_row(uint32_t type, const uint8_t* W, size_t cols, size_t row, float* out, hipStream_t st);
+
+// ---- decode GEMV (mvh_gemv.hip); W is the tensor in native GGUF layout ----
+// y[N] = W[N x K] . x[K]; `rows` are N, `cols` are K.
+hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, const int* as, float* y,
+                            size_t rows, size_t cols, hipStream_t st);
+hipError_t launch_gemv_q8_0(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                            hipStream_t st);
+hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                            hipStream_t st);
+// dot_q4_0_fp32 per (row, token): y[b*rows + r]
+hipError_t launch_gemv_q4_0_f32act(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                                   hipStream_t st);
+// q4/q8_row_batch4_fp32 numerics per (row, token) for Q4_0 / Q8_0
+hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,
+                                size_t batch, hipStream_t st);
+
+// ---- paged F16 KV + decode attention (mvh_attn.hip) ----
+hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
+                           size_t n_tokens, size_t kv_dim, size_t page_tokens, hipStream_t st);
+// scores needs n_head * (pos+1) floats of scratch
+hipError_t launch_attn_decode(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
+                              float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim,
+                              size_t page_tokens, hipStream_t st);
+
+}  // namespace mvh

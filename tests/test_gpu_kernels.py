@@ -1,0 +1,237 @@
+"""GPU parity: every kernel through the C ABI against the oracle on the same
+seeded inputs.  Integer/byte results and the fp32 chains that reproduce the
+reference's operation order are compared bit for bit; the two places that
+add a double sum in a different order (Q6_K rows, the attention softmax
+denominator) are compared within 2 ulp and must be bit-identical on at least
+99.9% of the outputs."""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, bits
+from memvanta_amd import capi, synth
+
+pytestmark = pytest.mark.gpu
+
+SHAPES_7B = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]  # (K, N)
+
+
+def _w(rng, ty, rows, cols):
+    return synth.quantize(ty, rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
+
+
+def ulp_diff(a, b):
+    a = bits(a).astype(np.int64)
+    b = bits(b).astype(np.int64)
+    a = np.where(a & 0x80000000, 0x80000000 - a, a)
+    b = np.where(b & 0x80000000, 0x80000000 - b, b)
+    return np.abs(a - b)
+
+
+# ---------------------------------------------------------------- conversions
+
+def test_fp16_to_fp32_all_65536(ctx, oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = ctx.fp16_to_fp32(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(bits(got)[~nan], bits(want)[~nan])
+    assert np.isnan(got[nan]).all()
+    # the oracle's conversion agrees on a spread of patterns incl. subnormals
+    probe = np.array([0, 1, 2, 0x3ff, 0x400, 0x3c00, 0x7bff, 0x7c00, 0x8001, 0xfbff], np.uint16)
+    assert np.array_equal(bits(oracle.fp16_to_fp32(probe)), bits(ctx.fp16_to_fp32(probe)))
+
+
+def test_fp32_to_fp16_reference_rounding(ctx, oracle):
+    rng = np.random.default_rng(3)
+    # 2^26 patterns strided over all 2^32, 2^24 random ones, and every
+    # exponent with mantissas at the rounding/carry boundaries
+    strided = (np.arange(1 << 26, dtype=np.uint64) * 64).astype(np.uint32)
+    rand = rng.integers(0, 1 << 32, size=1 << 24, dtype=np.uint64).astype(np.uint32)
+    e = np.arange(512, dtype=np.uint32) << 23
+    m = np.concatenate([np.array([0, 1, 0xfff, 0x1000, 0x1001, 0x1fff, 0x2000, 0x7fefff, 0x7ff000, 0x7fffff], np.uint32),
+                        rng.integers(0, 1 << 23, size=2000, dtype=np.uint64).astype(np.uint32)])
+    edge = (e[:, None] | m[None, :]).ravel()
+    pats = np.concatenate([strided, rand, edge])
+    got = ctx.fp32_to_fp16(pats.view(np.float32))
+    want = oracle.fp32_to_fp16(pats.view(np.float32))
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} mismatches, first pattern 0x{pats[bad[0]]:08x}"
+    # known answers of the non-RNE routine (ties away, OR-ed carry)
+    kv = np.array([1.00048828125, 1.9999, 0.12499999, 65504.0, 70000.0, 1e-6, -1.9999], np.float32)
+    assert list(ctx.fp32_to_fp16(kv)) == [0x3c01, 0x3c00, 0x2c00, 0x7bff, 0x7c00, 0x0011, 0xbc00]
+
+
+# ---------------------------------------------------------------- quantizer
+
+@pytest.mark.parametrize("m,k", [(1, 4096), (1, 11008), (32, 4096), (7, 288), (512, 2048)])
+def test_quantize_q8_bitexact(ctx, oracle, m, k):
+    rng = np.random.default_rng(m * 1000 + k)
+    x = synth.activations(rng, m, k)
+    x[0, :32] = 0.0                                   # all-zero block -> d = 1, q = 0
+    x[0, 32:64] = np.float32(0.0)
+    x[0, 40] = 127.0                                  # d = 1, inv = 1
+    x[0, 41], x[0, 42], x[0, 43] = 2.5, -2.5, 126.5   # ties round away from zero
+    if k > 96:
+        x[0, 64:96] = np.float32(1e-30)               # tiny but non-zero block
+    q, d = ctx.quantize_q8(x)
+    q_ref, d_ref = oracle.quantize_q8(x)
+    assert np.array_equal(q, q_ref)
+    assert_bitexact(d, d_ref, "q8 scales")
+    assert q[0, 41] == 3 and q[0, 42] == -3 and q[0, 43] == 127 and d[0, 0] == 1.0
+
+
+# ---------------------------------------------------------------- decode GEMV
+
+@pytest.mark.parametrize("k,n", SHAPES_7B + [(288, 768), (768, 288), (2048, 2048), (5632, 2048)])
+def test_gemv_q4_0_bitexact(ctx, oracle, k, n):
+    rng = np.random.default_rng(k + n)
+    w = _w(rng, synth.Q4_0, n, k)
+    t = ctx.upload("blk.0.attn_q.weight", synth.Q4_0, k, n, w)
+    for rep in range(2):
+        x = synth.activations(rng, 1, k)[0]
+        assert_bitexact(ctx.matvec(t, x), oracle.matvec(w, synth.Q4_0, n, k, x), f"Q4_0 {k}->{n}")
+    t.free()
+
+
+@pytest.mark.parametrize("k,n", [(288, 32000), (2048, 2048), (2048, 256), (5632, 2048), (4096, 4096), (288, 768)])
+def test_gemv_q8_0_bitexact(ctx, oracle, k, n):
+    rng = np.random.default_rng(7 * k + n)
+    w = _w(rng, synth.Q8_0, n, k)
+    t = ctx.upload("output.weight", synth.Q8_0, k, n, w)
+    x = synth.activations(rng, 1, k)[0]
+    assert_bitexact(ctx.matvec(t, x), oracle.matvec(w, synth.Q8_0, n, k, x), f"Q8_0 {k}->{n}")
+    t.free()
+
+
+@pytest.mark.parametrize("k,n", [(4096, 32000), (2048, 32000), (5632, 2048), (256, 64)])
+def test_gemv_q6_k(ctx, oracle, k, n):
+    rng = np.random.default_rng(3 * k + n)
+    w = _w(rng, synth.Q6_K, n, k)
+    t = ctx.upload("output.weight", synth.Q6_K, k, n, w)
+    x = synth.activations(rng, 1, k)[0]
+    got = ctx.matvec(t, x)
+    want = oracle.matvec(w, synth.Q6_K, n, k, x)
+    u = ulp_diff(got, want)
+    assert u.max() <= 2, u.max()
+    assert (u == 0).mean() >= 0.999, (u == 0).mean()
+    t.free()
+
+
+def test_matvec_errors_match_reference_text(ctx):
+    w = np.zeros(210, np.uint8)
+    t = ctx.upload("blk.3.ffn_down.weight", synth.Q6_K, 128, 2, w)
+    with pytest.raises(capi.MvhError, match="Q6_K matrix row not block aligned: blk.3.ffn_down.weight"):
+        ctx.matvec(t, np.zeros(128, np.float32))
+    with pytest.raises(capi.MvhError, match="does not match"):
+        ctx.upload("bad", synth.Q4_0, 64, 2, np.zeros(10, np.uint8))
+
+
+# ---------------------------------------------------------------- batched prefill
+
+@pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0])
+@pytest.mark.parametrize("name", ["blk.0.attn_q.weight", "blk.0.ffn_up.weight"])
+@pytest.mark.parametrize("batch", [2, 5, 11, 32])
+def test_matmul_v06_ref_mode_bitexact(ctx, oracle, ty, name, batch):
+    rng = np.random.default_rng(batch * 31 + ty)
+    k, n = 1024, 96
+    w = _w(rng, ty, n, k)
+    t = ctx.upload(name, ty, k, n, w)
+    x = synth.activations(rng, batch, k)
+    got = ctx.matmul_batch_v06(t, x, capi.MVH_ACT_REF)
+    want = oracle.matmul_batch_v06(w, ty, n, k, x, is_ffn="ffn" in name, force_q8=False)
+    assert_bitexact(got, want, f"v06 ref {name} B={batch}")
+    t.free()
+
+
+@pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0])
+@pytest.mark.parametrize("batch,k,n", [(2, 1024, 96), (32, 4096, 512), (7, 288, 768)])
+def test_matmul_v06_q8_mode_bitexact(ctx, oracle, ty, batch, k, n):
+    rng = np.random.default_rng(batch + k + n + ty)
+    w = _w(rng, ty, n, k)
+    t = ctx.upload("blk.0.attn_k.weight", ty, k, n, w)
+    x = synth.activations(rng, batch, k)
+    got = ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8)
+    want = oracle.matmul_batch_v06(w, ty, n, k, x, is_ffn=False, force_q8=True)
+    assert_bitexact(got, want, f"v06 q8 B={batch}")
+    t.free()
+
+
+@pytest.mark.parametrize("ty,k", [(synth.Q4_0, 288), (synth.Q8_0, 1024), (synth.Q6_K, 512)])
+def test_matmul_batch_fallback(ctx, oracle, ty, k):
+    rng = np.random.default_rng(k + ty)
+    n = 80
+    w = _w(rng, ty, n, k)
+    t = ctx.upload("blk.1.ffn_down.weight", ty, k, n, w)
+    x = synth.activations(rng, 3, k)
+    got = ctx.matmul_batch(t, x)
+    want = oracle.matmul_batch(w, ty, n, k, x)
+    if ty == synth.Q6_K:
+        assert ulp_diff(got, want).max() <= 2
+    else:
+        assert_bitexact(got, want, "matmul_batch")
+    # batch 1 through v06 falls back to the same per-token fp32 dot
+    assert_bitexact(ctx.matmul_batch_v06(t, x[:1]), got[:1], "v06 B=1")
+    t.free()
+
+
+@pytest.mark.parametrize("ty,k", [(synth.Q4_0, 288), (synth.Q8_0, 4096), (synth.Q6_K, 2048)])
+def test_read_row(ctx, oracle, ty, k):
+    rng = np.random.default_rng(k)
+    n = 50
+    w = _w(rng, ty, n, k)
+    t = ctx.upload("token_embd.weight", ty, k, n, w)
+    for row in (0, 17, n - 1):
+        assert_bitexact(ctx.read_row(t, row), oracle.read_row(w, ty, n, k, row), f"row {row}")
+    with pytest.raises(capi.MvhError, match="tensor row shape mismatch"):
+        ctx.read_row(t, n)
+    t.free()
+
+
+# ---------------------------------------------------------------- paged KV + attention
+
+@pytest.mark.parametrize("kv_dim,page", [(288, 128), (256, 16), (4096, 128)])
+def test_kv_write_bits_and_pages(ctx, oracle, kv_dim, page):
+    rng = np.random.default_rng(kv_dim + page)
+    kv = ctx.kv_cache(2, kv_dim, page, 400)
+    okv = oracle.kv(kv_dim, page)
+    n = 300
+    k = rng.standard_normal((n, kv_dim), dtype=np.float32) * np.float32(3)
+    v = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    kv.write(1, 0, k[:37], v[:37])          # a multi-token write
+    for p in range(37, n):
+        kv.write(1, p, k[p], v[p])
+    for p in range(n):
+        okv.write(p, k[p], v[p])
+    for p in (0, 36, 37, page - 1, page, n - 1):
+        assert np.array_equal(kv.read_row(1, p, 0), okv.row(p, 0))
+        assert np.array_equal(kv.read_row(1, p, 1), okv.row(p, 1))
+    assert kv.bytes_allocated() == okv.bytes_allocated()
+    with pytest.raises(capi.MvhError, match="page missing"):
+        kv.read_row(0, 0, 0)
+    kv.reset()
+    assert kv.bytes_allocated() == 0
+    with pytest.raises(capi.MvhError, match="context exhausted"):
+        kv.write(0, 399, k[:2], v[:2])
+    kv.close()
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,pos", [(6, 6, 48, 0), (6, 6, 48, 200), (32, 4, 64, 511),
+                                                (32, 32, 128, 767), (32, 32, 128, 130)])
+def test_attn_decode(ctx, oracle, n_head, n_kv, hd, pos):
+    rng = np.random.default_rng(n_head + hd + pos)
+    kv_dim = n_kv * hd
+    kv = ctx.kv_cache(1, kv_dim, 128, 1024)
+    okv = oracle.kv(kv_dim, 128)
+    k = rng.standard_normal((pos + 1, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((pos + 1, kv_dim), dtype=np.float32)
+    kv.write(0, 0, k, v)
+    for p in range(pos + 1):
+        okv.write(p, k[p], v[p])
+    q = rng.standard_normal(n_head * hd, dtype=np.float32) * np.float32(2)
+    got = kv.attn_decode(0, q, pos, n_head, n_kv, hd)
+    want = okv.attn_decode(q, pos, n_head, n_kv, hd)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel <= 1e-6, rel
+    assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+    print(f"attn exact fraction {(bits(got) == bits(want)).mean():.4f}")
+    kv.close()
