@@ -94,6 +94,10 @@ int mvh_tensor_info(const mvh_tensor* t, uint32_t* ggml_type, uint64_t* ne0, uin
 int mvh_quantize_q8(mvh_context* ctx, const float* x, size_t batch, size_t cols, int8_t* q, float* d, int ptr_kind);
 /* tensor_matvec: y[ne1] = W . x[ne0] */
 int mvh_matvec(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, int ptr_kind);
+/* Q4_0 weights x an already quantized Q8 activation (the q/d pair mvh_quantize_q8 returns): the
+ * per-row kernel of tensor_matvec's Q4_0 branch (dot_q4_q8, src/gguf_kernels.cpp:189) without the
+ * quantization, so one quantized input can feed several tensors.  Device q must be 16-byte aligned. */
+int mvh_matvec_q8(mvh_context* ctx, const mvh_tensor* w, const int8_t* q, const float* d, float* y, int ptr_kind);
 /* tensor_matmul_batch: y[b*ne1 + r] = row r . x[b*ne0 ..], fp32 activations */
 int mvh_matmul_batch(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, size_t batch, int ptr_kind);
 /* tensor_matmul_batch_v06 with its fallbacks; act_mode MVH_ACT_REF or MVH_ACT_Q8.  As in the

@@ -52,6 +52,7 @@ _SIGS = {
                                C.POINTER(_vp)]),
     "mvh_quantize_q8": (_int, [_vp, _vp, _sz, _sz, _vp, _vp, _int]),
     "mvh_matvec": (_int, [_vp, _vp, _vp, _vp, _int]),
+    "mvh_matvec_q8": (_int, [_vp, _vp, _vp, _vp, _vp, _int]),
     "mvh_matmul_batch": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
     "mvh_matmul_batch_v06": (_int, [_vp, _vp, _vp, _vp, _sz, _int, _int]),
     "mvh_read_row_f32": (_int, [_vp, _vp, _sz, _vp, _int]),
@@ -173,6 +174,14 @@ class Context:
             y = np.empty(w.ne1, np.float32)
             x = np.ascontiguousarray(x, np.float32)
         self._check(self.lib.mvh_matvec(self.h, w.h, _ptr(x), _ptr(y), _kind(x, y)))
+        return y
+
+    def matvec_q8(self, w: "Tensor", q, d, y=None):
+        if y is None:
+            q = np.ascontiguousarray(q, np.int8)
+            d = np.ascontiguousarray(d, np.float32)
+            y = np.empty(w.ne1, np.float32)
+        self._check(self.lib.mvh_matvec_q8(self.h, w.h, _ptr(q), _ptr(d), _ptr(y), _kind(q, d, y)))
         return y
 
     def matmul_batch(self, w: "Tensor", x, y=None):

@@ -374,7 +374,7 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
             ActView a;
             if (int rc = act_buffers(c, 1, cols, &a)) return rc;
             MVH_HIP(mvh::launch_quantize_q8(static_cast<const float*>(xd), a.q, a.d, a.s, 1, cols, c->stream));
-            MVH_HIP(mvh::launch_gemv_q4_0(W, a.q, a.d, a.s, yd, rows, cols, c->stream));
+            MVH_HIP(mvh::launch_gemv_q4_0(W, a.q, a.d, yd, rows, cols, c->stream));
             break;
         }
         case MVH_TYPE_Q8_0:
@@ -384,6 +384,37 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
         default:
             return fail(MVH_E_TYPE, "unsupported matvec tensor type %s: %s", type_name(w->type), w->name.c_str());
     }
+    return finish_out(c, y, yd, rows * 4, kind);
+}
+
+int mvh_matvec_q8(mvh_context* c, const mvh_tensor* w, const int8_t* q, const float* d, float* y, int kind) {
+    CHECK_CTX(c);
+    if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (!q || !d || !y) return fail(MVH_E_INVALID, "null q/d/y");
+    if (w->type != MVH_TYPE_Q4_0)
+        return fail(MVH_E_TYPE, "Q8-activation matvec needs a Q4_0 tensor, got %s: %s", type_name(w->type),
+                    w->name.c_str());
+    const size_t cols = w->ne0, rows = w->ne1, nb = cols / 32;
+    if (cols % 32) return fail(MVH_E_SHAPE, "Q4_0 matrix row not block aligned: %s", w->name.c_str());
+    if (!rows) return MVH_OK;
+    const int8_t* qd = q;
+    const float* dd = d;
+    float* yd = y;
+    if (kind == MVH_HOST) {
+        ActView a;
+        if (int rc = act_buffers(c, 1, cols, &a)) return rc;
+        MVH_HIP(hipMemcpyAsync(a.q, q, cols, hipMemcpyHostToDevice, c->stream));
+        MVH_HIP(hipMemcpyAsync(a.d, d, nb * 4, hipMemcpyHostToDevice, c->stream));
+        if (int rc = grow(c, c->yout, rows * 4)) return rc;
+        qd = a.q;
+        dd = a.d;
+        yd = static_cast<float*>(c->yout.p);
+    } else if (kind != MVH_DEVICE) {
+        return fail(MVH_E_INVALID, "ptr_kind must be MVH_HOST or MVH_DEVICE");
+    } else if (reinterpret_cast<uintptr_t>(q) & 15) {
+        return fail(MVH_E_INVALID, "device q must be 16-byte aligned");
+    }
+    MVH_HIP(mvh::launch_gemv_q4_0(static_cast<const uint8_t*>(w->d), qd, dd, yd, rows, cols, c->stream));
     return finish_out(c, y, yd, rows * 4, kind);
 }
 
@@ -431,8 +462,7 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
             if (int rc = act_buffers(c, batch, cols, &a)) return rc;
             MVH_HIP(mvh::launch_quantize_q8(xd, a.q, a.d, a.s, batch, cols, c->stream));
             for (size_t b = 0; b < batch; ++b)
-                MVH_HIP(mvh::launch_gemv_q4_0(W, a.q + b * cols, a.d + b * nb, a.s + b * nb, yd + b * rows, rows, cols,
-                                              c->stream));
+                MVH_HIP(mvh::launch_gemv_q4_0(W, a.q + b * cols, a.d + b * nb, yd + b * rows, rows, cols, c->stream));
         } else {
             MVH_HIP(mvh::launch_gemv_q8_0(W, xd, yd, rows, cols, batch, c->stream));
         }

@@ -55,8 +55,7 @@ __device__ __forceinline__ void fold_pairs(const float2* s_pair, int pitch, int 
 template <int G>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_0_kernel(const uint8_t* __restrict__ W,
                                                                   const int8_t* __restrict__ aq,
-                                                                  const float* __restrict__ ad,
-                                                                  const int* __restrict__ as, float* __restrict__ y,
+                                                                  const float* __restrict__ ad, float* __restrict__ y,
                                                                   int N, int nb, int rows_per_wg) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int ngrp = (nb + 7) >> 3;
@@ -70,9 +69,23 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_0_kernel(const uint8_t* 
     const int K = nb * 32;
     for (int c = threadIdx.x; c < K / 16; c += blockDim.x)
         *reinterpret_cast<uint4*>(s_aq + (c >> 4) * kActPitch + (c & 15) * 16) = reinterpret_cast<const uint4*>(aq)[c];
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) s_ad[b] = ad[b];
+    __syncthreads();
+    // s_b = sum of the 32 activation bytes of block b, for the "-8" nibble bias
     for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-        s_ad[b] = ad[b];
-        s_as[b] = as[b];
+        const uint4* a = reinterpret_cast<const uint4*>(s_aq + (b >> 3) * kActPitch + (b & 7) * 32);
+        const uint4 a0 = a[0], a1 = a[1];
+        constexpr int ones = 0x01010101;
+        int t = 0;
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a0.x), ones, t, false);
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a0.y), ones, t, false);
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a0.z), ones, t, false);
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a0.w), ones, t, false);
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a1.x), ones, t, false);
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a1.y), ones, t, false);
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a1.z), ones, t, false);
+        t = __builtin_amdgcn_sdot4(static_cast<int>(a1.w), ones, t, false);
+        s_as[b] = t;
     }
     __syncthreads();
 
@@ -368,8 +381,8 @@ int pick_rows_per_wg(size_t rows, size_t nb, size_t pair_budget) {
 
 }  // namespace
 
-hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, const int* as, float* y,
-                            size_t rows, size_t cols, hipStream_t st) {
+hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows, size_t cols,
+                            hipStream_t st) {
     const int nb = static_cast<int>(cols / 32);
     const int ngrp = (nb + 7) / 8;
     const size_t fixed = static_cast<size_t>(ngrp) * kActPitch + 8u * nb;
@@ -377,9 +390,9 @@ hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad,
     const size_t lds = fixed + static_cast<size_t>(rpw) * (nb + 1) * sizeof(float2);
     const unsigned grid = static_cast<unsigned>((rows + rpw - 1) / rpw);
     if (nb % 8 == 0)
-        gemv_q4_0_kernel<8><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, as, y, static_cast<int>(rows), nb, rpw);
+        gemv_q4_0_kernel<8><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, static_cast<int>(rows), nb, rpw);
     else
-        gemv_q4_0_kernel<1><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, as, y, static_cast<int>(rows), nb, rpw);
+        gemv_q4_0_kernel<1><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, static_cast<int>(rows), nb, rpw);
     return hipGetLastError();
 }
 
