@@ -27,7 +27,7 @@ struct mvh_context {
 };
 
 struct mvh_tensor {
-    mvh_context* ctx = nullptr;
+    int device = 0;  // a tensor outlives nothing but its device: freeing it never touches the context
     std::string name;
     uint32_t type = 0;
     uint64_t ne0 = 0, ne1 = 0, nbytes = 0;
@@ -36,7 +36,7 @@ struct mvh_tensor {
 };
 
 struct mvh_kv_cache {
-    mvh_context* ctx = nullptr;
+    int device = 0;  // reset/destroy synchronise the device, so they never touch a context
     size_t n_layer = 0, kv_dim = 0, page_tokens = 0, max_tokens = 0, max_pages = 0;
     std::vector<uint16_t*> hk, hv;  // host mirror of the page tables, [layer*max_pages + page]
     uint16_t** dk = nullptr;        // device page tables
@@ -267,7 +267,7 @@ static int make_tensor(mvh_context* c, const char* name, uint32_t type, uint64_t
                     static_cast<unsigned long long>(ne0), name ? name : "");
     auto* t = new (std::nothrow) mvh_tensor;
     if (!t) return fail(MVH_E_NOMEM, "host allocation failed");
-    t->ctx = c;
+    t->device = c->device;
     t->name = name ? name : "";
     t->type = type;
     t->ne0 = ne0;
@@ -315,9 +315,8 @@ int mvh_tensor_wrap(mvh_context* c, const char* name, uint32_t type, uint64_t ne
 int mvh_tensor_free(mvh_tensor* t) {
     if (!t) return MVH_OK;
     if (t->owned && t->d) {
-        (void)hipSetDevice(t->ctx->device);
-        (void)hipStreamSynchronize(t->ctx->stream);
-        (void)hipFree(t->d);
+        (void)hipSetDevice(t->device);
+        (void)hipFree(t->d);  // hipFree waits for work that may still read it
     }
     delete t;
     return MVH_OK;
@@ -371,6 +370,11 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
     switch (w->type) {
         case MVH_TYPE_Q4_0: {
             if (cols % 32) return fail(MVH_E_SHAPE, "Q4_0 matrix row not block aligned: %s", w->name.c_str());
+            if (mvh::gemv_q4_0_persistent_ok(cols)) {  // quantization fused into the GEMV
+                MVH_HIP(mvh::launch_gemv_q4_0_persistent(W, static_cast<const float*>(xd), nullptr, nullptr, yd, rows,
+                                                         cols, c->stream));
+                break;
+            }
             ActView a;
             if (int rc = act_buffers(c, 1, cols, &a)) return rc;
             MVH_HIP(mvh::launch_quantize_q8(static_cast<const float*>(xd), a.q, a.d, a.s, 1, cols, c->stream));
@@ -536,7 +540,7 @@ int mvh_kv_create(mvh_context* c, size_t n_layer, size_t kv_dim, size_t page_tok
     if (max_tokens > 16000) return fail(MVH_E_RANGE, "max_tokens above 16000 is not supported");
     auto* kv = new (std::nothrow) mvh_kv_cache;
     if (!kv) return fail(MVH_E_NOMEM, "host allocation failed");
-    kv->ctx = c;
+    kv->device = c->device;
     kv->n_layer = n_layer;
     kv->kv_dim = kv_dim;
     kv->page_tokens = page_tokens;
@@ -559,8 +563,8 @@ int mvh_kv_create(mvh_context* c, size_t n_layer, size_t kv_dim, size_t page_tok
 
 int mvh_kv_reset(mvh_kv_cache* kv) {
     if (!kv) return fail(MVH_E_INVALID, "null KV cache");
-    MVH_HIP(hipSetDevice(kv->ctx->device));
-    MVH_HIP(hipStreamSynchronize(kv->ctx->stream));
+    MVH_HIP(hipSetDevice(kv->device));
+    MVH_HIP(hipDeviceSynchronize());
     for (size_t i = 0; i < kv->hk.size(); ++i)
         if (kv->hk[i]) {
             kv->pool.push_back(kv->hk[i]);
@@ -575,8 +579,8 @@ int mvh_kv_reset(mvh_kv_cache* kv) {
 
 int mvh_kv_destroy(mvh_kv_cache* kv) {
     if (!kv) return MVH_OK;
-    (void)hipSetDevice(kv->ctx->device);
-    (void)hipStreamSynchronize(kv->ctx->stream);
+    (void)hipSetDevice(kv->device);
+    (void)hipDeviceSynchronize();
     for (auto* p : kv->hk)
         if (p) (void)hipFree(p);
     for (auto* p : kv->pool) (void)hipFree(p);

@@ -89,6 +89,28 @@ __device__ __forceinline__ double wave_sum(double v) {
     return mine + other;
 }
 
+// quantize_q8 (src/gguf_kernels.cpp:160-172) for one 32-element block held as
+// 4 consecutive floats in each lane of an aligned group of 8 lanes:
+//   mx = max|z| (exact in any order), d = mx > 0 ? mx/127 : 1, inv = 1/d,
+//   q = clamp(round_half_away(z*inv), -127, 127).
+// Returns the lane's 4 int8 values packed; d and the block sum s = sum(q)
+// are the same in all 8 lanes.  Every lane of the group must call it.
+__device__ __forceinline__ uint32_t quantize_q8_x4(float4 v, float& d, int& s) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = group_max<8>(m);
+    d = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, d);
+    auto qz = [&](float z) {
+        float r = roundf(z * inv);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        return static_cast<int>(r);
+    };
+    const int q0 = qz(v.x), q1 = qz(v.y), q2 = qz(v.z), q3 = qz(v.w);
+    s = group_sum<8>(q0 + q1 + q2 + q3);
+    return (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (weights are read once per call: nontemporal hint).

@@ -12,6 +12,9 @@
 // starts 16-byte aligned when K % 256 == 0); other K take a 1-block path.
 #include "mvh_kernels.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace mvh {
 namespace {
 
@@ -52,7 +55,14 @@ __device__ __forceinline__ void fold_pairs(const float2* s_pair, int pitch, int 
     }
 }
 
-template <int G>
+// Weight load modes of the 8-block path:
+//   kLoadStream  each lane reads its own 144-byte unit (9 x 16 B, lane stride 144 B), non-temporal;
+//   kLoadCached  the same pattern through the caches;
+//   kLoadStaged  the tile is read with coalesced 16-byte loads (consecutive lanes, consecutive
+//                bytes) into LDS, and every lane then reads its unit from LDS.
+enum { kLoadStream = 0, kLoadCached = 1, kLoadStaged = 2 };
+
+template <int G, int MODE>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_0_kernel(const uint8_t* __restrict__ W,
                                                                   const int8_t* __restrict__ aq,
                                                                   const float* __restrict__ ad, float* __restrict__ y,
@@ -94,6 +104,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_0_kernel(const uint8_t* 
     const int upr = nb / G;
     const int nunits = rows * upr;
     const uint8_t* tile = W + static_cast<size_t>(r0) * nb * 18;
+    // raw weight tile (staged mode), 16-byte aligned after the pair buffer
+    uint8_t* s_raw = smem + ((reinterpret_cast<uint8_t*>(s_pair + rows_per_wg * pitch) - smem + 15) & ~15);
+    if constexpr (MODE == kLoadStaged && G == 8) {
+        const int nchunks = rows * nb * 18 / 16;  // nb % 8 == 0: whole 16-byte chunks
+        for (int c = threadIdx.x; c < nchunks; c += blockDim.x)
+            reinterpret_cast<uint4*>(s_raw)[c] = ld_stream16(reinterpret_cast<const uint4*>(tile) + c);
+        __syncthreads();
+    }
 
     for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
         const int row = u / upr;
@@ -101,10 +119,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_0_kernel(const uint8_t* 
         float2* pout = s_pair + row * pitch + b0;
         if constexpr (G == 8) {
             uint32_t w[36];
-            const uint4* src = reinterpret_cast<const uint4*>(tile + static_cast<size_t>(u) * 144);
+            const uint4* src = MODE == kLoadStaged ? reinterpret_cast<const uint4*>(s_raw + u * 144)
+                                                   : reinterpret_cast<const uint4*>(tile + static_cast<size_t>(u) * 144);
 #pragma unroll
             for (int k = 0; k < 9; ++k) {
-                const uint4 v = ld_stream16(src + k);
+                const uint4 v = MODE == kLoadStream ? ld_stream16(src + k) : src[k];
                 w[4 * k] = v.x;
                 w[4 * k + 1] = v.y;
                 w[4 * k + 2] = v.z;
@@ -383,16 +402,30 @@ int pick_rows_per_wg(size_t rows, size_t nb, size_t pair_budget) {
 
 hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows, size_t cols,
                             hipStream_t st) {
+    if (gemv_q4_0_persistent_ok(cols)) return launch_gemv_q4_0_persistent(W, nullptr, aq, ad, y, rows, cols, st);
+    static const int mode = [] {
+        const char* e = getenv("MVH_GEMV_LOAD");
+        return e ? atoi(e) : kLoadStaged;
+    }();
     const int nb = static_cast<int>(cols / 32);
     const int ngrp = (nb + 7) / 8;
     const size_t fixed = static_cast<size_t>(ngrp) * kActPitch + 8u * nb;
-    const int rpw = pick_rows_per_wg(rows, nb, 60 * 1024 - fixed);
-    const size_t lds = fixed + static_cast<size_t>(rpw) * (nb + 1) * sizeof(float2);
+    const bool staged = mode == kLoadStaged && nb % 8 == 0;
+    // staged tiles also hold the raw weight bytes of every row in LDS
+    const size_t per_row = (nb + 1) * sizeof(float2) + (staged ? 18u * nb : 0u);
+    int rpw = pick_rows_per_wg(rows, nb, 60 * 1024 - fixed);
+    rpw = std::max(1, std::min<int>(rpw, static_cast<int>((60 * 1024 - fixed) / per_row)));
+    const size_t lds = fixed + static_cast<size_t>(rpw) * per_row + 16;
     const unsigned grid = static_cast<unsigned>((rows + rpw - 1) / rpw);
-    if (nb % 8 == 0)
-        gemv_q4_0_kernel<8><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, static_cast<int>(rows), nb, rpw);
+    const int n = static_cast<int>(rows);
+    if (nb % 8 != 0)
+        gemv_q4_0_kernel<1, kLoadCached><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, n, nb, rpw);
+    else if (mode == kLoadStream)
+        gemv_q4_0_kernel<8, kLoadStream><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, n, nb, rpw);
+    else if (mode == kLoadCached)
+        gemv_q4_0_kernel<8, kLoadCached><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, n, nb, rpw);
     else
-        gemv_q4_0_kernel<1><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, static_cast<int>(rows), nb, rpw);
+        gemv_q4_0_kernel<8, kLoadStaged><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, n, nb, rpw);
     return hipGetLastError();
 }
 

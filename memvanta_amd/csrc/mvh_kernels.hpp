@@ -23,6 +23,11 @@ hipError_t launch_gemv_q8_0(const uint8_t* W, const float* x, float* y, size_t r
                             hipStream_t st);
 hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                             hipStream_t st);
+// Persistent Q4_0 x Q8 GEMV (cols % 256 == 0): x != nullptr quantizes the fp32
+// input inside the kernel; otherwise aq (16-byte aligned) / ad are the Q8 input.
+bool gemv_q4_0_persistent_ok(size_t cols);
+hipError_t launch_gemv_q4_0_persistent(const uint8_t* W, const float* x, const int8_t* aq, const float* ad, float* y,
+                                       size_t rows, size_t cols, hipStream_t st);
 // dot_q4_0_fp32 per (row, token): y[b*rows + r]
 hipError_t launch_gemv_q4_0_f32act(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                                    hipStream_t st);

@@ -4,30 +4,18 @@
 namespace mvh {
 
 // quantize_q8 (src/gguf_kernels.cpp:160-172), one 32-element block per 8
-// lanes, 4 elements per lane (one 16-byte load, one 4-byte store):
-//   mx = max|z| (exact in any order), d = mx > 0 ? mx/127 : 1, inv = 1/d,
-//   q = clamp(round_half_away(z*inv), -127, 127).
-// Besides q and the f32 scale d it writes s = sum of the 32 q values, which
-// lets the GEMV fold the Q4_0 "-8" bias into one multiply per block.
+// lanes, 4 elements per lane (one 16-byte load, one 4-byte store).  Besides q
+// and the f32 scale d it writes s = sum of the 32 q values.
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float4* __restrict__ x, uint32_t* __restrict__ q,
                                                           float* __restrict__ d, int* __restrict__ s, size_t n4) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const bool live = i < n4;  // n4 % 8 == 0, so an 8-lane group is all-live or all-dead
-    float4 v = live ? x[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    m = group_max<8>(m);
-    const float dd = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
-    const float inv = __fdiv_rn(1.0f, dd);
-    auto qz = [&](float z) {
-        float r = roundf(z * inv);
-        r = fminf(fmaxf(r, -127.0f), 127.0f);
-        return static_cast<int>(r);
-    };
-    const int q0 = qz(v.x), q1 = qz(v.y), q2 = qz(v.z), q3 = qz(v.w);
-    const int bsum = group_sum<8>(q0 + q1 + q2 + q3);
+    const float4 v = live ? x[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float dd;
+    int bsum;
+    const uint32_t packed = quantize_q8_x4(v, dd, bsum);
     if (live) {
-        q[i] = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
-               ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
+        q[i] = packed;
         if ((threadIdx.x & 7) == 0) {
             d[i >> 3] = dd;
             s[i >> 3] = bsum;
