@@ -3,30 +3,27 @@
 // Numerics are those of tensor_matvec's Q4_0 branch (src/gguf_kernels.cpp:246):
 // x is quantized with quantize_q8 (:160-172), then per row
 //   sum = fma(f16(d_w) * d_a, float(isum_b), sum)   over blocks b in order (:189).
-// Work split:
-//   * a tile is R whole rows; each of the R * K/256 "units" (8 consecutive
-//     blocks = 144 bytes of one row) belongs to one lane, which turns its 8
-//     blocks into (p_b = d_w*d_a, f_b = float(isum_b)) pairs (isum via
-//     v_dot4_i32_i8, exact) and stores them in LDS;
-//   * after one barrier, R lanes fold the pairs of their row in block order
-//     with v_fma_f32 -- the reference's own chain, so y is bit-identical.
-// Throughput structure:
-//   * workgroups are persistent (grid <= 3 per CU) and walk tiles with a
-//     stride of gridDim.x;
-//   * the weight units of the next two tiles are already in flight in
-//     registers while the current tile's pairs are folded;
-//   * the fp32 input is quantized inside every workgroup (it is tiny and
-//     cached), overlapping the first weight loads -- no separate launch;
-//   * pair buffers are double-buffered, so each tile needs one barrier, and
-//     padded (9 pairs per unit) so the unit-strided LDS writes do not collide.
+// Work split (one wave = one tile of TR = 64/(K/256) whole rows):
+//   * lane (r, u) owns "unit" u of row r -- 8 consecutive blocks = 144 bytes,
+//     the units of a row sit in consecutive lanes -- loads it with 9 x 16-byte
+//     loads and turns its 8 blocks into (p_b = d_w*d_a, f_b = float(isum_b))
+//     pairs held in registers (isum via v_dot4_i32_i8, exact);
+//   * the row's fma chain then walks the lanes in unit order: at every stage
+//     each lane takes its left neighbour's running value (DPP wave_shr:1) and
+//     applies its 8 fmas; after K/256 stages the last lane of the row holds
+//     the reference's in-order chain, bit for bit.
+// Throughput structure: persistent waves walk tiles with a stride of the
+// grid's wave count; the units of the next two tiles are in flight in
+// registers while a tile is reduced; the fp32 input is quantized into LDS by
+// every workgroup (no separate launch) while the first loads are in flight.
 #include "mvh_kernels.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace mvh {
 namespace {
 
-constexpr int kT = 256;         // threads per workgroup
 constexpr int kActPitch = 272;  // LDS bytes per 8-block activation group (256 + 16 pad)
 
 __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ W, size_t row_bytes, int grow, int unit,
@@ -84,7 +81,7 @@ __device__ __forceinline__ float shift_up1(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x138, 0xf, 0xf, false));
 }
 
-template <bool QUANT>
+template <bool QUANT, int kT>
 __global__ __launch_bounds__(kT) void gemv_q4_0_persistent(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                            const int8_t* __restrict__ aq,
                                                            const float* __restrict__ ad, float* __restrict__ y, int N,
@@ -124,6 +121,7 @@ __global__ __launch_bounds__(kT) void gemv_q4_0_persistent(const uint8_t* __rest
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
+                if (i0 + k * kT >= n4) break;  // uniform: skip slices past the end
                 const int i = i0 + k * kT + t;
                 float d;
                 int s;
@@ -171,13 +169,17 @@ __global__ __launch_bounds__(kT) void gemv_q4_0_persistent(const uint8_t* __rest
         const bool live = worker && grow < N;
         float2 pr[8];
         if (live) unit_pairs(w, agrp, s_ad, s_as, b0, pr);
+        // every lane redoes its 8 fmas from its left neighbour's value at every
+        // stage; lane u's value is final from stage u on (its neighbour's was
+        // final at u-1), so after upr stages the last lane of each row holds
+        // the complete in-order chain
         float sum = 0.0f;
         for (int st = 0; st < upr; ++st) {
             const float in = shift_up1(sum);
             float acc = u == 0 ? 0.0f : in;
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc = fmaf(pr[j].x, pr[j].y, acc);
-            if (u == st) sum = acc;
+            sum = acc;
         }
         if (live && u == upr - 1) y[grow] = sum;
     };
@@ -221,12 +223,23 @@ hipError_t launch_gemv_q4_0_persistent(const uint8_t* W, const float* x, const i
     const int tr = 64 / (nb / 8);
     const int ntiles = static_cast<int>((rows + tr - 1) / tr);
     const size_t lds = persistent_lds(nb);
-    const int waves = std::min(ntiles, g_cu_count * 16);
-    const int grid = (waves + kT / 64 - 1) / (kT / 64);
-    if (x)
-        gemv_q4_0_persistent<true><<<grid, kT, lds, st>>>(W, x, nullptr, nullptr, y, static_cast<int>(rows), nb, ntiles);
-    else
-        gemv_q4_0_persistent<false><<<grid, kT, lds, st>>>(W, nullptr, aq, ad, y, static_cast<int>(rows), nb, ntiles);
+    static const int wpc = [] {  // resident waves per CU (tuning override)
+        const char* e = getenv("MVH_GEMV_WPC");
+        return e && atoi(e) > 0 ? atoi(e) : 16;
+    }();
+    const int waves = std::min(ntiles, g_cu_count * wpc);
+    if (x) {
+        // fp32 input: every workgroup quantizes it into LDS
+        constexpr int T = 256;
+        const int grid = (waves + T / 64 - 1) / (T / 64);
+        gemv_q4_0_persistent<true, T><<<grid, T, lds, st>>>(W, x, nullptr, nullptr, y, static_cast<int>(rows), nb,
+                                                            ntiles);
+    } else {
+        constexpr int T = 256;
+        const int grid = (waves + T / 64 - 1) / (T / 64);
+        gemv_q4_0_persistent<false, T><<<grid, T, lds, st>>>(W, nullptr, aq, ad, y, static_cast<int>(rows), nb,
+                                                             ntiles);
+    }
     return hipGetLastError();
 }
 

@@ -1,0 +1,292 @@
+"""Pins the C restatement (oracle/mv_oracle.c) to MemVanta's own outputs.
+
+* golden vectors written by tests/golden/make_golden.py from the compiled
+  reference (bit-exact comparisons);
+* the compiled reference itself when oracle/_ref is built here (exhaustive
+  fp32_to_fp16 sweep, live model run);
+* closed forms and invariants (exact fp16 decode, quantizer special cases,
+  fp64 brute-force bounds, thread-count independence, 8- vs 4-token blocking);
+* planted mistakes: mutated copies of the oracle must FAIL the golden check,
+  which shows the checks above would catch each of those errors.
+"""
+import hashlib
+import os
+import shutil
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, assert_bitexact, bits, golden
+from memvanta_amd import synth
+
+import importlib.util
+
+_spec = importlib.util.spec_from_file_location("make_golden", os.path.join(ROOT, "tests", "golden", "make_golden.py"))
+mg = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(mg)
+
+
+@pytest.fixture(scope="module")
+def mats():
+    """Weights of make_golden.MATS regenerated from the seed (sha-checked)."""
+    g = golden("kernels.npz")
+    rng = np.random.default_rng(mg.MAT_SEED)
+    out = {}
+    for name, rows, cols, ty in mg.MATS:
+        w = synth.quantize(ty, rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
+        key = name.replace(".", "_")
+        assert hashlib.sha256(w.tobytes()).hexdigest() == str(g[f"{key}__sha"]), f"weight generator drifted: {name}"
+        out[name] = (w, rows, cols, ty, key)
+    return out
+
+
+@pytest.fixture(scope="module")
+def tiny_model(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("model") / "tiny.gguf")
+    sha = synth.write_model(synth.TINY, path, seed=1234)
+    assert sha == str(golden("model_tiny.npz")["model_sha"]), "model generator drifted"
+    return path
+
+
+# ----------------------------------------------------------------- fp16
+
+def test_fp16_to_fp32_exhaustive(oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.fp16_to_fp32(h)
+    want = h.view(np.float16).astype(np.float32)
+    ok = ~np.isnan(want)
+    assert np.array_equal(bits(got)[ok], bits(want)[ok])
+    assert np.isnan(got[~ok]).all()
+
+
+def test_fp32_to_fp16_golden(oracle):
+    g = golden("fp16.npz")
+    got = oracle.fp32_to_fp16(g["bits"].view(np.float32))
+    assert np.array_equal(got, g["half"])
+    # the quirks the golden set covers: ties away from zero, OR-ed carry
+    kv = np.array([1.00048828125, 1.9999, 0.12499999, 65504.0, 70000.0, 1e-6, -1.9999], np.float32)
+    assert [int(v) for v in oracle.fp32_to_fp16(kv)] == [0x3c01, 0x3c00, 0x2c00, 0x7bff, 0x7c00, 0x0011, 0xbc00]
+
+
+def test_fp32_to_fp16_exhaustive_vs_reference(oracle, ref):
+    step = 1 << 28
+    for first in range(0, 1 << 32, step):
+        want = ref.fp32_to_fp16_bits(first, step)
+        bad = oracle.lib.mvo_fp32_to_fp16_count_mismatch(first, step, want)
+        assert bad == 0, f"{bad} mismatches in [0x{first:08x}, +2^28)"
+
+
+# ----------------------------------------------------------------- quantizer
+
+def test_quantizer_probe_golden(oracle):
+    g = golden("kernels.npz")
+    w, x, y = g["probe__w"], g["probe__x"], g["probe__y"]
+    for i in range(x.shape[0]):
+        assert_bitexact(oracle.matvec(w, synth.Q4_0, 256, 256, x[i]), y[i], f"probe {i}")
+
+
+def test_quantizer_closed_form(oracle):
+    g = golden("kernels.npz")
+    x = g["probe__x"]
+    q, d = oracle.quantize_q8(x)
+    # the probe rows recover d_a * q_e exactly rounded: same q from both sides
+    y = g["probe__y"]
+    for i in range(x.shape[0]):
+        rec = (d[i].repeat(32).astype(np.float64) * q[i]).astype(np.float32)
+        assert np.array_equal(bits(rec), bits(y[i]))
+    blocks = x.reshape(x.shape[0], -1, 32)
+    mx = np.abs(blocks).max(axis=2)
+    assert np.array_equal(d[mx > 0], (mx[mx > 0] / np.float32(127)).astype(np.float32))
+    assert (d[mx == 0] == 1).all() and (q.reshape(blocks.shape)[mx == 0] == 0).all()
+    assert np.abs(q).max() == 127
+    # x[2][:8] has block max 127 -> d = 1, and ties round away from zero
+    assert list(q[2][:8]) == [3, -3, 1, -1, 127, 127, -127, 2]
+    assert q[3][32:64].tolist() == [127] * 32  # 1e-30 block: d = mx/127 still normalises
+
+
+# ----------------------------------------------------------------- kernels
+
+def test_matvec_golden(oracle, mats):
+    g = golden("kernels.npz")
+    for name, (w, rows, cols, ty, key) in mats.items():
+        assert_bitexact(oracle.matvec(w, ty, rows, cols, g[f"{key}__x"]), g[f"{key}__matvec"], f"matvec {name}")
+
+
+def test_matmul_batch_golden(oracle, mats):
+    g = golden("kernels.npz")
+    for name, (w, rows, cols, ty, key) in mats.items():
+        assert_bitexact(oracle.matmul_batch(w, ty, rows, cols, g[f"{key}__xb"]), g[f"{key}__batch"], f"batch {name}")
+
+
+def test_matmul_v06_golden_both_modes(oracle, mats):
+    g = golden("kernels.npz")
+    n = 0
+    for name, (w, rows, cols, ty, key) in mats.items():
+        for B in (2, 5, 11, 32):
+            if f"{key}__v06_x{B}" not in g:
+                continue
+            X = g[f"{key}__v06_x{B}"]
+            ffn = ".ffn_" in name
+            assert_bitexact(oracle.matmul_batch_v06(w, ty, rows, cols, X, ffn, False), g[f"{key}__v06_ref{B}"],
+                            f"v06 ref {name} B={B}")
+            assert_bitexact(oracle.matmul_batch_v06(w, ty, rows, cols, X, ffn, True), g[f"{key}__v06_q8{B}"],
+                            f"v06 q8 {name} B={B}")
+            n += 1
+    assert n == 12  # three K=1024 tensors x four batch sizes
+
+
+def test_read_row_golden(oracle, mats):
+    g = golden("kernels.npz")
+    w, rows, cols, ty, key = mats["token_embd.weight"]
+    assert_bitexact(oracle.read_row(w, ty, rows, cols, 5), g[f"{key}__row5"], "read_row")
+
+
+def test_fp64_bounds(oracle, mats):
+    """The fp32 results stay within a few ulp-scale units of the exact dot."""
+    g = golden("kernels.npz")
+    for name, (w, rows, cols, ty, key) in mats.items():
+        x = g[f"{key}__x"]
+        W = synth.dequantize(ty, w, rows, cols)
+        if ty == synth.Q4_0:  # the activation is quantized first
+            q, d = oracle.quantize_q8(x)
+            xe = q.astype(np.float64) * np.repeat(d.astype(np.float64), 32)
+        else:
+            xe = x.astype(np.float64)
+        exact = W @ xe
+        got = oracle.matvec(w, ty, rows, cols, x).astype(np.float64)
+        scale = np.abs(W) @ np.abs(xe)
+        assert (np.abs(got - exact) <= 1e-6 * scale + 1e-30).all(), name
+
+
+def test_thread_count_independence(oracle, mats):
+    g = golden("kernels.npz")
+    for name, (w, rows, cols, ty, key) in mats.items():
+        x = g[f"{key}__x"]
+        assert_bitexact(oracle.matvec(w, ty, rows, cols, x, threads=1), oracle.matvec(w, ty, rows, cols, x, threads=7),
+                        name)
+
+
+def test_batch8_equals_two_batch4(oracle, mats):
+    """FFN tensors block 8 tokens as two 4-token calls: identical results."""
+    g = golden("kernels.npz")
+    w, rows, cols, ty, key = mats["blk.0.ffn_up.weight"]
+    X = g[f"{key}__v06_x32"]
+    assert_bitexact(oracle.matmul_batch_v06(w, ty, rows, cols, X, True), oracle.matmul_batch_v06(w, ty, rows, cols, X, False),
+                    "batch8 vs batch4")
+
+
+def test_kv_golden(oracle):
+    g = golden("kv.npz")
+    kv = oracle.kv(64, int(g["page"]))
+    for p in range(g["k"].shape[0]):
+        kv.write(p, g["k"][p], g["v"][p])
+    q = g["q"]
+    dots = np.array([[kv.dot_key(p, off, q[off:off + 32]) for off in (0, 32)] for p in range(g["k"].shape[0])],
+                    np.float32)
+    assert_bitexact(dots, g["dots"], "dot_key")
+    acc = np.zeros(64, np.float32)
+    for p in range(g["k"].shape[0]):
+        kv.add_value(p, 0, np.float32(0.37 / (p + 1)), acc)
+    assert_bitexact(acc, g["acc"], "add_value")
+    assert kv.bytes_allocated() == int(g["bytes"])
+
+
+# ----------------------------------------------------------------- model
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_tiny_model_golden(oracle, tiny_model, mode):
+    g = golden("model_tiny.npz")
+    m = oracle.model(tiny_model, ctx=256, force_q8=bool(mode))
+    assert_bitexact(m.prefill(g["prompt"], 32), g[f"prefill_logits_m{mode}"], "prefill logits")
+    ids, cur = [], 17
+    for _ in range(12):
+        lg = m.forward(cur)
+        cur = int(np.argmax(lg))
+        ids.append(cur)
+    assert ids == g[f"decode_ids_m{mode}"].tolist()
+    assert_bitexact(lg, g[f"decode_last_logits_m{mode}"], "decode logits")
+    assert m.kv_bytes() == int(g[f"kv_bytes_m{mode}"])
+    m.reset()
+    assert_bitexact(m.prefill(g["prompt33"], 32), g[f"prefill33_logits_m{mode}"], "prefill 32+1")
+
+
+def test_tiny_model_vs_reference_live(oracle, ref, tiny_model):
+    mo = oracle.model(tiny_model, ctx=256)
+    mr = ref.model(tiny_model, ctx=256)
+    t = synth.prompt_tokens(77, 70)
+    assert_bitexact(mo.prefill(t, 32), mr.prefill(t, 32), "live prefill")
+    for tok in (3, 31999, 0):
+        assert_bitexact(mo.forward(tok), mr.forward(tok), "live decode")
+
+
+def test_model_errors(oracle, tiny_model):
+    m = oracle.model(tiny_model, ctx=4)
+    with pytest.raises(RuntimeError, match="token id out of range"):
+        m.forward(32000)
+    m.prefill(np.array([1, 2, 3, 4], np.int32), 2, logits=False)
+    with pytest.raises(RuntimeError, match="context exhausted"):
+        m.forward(1)
+
+
+# ----------------------------------------------------------------- planted mistakes
+
+MUTATIONS = {
+    "rope_unfused": ("b[i] = fmaf(x0, c, -(x1 * s));", "b[i] = x0 * c - x1 * s;"),
+    "q4q8_unfused": ("sum = fmaf(p, (float)dot_q4_q8_block(blk, aq + 32 * b), sum);",
+                     "sum = sum + p * (float)dot_q4_q8_block(blk, aq + 32 * b);"),
+    "quant_round_even": ("long r = lroundf(z[k] * inv);", "long r = lrintf(z[k] * inv);"),
+    "fp16_carry_added": ("return (uint16_t)(sign | ((uint32_t)exp << 10) | ((mant + 0x1000u) >> 13));",
+                         "return (uint16_t)(sign | (((uint32_t)exp << 10) + ((mant + 0x1000u) >> 13)));"),
+    "q8_lane_order": ("for (int j = 0; j < 8; ++j) t[j] = fmaf((float)qs[k + j], x[b * 32 + k + j], t[j]);",
+                      "for (int j = 0; j < 8; ++j) t[j] = fmaf((float)qs[k + j], x[b * 32 + k + j], t[(j + k / 8) & 7]);"),
+    "batch4_unrounded_scale": ("float q = (float)qi * d;\n                    size_t off = b * 32 + h * 16 + k + j;",
+                               "float q = (float)qi;\n                    size_t off = b * 32 + h * 16 + k + j;"),
+}
+
+
+def _mutant(tmp, name):
+    src = open(os.path.join(ROOT, "oracle", "mv_oracle.c")).read()
+    a, b = MUTATIONS[name]
+    assert a in src, f"mutation anchor missing: {name}"
+    d = os.path.join(tmp, name)
+    os.makedirs(d)
+    shutil.copy(os.path.join(ROOT, "oracle", "mv_oracle.h"), d)
+    with open(os.path.join(d, "mv_oracle.c"), "w") as f:
+        f.write(src.replace(a, b))
+    so = os.path.join(d, "lib.so")
+    subprocess.run(["gcc", "-std=gnu11", "-O2", "-mavx2", "-mfma", "-mf16c", "-ffp-contract=off", "-fopenmp", "-fPIC",
+                    "-shared", "-o", so, os.path.join(d, "mv_oracle.c"), "-lm"], check=True)
+    from oracle.pyoracle import Oracle
+
+    return Oracle(so)
+
+
+def _golden_ok(o, mats, tiny_model):
+    g = golden("kernels.npz")
+    try:
+        for name, (w, rows, cols, ty, key) in mats.items():
+            assert_bitexact(o.matvec(w, ty, rows, cols, g[f"{key}__x"]), g[f"{key}__matvec"])
+            for B in (5, 32):
+                if f"{key}__v06_x{B}" in g:
+                    X = g[f"{key}__v06_x{B}"]
+                    assert_bitexact(o.matmul_batch_v06(w, ty, rows, cols, X, ".ffn_" in name, False),
+                                    g[f"{key}__v06_ref{B}"])
+        for i in range(g["probe__x"].shape[0]):
+            assert_bitexact(o.matvec(g["probe__w"], synth.Q4_0, 256, 256, g["probe__x"][i]), g["probe__y"][i])
+        f16 = golden("fp16.npz")
+        assert np.array_equal(o.fp32_to_fp16(f16["bits"].view(np.float32)), f16["half"])
+        gm = golden("model_tiny.npz")
+        m = o.model(tiny_model, ctx=256)
+        assert_bitexact(m.prefill(gm["prompt"], 32), gm["prefill_logits_m0"])
+        m.close()
+    except AssertionError:
+        return False
+    return True
+
+
+@pytest.mark.parametrize("name", sorted(MUTATIONS))
+def test_planted_mistake_is_caught(name, mats, tiny_model):
+    with tempfile.TemporaryDirectory() as tmp:
+        assert not _golden_ok(_mutant(tmp, name), mats, tiny_model), f"golden checks miss mutation {name}"
