@@ -29,6 +29,8 @@
  *                         LlamaModel::forward      src/llama_model.cpp:256
  *   mvh_tensor_upload     GgufFile::tensor_data    include/memvanta/gguf.hpp:57, src/gguf.cpp:139
  *                         (the bytes it returns are copied to HBM once)
+ *   mvh_model_*           LlamaModel               include/memvanta/llama_model.hpp:100-138,
+ *                                                  src/llama_model.cpp:222-262 (device resident)
  */
 #ifndef MEMVANTA_HIP_H
 #define MEMVANTA_HIP_H
@@ -67,6 +69,7 @@ extern "C" {
 typedef struct mvh_context mvh_context;
 typedef struct mvh_tensor mvh_tensor;
 typedef struct mvh_kv_cache mvh_kv_cache;
+typedef struct mvh_model mvh_model;
 
 /* ---- library / context ---- */
 const char* mvh_last_error(void);
@@ -125,6 +128,25 @@ int mvh_kv_read_row(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, size
 /* decode attention of one layer over positions 0..pos: q[n_head*hd] -> out[n_head*hd] */
 int mvh_attn_decode(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos,
                     size_t n_head, size_t n_head_kv, size_t head_dim, float* out, int ptr_kind);
+
+/* ---- whole model: LlamaModel on one device (weights, paged F16 KV and activations in HBM) ---- */
+/* act_mode selects the prefill numerics (MVH_ACT_REF / MVH_ACT_Q8); max_batch bounds the prefill chunk */
+int mvh_model_open(const char* gguf_path, int device, size_t ctx_override, size_t kv_page_tokens, int act_mode,
+                   size_t max_batch, mvh_model** out);
+int mvh_model_close(mvh_model* m);
+/* n_ctx, n_embd, n_ff, n_layer, n_head, n_head_kv, vocab */
+int mvh_model_config(const mvh_model* m, size_t out[7]);
+int mvh_model_reset(mvh_model* m);
+/* LlamaModel::forward: one decode step; logits (host, vocab floats) may be NULL */
+int mvh_model_forward(mvh_model* m, int token, float* logits);
+/* LlamaModel::prefill: chunks of `batch`; logits of the last token when logits != NULL */
+int mvh_model_prefill(mvh_model* m, const int* tokens, size_t n, size_t batch, float* logits);
+/* n greedy decode steps from `token`, run on the device from one HIP graph (the argmax of each step
+ * feeds the next); out_tokens (host) receives the n sampled ids, last_logits (host) may be NULL */
+int mvh_model_generate_greedy(mvh_model* m, int token, size_t n, int* out_tokens, float* last_logits);
+int mvh_model_position(const mvh_model* m, size_t* pos);
+int mvh_model_kv_bytes(const mvh_model* m, size_t* bytes);
+int mvh_model_stream(mvh_model* m, void** stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ LIB = os.path.join(HERE, "libmemvanta_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: every FMA in the kernels is written out, nothing else fuses.
 # -packed-fp32-ops off: no v_pk_*_f32 in the generated code.
-HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-shared", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
@@ -30,9 +30,10 @@ def _run(cmd, cwd=ROOT):
 
 
 def build_hip(verbose: bool = False) -> str:
-    srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip"))) + sorted(glob.glob(os.path.join(HERE, "host", "*.cpp")))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(HERE, 'csrc')}", "-o", tmp, *srcs]
+    cmd = [HIPCC, *HIP_FLAGS, f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(HERE, 'csrc')}",
+           f"-I{os.path.join(HERE, 'host')}", "-o", tmp, "-x", "hip", *srcs]
     out = _run(cmd)
     os.replace(tmp, LIB)
     if verbose and out.strip():

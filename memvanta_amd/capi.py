@@ -65,6 +65,16 @@ _SIGS = {
     "mvh_kv_write": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
     "mvh_kv_read_row": (_int, [_vp, _vp, _sz, _sz, _int, _vp]),
     "mvh_attn_decode": (_int, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _vp, _int]),
+    "mvh_model_open": (_int, [C.c_char_p, _int, _sz, _sz, _int, _sz, C.POINTER(_vp)]),
+    "mvh_model_close": (_int, [_vp]),
+    "mvh_model_config": (_int, [_vp, C.POINTER(_sz)]),
+    "mvh_model_reset": (_int, [_vp]),
+    "mvh_model_forward": (_int, [_vp, _int, _vp]),
+    "mvh_model_prefill": (_int, [_vp, _vp, _sz, _sz, _vp]),
+    "mvh_model_generate_greedy": (_int, [_vp, _int, _sz, _vp, _vp]),
+    "mvh_model_position": (_int, [_vp, C.POINTER(_sz)]),
+    "mvh_model_kv_bytes": (_int, [_vp, C.POINTER(_sz)]),
+    "mvh_model_stream": (_int, [_vp, C.POINTER(_vp)]),
 }
 
 _lib = None
@@ -291,3 +301,67 @@ class KVCache:
         self.ctx._check(self.ctx.lib.mvh_attn_decode(self.ctx.h, self.h, layer, _ptr(q), pos, n_head, n_head_kv,
                                                      head_dim, _ptr(out), _kind(q, out)))
         return out
+
+
+class Model:
+    """LlamaModel on one device (mvh_model_*)."""
+
+    def __init__(self, path: str, device: int = 0, ctx: int = 0, page_tokens: int = 128,
+                 act_mode: int = MVH_ACT_Q8, max_batch: int = 64):
+        self.lib = load_library()
+        h = _vp()
+        rc = self.lib.mvh_model_open(path.encode(), device, ctx, page_tokens, act_mode, max_batch, C.byref(h))
+        self._check(rc)
+        self.h = h.value
+        cfg = (_sz * 7)()
+        self._check(self.lib.mvh_model_config(self.h, cfg))
+        self.n_ctx, self.n_embd, self.n_ff, self.n_layer, self.n_head, self.n_head_kv, self.vocab = list(cfg)
+
+    def _check(self, rc):
+        if rc != 0:
+            raise MvhError(rc, self.lib.mvh_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.mvh_model_close(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def reset(self):
+        self._check(self.lib.mvh_model_reset(self.h))
+
+    def forward(self, token: int, logits: bool = True):
+        out = np.empty(self.vocab, np.float32) if logits else None
+        self._check(self.lib.mvh_model_forward(self.h, int(token), out.ctypes.data if logits else None))
+        return out
+
+    def prefill(self, tokens, batch: int = 32, logits: bool = True):
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.vocab, np.float32) if logits else None
+        self._check(self.lib.mvh_model_prefill(self.h, t.ctypes.data, t.size, batch, out.ctypes.data if logits else None))
+        return out
+
+    def generate_greedy(self, token: int, n: int, logits: bool = False):
+        ids = np.empty(n, np.int32)
+        out = np.empty(self.vocab, np.float32) if logits else None
+        self._check(self.lib.mvh_model_generate_greedy(self.h, int(token), n, ids.ctypes.data,
+                                                       out.ctypes.data if logits else None))
+        return (ids, out) if logits else ids
+
+    @property
+    def position(self) -> int:
+        p = _sz()
+        self._check(self.lib.mvh_model_position(self.h, C.byref(p)))
+        return p.value
+
+    def kv_bytes(self) -> int:
+        p = _sz()
+        self._check(self.lib.mvh_model_kv_bytes(self.h, C.byref(p)))
+        return p.value
+
+    @property
+    def stream(self) -> int:
+        s = _vp()
+        self._check(self.lib.mvh_model_stream(self.h, C.byref(s)))
+        return s.value

@@ -4,6 +4,8 @@
 // positions [p*page_tokens, (p+1)*page_tokens) as [slot][kv_dim] fp16, K and V
 // in separate arrays -- the PagedKVCache layout of src/llama_model.cpp:18-22.
 #include "mvh_kernels.hpp"
+#define MVH_EXPF_QUAL __device__ __forceinline__
+#include "mvh_expf.h"
 
 namespace mvh {
 namespace {
@@ -23,20 +25,27 @@ __global__ __launch_bounds__(256) void kv_write_kernel(uint16_t* const* __restri
     pt_v[p / page_tokens][off] = f2h_ref(v[i]);
 }
 
-// Scores of one head against positions 0..pos (dot_key, src/llama_model.cpp:
-// 23-39, divided by sqrtf(hd) as at :256): lane e of 8 accumulates
-// fma(q[d], k[d]) for d = e, e+8, ...; sum = t0+t1+..+t7; the tail beyond a
-// multiple of 8 is fma-accumulated into the sum.  blockIdx.x = head.
+// Scores of query token b (grid z) and head h (grid x) against positions
+// 0..upto, upto = pos + b (dot_key, src/llama_model.cpp:23-39, divided by
+// sqrtf(hd) as at :248/:256): lane e of 8 accumulates fma(q[d], k[d]) for
+// d = e, e+8, ...; sum = t0+t1+..+t7; a tail beyond a multiple of 8 is
+// fma-accumulated into the sum.  pos comes from *d_pos when d_pos != null, so
+// the launch (sized for the largest position) can be replayed from a graph.
 __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* __restrict__ pt_k,
                                                          const float* __restrict__ q, float* __restrict__ scores,
-                                                         int pos, int group, int hd, int kv_dim, int page_tokens,
+                                                         const int* __restrict__ d_pos, int pos_arg, int n_head,
+                                                         int group, int hd, int kv_dim, int page_tokens,
                                                          int score_pitch) {
     extern __shared__ float s_q[];
-    const int h = blockIdx.x;
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) s_q[i] = q[static_cast<size_t>(h) * hd + i];
+    const int h = blockIdx.x, b = blockIdx.z;
+    const int upto = (d_pos ? *d_pos : pos_arg) + b;
+    const int t0 = blockIdx.y * blockDim.x;
+    if (t0 > upto) return;  // whole block past the causal limit
+    const float* qh = q + (static_cast<size_t>(b) * n_head + h) * hd;
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) s_q[i] = qh[i];
     __syncthreads();
-    const int t = blockIdx.y * blockDim.x + threadIdx.x;
-    if (t > pos) return;
+    const int t = t0 + threadIdx.x;
+    if (t > upto) return;
     const int kh = h / group;
     const uint16_t* krow = pt_k[t / page_tokens] + static_cast<size_t>(t % page_tokens) * kv_dim + kh * hd;
     float acc[8];
@@ -53,7 +62,7 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* 
 #pragma unroll
     for (int e = 1; e < 8; ++e) sum = sum + acc[e];
     for (; c < hd; ++c) sum = fmaf(s_q[c], h2f(krow[c]), sum);
-    scores[static_cast<size_t>(h) * score_pitch + t] = __fdiv_rn(sum, __fsqrt_rn(static_cast<float>(hd)));
+    scores[(static_cast<size_t>(b) * n_head + h) * score_pitch + t] = __fdiv_rn(sum, __fsqrt_rn(static_cast<float>(hd)));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -62,25 +71,27 @@ __device__ __forceinline__ float wave_max(float v) {
                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
 }
 
-// Softmax and the value sum (src/llama_model.cpp:256): mx = max s, e = expf(s-mx),
-// den = sum of e in double, inv = float(1/den), out[d] = fma(e_t*inv, V_t[d], out[d])
-// over t in order.  One wave per (head, 64-wide slice of head_dim); the value
-// chain of each output element runs in t order in its own lane, as in the
-// reference.  The double `den` is added as a tree instead of in t order.
+// Softmax and the value sum (src/llama_model.cpp:248,256): mx = max s,
+// e = expf(s-mx), den = sum of e in double, inv = float(1/den),
+// out[d] = fma(e_t*inv, V_t[d], out[d]) over t in order.  One wave per
+// (head, 64-wide slice of head_dim, query token); every output element's
+// value chain runs in t order in its own lane, as in the reference.  The
+// double `den` is added as a tree instead of in t order.
 __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* const* __restrict__ pt_v,
                                                             const float* __restrict__ scores, float* __restrict__ out,
-                                                            int pos, int group, int hd, int kv_dim, int page_tokens,
+                                                            const int* __restrict__ d_pos, int pos_arg, int n_head,
+                                                            int group, int hd, int kv_dim, int page_tokens,
                                                             int score_pitch) {
     extern __shared__ float s_a[];
-    const int h = blockIdx.x;
-    const float* sc = scores + static_cast<size_t>(h) * score_pitch;
-    const int n = pos + 1;
+    const int h = blockIdx.x, b = blockIdx.z;
+    const int n = (d_pos ? *d_pos : pos_arg) + b + 1;
+    const float* sc = scores + (static_cast<size_t>(b) * n_head + h) * score_pitch;
     float mx = -INFINITY;
     for (int t = threadIdx.x; t < n; t += 64) mx = fmaxf(mx, sc[t]);
     mx = wave_max(mx);
     double den = 0.0;
     for (int t = threadIdx.x; t < n; t += 64) {
-        const float e = expf(sc[t] - mx);
+        const float e = mvh_expf(sc[t] - mx);
         s_a[t] = e;
         den += static_cast<double>(e);
     }
@@ -106,7 +117,7 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* cons
         }
         for (; i < m; ++i) acc = fmaf(s_a[p0 + i], h2f(vp[static_cast<size_t>(i) * kv_dim]), acc);
     }
-    out[static_cast<size_t>(h) * hd + d] = acc;
+    out[(static_cast<size_t>(b) * n_head + h) * hd + d] = acc;
 }
 
 }  // namespace
@@ -121,22 +132,32 @@ hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const f
     return hipGetLastError();
 }
 
+hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
+                       float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
+                       size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st) {
+    if (!B) return hipSuccess;
+    const int group = static_cast<int>(n_head / n_head_kv);
+    const int pitch = static_cast<int>(max_pos);  // scores row pitch >= last position + 1
+    const dim3 g1(static_cast<unsigned>(n_head), static_cast<unsigned>((max_pos + 63) / 64), static_cast<unsigned>(B));
+    attn_scores_kernel<<<g1, 64, hd * sizeof(float), st>>>(pt_k, q, scores, d_pos, static_cast<int>(pos),
+                                                           static_cast<int>(n_head), group, static_cast<int>(hd),
+                                                           static_cast<int>(kv_dim), static_cast<int>(page_tokens),
+                                                           pitch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 g2(static_cast<unsigned>(n_head), static_cast<unsigned>((hd + 63) / 64), static_cast<unsigned>(B));
+    attn_softmax_v_kernel<<<g2, 64, max_pos * sizeof(float), st>>>(pt_v, scores, out, d_pos, static_cast<int>(pos),
+                                                                    static_cast<int>(n_head), group,
+                                                                    static_cast<int>(hd), static_cast<int>(kv_dim),
+                                                                    static_cast<int>(page_tokens), pitch);
+    return hipGetLastError();
+}
+
 hipError_t launch_attn_decode(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
                               float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim,
                               size_t page_tokens, hipStream_t st) {
-    const int group = static_cast<int>(n_head / n_head_kv);
-    const int pitch = static_cast<int>(pos + 1);
-    const dim3 g1(static_cast<unsigned>(n_head), static_cast<unsigned>((pos + 1 + 63) / 64));
-    attn_scores_kernel<<<g1, 64, hd * sizeof(float), st>>>(pt_k, q, scores, static_cast<int>(pos), group,
-                                                           static_cast<int>(hd), static_cast<int>(kv_dim),
-                                                           static_cast<int>(page_tokens), pitch);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const dim3 g2(static_cast<unsigned>(n_head), static_cast<unsigned>((hd + 63) / 64));
-    attn_softmax_v_kernel<<<g2, 64, (pos + 1) * sizeof(float), st>>>(pt_v, scores, out, static_cast<int>(pos), group,
-                                                                     static_cast<int>(hd), static_cast<int>(kv_dim),
-                                                                     static_cast<int>(page_tokens), pitch);
-    return hipGetLastError();
+    return launch_attn(pt_k, pt_v, q, scores, out, nullptr, pos, pos + 1, 1, n_head, n_head_kv, hd, kv_dim,
+                       page_tokens, st);
 }
 
 }  // namespace mvh

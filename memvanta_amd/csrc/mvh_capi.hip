@@ -4,6 +4,7 @@
 // (src/gguf_kernels.cpp:244-271); all arithmetic runs in the gfx950 kernels.
 #include "memvanta_hip.h"
 #include "mvh_kernels.hpp"
+#include "llama_model.hpp"
 
 #include <algorithm>
 #include <cstdarg>
@@ -664,6 +665,111 @@ int mvh_attn_decode(mvh_context* c, const mvh_kv_cache* kv, size_t layer, const 
                                     static_cast<float*>(c->scratch.p), od, pos, n_head, n_head_kv, head_dim,
                                     kv->kv_dim, kv->page_tokens, c->stream));
     return finish_out(c, out, od, qn * 4, kind);
+}
+
+}  // extern "C"
+
+namespace {
+using ModelT = memvanta::hip::LlamaModel;
+ModelT* M(mvh_model* m) { return reinterpret_cast<ModelT*>(m); }
+const ModelT* M(const mvh_model* m) { return reinterpret_cast<const ModelT*>(m); }
+template <class F>
+int guarded(F&& f) {
+    try {
+        f();
+        return MVH_OK;
+    } catch (const std::exception& e) {
+        const std::string w = e.what();
+        const int code = w.find("out of range") != std::string::npos || w.find("exhausted") != std::string::npos
+                             ? MVH_E_RANGE
+                             : w.find("hip") != std::string::npos ? MVH_E_DEVICE : MVH_E_INVALID;
+        return fail(code, "%s", w.c_str());
+    }
+}
+}  // namespace
+
+extern "C" {
+
+int mvh_model_open(const char* path, int device, size_t ctx_override, size_t page_tokens, int act_mode,
+                   size_t max_batch, mvh_model** out) {
+    if (!path || !out) return fail(MVH_E_INVALID, "null argument");
+    *out = nullptr;
+    if (act_mode != MVH_ACT_REF && act_mode != MVH_ACT_Q8) return fail(MVH_E_INVALID, "bad act_mode %d", act_mode);
+    return guarded([&] {
+        auto mode = act_mode == MVH_ACT_Q8 ? memvanta::hip::PrefillMode::Q8 : memvanta::hip::PrefillMode::Reference;
+        *out = reinterpret_cast<mvh_model*>(new ModelT(path, device, ctx_override, page_tokens, mode, max_batch));
+    });
+}
+
+int mvh_model_close(mvh_model* m) {
+    delete M(m);
+    return MVH_OK;
+}
+
+int mvh_model_config(const mvh_model* m, size_t out[7]) {
+    if (!m || !out) return fail(MVH_E_INVALID, "null argument");
+    const auto& c = M(m)->config();
+    out[0] = c.n_ctx;
+    out[1] = c.n_embd;
+    out[2] = c.n_ff;
+    out[3] = c.n_layer;
+    out[4] = c.n_head;
+    out[5] = c.n_head_kv;
+    out[6] = c.vocab;
+    return MVH_OK;
+}
+
+int mvh_model_reset(mvh_model* m) {
+    if (!m) return fail(MVH_E_INVALID, "null model");
+    M(m)->reset();
+    return MVH_OK;
+}
+
+int mvh_model_forward(mvh_model* m, int token, float* logits) {
+    if (!m) return fail(MVH_E_INVALID, "null model");
+    return guarded([&] {
+        const auto& l = M(m)->forward(token, logits != nullptr);
+        if (logits) std::memcpy(logits, l.data(), l.size() * sizeof(float));
+    });
+}
+
+int mvh_model_prefill(mvh_model* m, const int* tokens, size_t n, size_t batch, float* logits) {
+    if (!m || (!tokens && n)) return fail(MVH_E_INVALID, "null argument");
+    return guarded([&] {
+        std::vector<int> t(tokens, tokens + n);
+        const auto& l = M(m)->prefill(t, batch, logits != nullptr);
+        if (logits && n) std::memcpy(logits, l.data(), l.size() * sizeof(float));
+    });
+}
+
+int mvh_model_generate_greedy(mvh_model* m, int token, size_t n, int* out_tokens, float* last_logits) {
+    if (!m || (!out_tokens && n)) return fail(MVH_E_INVALID, "null argument");
+    return guarded([&] {
+        const auto ids = M(m)->generate_greedy(token, n);
+        std::memcpy(out_tokens, ids.data(), n * sizeof(int));
+        if (last_logits && n) {
+            const auto& l = M(m)->logits();
+            std::memcpy(last_logits, l.data(), l.size() * sizeof(float));
+        }
+    });
+}
+
+int mvh_model_position(const mvh_model* m, size_t* pos) {
+    if (!m || !pos) return fail(MVH_E_INVALID, "null argument");
+    *pos = M(m)->position();
+    return MVH_OK;
+}
+
+int mvh_model_kv_bytes(const mvh_model* m, size_t* bytes) {
+    if (!m || !bytes) return fail(MVH_E_INVALID, "null argument");
+    *bytes = M(m)->kv_bytes_allocated();
+    return MVH_OK;
+}
+
+int mvh_model_stream(mvh_model* m, void** stream) {
+    if (!m || !stream) return fail(MVH_E_INVALID, "null argument");
+    *stream = M(m)->stream();
+    return MVH_OK;
 }
 
 }  // extern "C"

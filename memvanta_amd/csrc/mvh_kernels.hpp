@@ -38,9 +38,26 @@ hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x,
 // ---- paged F16 KV + decode attention (mvh_attn.hip) ----
 hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
                            size_t n_tokens, size_t kv_dim, size_t page_tokens, hipStream_t st);
+// B query tokens at positions pos..pos+B-1 (pos = *d_pos when d_pos != null),
+// causal; scores needs B * n_head * max_pos floats, max_pos > last position
+hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
+                       float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
+                       size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st);
 // scores needs n_head * (pos+1) floats of scratch
 hipError_t launch_attn_decode(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
                               float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim,
                               size_t page_tokens, hipStream_t st);
+
+// ---- model step pieces (mvh_model.hip) ----
+hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int* tokens, size_t B, float* out,
+                        hipStream_t st);
+// x += add (if add), n = rmsnorm(x)*w, and q/qd = Q8 of n (if q); B rows of D
+hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
+                          size_t D, float eps, hipStream_t st);
+hipError_t launch_rope_kv(float* q, float* k, const float* v, const float* cos_t, const float* sin_t, const int* d_pos,
+                          size_t pos0, size_t B, size_t n_head, size_t n_kv, size_t hd, uint16_t* const* pt_k,
+                          uint16_t* const* pt_v, size_t page_tokens, hipStream_t st);
+hipError_t launch_swiglu(const float* g, const float* u, float* ff, int8_t* q, float* qd, size_t n, hipStream_t st);
+hipError_t launch_argmax(const float* logits, size_t V, size_t B, int* out, int* d_pos, int* hist, hipStream_t st);
 
 }  // namespace mvh

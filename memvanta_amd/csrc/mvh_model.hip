@@ -1,0 +1,248 @@
+// mvh_model.hip -- the element-wise pieces of LlamaModel's decode and
+// prefill steps (src/llama_model.cpp:237-259), kept on the device so a whole
+// step runs without host round trips.  Positions and token ids can be read
+// from device memory, so one captured HIP graph serves every decode step.
+#include "mvh_kernels.hpp"
+#define MVH_EXPF_QUAL __device__ __forceinline__
+#include "mvh_expf.h"
+
+namespace mvh {
+
+// One element of row `row` of a GGUF tensor, dequantized the way
+// tensor_read_row_f32 does it (src/gguf_kernels.cpp:226).
+__device__ __forceinline__ float dequant_elem(uint32_t type, const uint8_t* W, int cols, size_t row, int i) {
+    if (type == kF32) return reinterpret_cast<const float*>(W)[row * cols + i];
+    if (type == kF16) return h2f(reinterpret_cast<const uint16_t*>(W)[row * cols + i]);
+    if (type == kQ4_0) {
+        const uint8_t* b = W + (row * (cols / 32) + i / 32) * 18;
+        const int e = i & 31;
+        const uint32_t byte = b[2 + (e & 15)];
+        const int q = static_cast<int>(e < 16 ? (byte & 15u) : (byte >> 4)) - 8;
+        return h2f(b[0] | (static_cast<uint32_t>(b[1]) << 8)) * static_cast<float>(q);
+    }
+    if (type == kQ8_0) {
+        const uint8_t* b = W + (row * (cols / 32) + i / 32) * 34;
+        return h2f(b[0] | (static_cast<uint32_t>(b[1]) << 8)) * static_cast<float>(static_cast<int8_t>(b[2 + (i & 31)]));
+    }
+    const uint8_t* b = W + (row * (cols / 256) + i / 256) * 210;  // Q6_K
+    const int e = i & 255;
+    const int row32 = e / 32, j = e % 32, group = row32 / 4, local = row32 % 4;
+    const int lo = (b[group * 64 + (local % 2) * 32 + j] >> (local < 2 ? 0 : 4)) & 0x0f;
+    const int hi = (b[128 + group * 32 + j] >> (2 * local)) & 0x03;
+    const float d = h2f(b[208] | (static_cast<uint32_t>(b[209]) << 8));
+    return (d * static_cast<float>(static_cast<int8_t>(b[192 + e / 16]))) * static_cast<float>((lo | (hi << 4)) - 32);
+}
+
+namespace {
+
+// Embedding rows of B tokens (token ids in device memory).
+__global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t* __restrict__ W, int cols,
+                                                    const int* __restrict__ tokens, float* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= cols) return;
+    out[static_cast<size_t>(blockIdx.y) * cols + i] = dequant_elem(type, W, cols, static_cast<size_t>(tokens[blockIdx.y]), i);
+}
+
+// x += add (when add != null), then LlamaModel::rmsnorm (src/llama_model.cpp:237):
+// ss = sum of x*x in double, inv = 1/sqrtf(float(ss/D) + eps), n = (x*inv)*w;
+// optionally also the Q8 activation of n (quantize_q8, bit-exact).  One
+// workgroup per row; D % 32 == 0.  The double sum is added as a tree, not in
+// the reference's element order; the two can differ only when the exact sum
+// of squares lies within ~1e-15 (relative) of an f32 rounding boundary of ss/D.
+constexpr int kNormT = 256;
+__global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ add,
+                                                         const float* __restrict__ w, float* __restrict__ n,
+                                                         int8_t* __restrict__ q, float* __restrict__ qd, int D,
+                                                         float eps) {
+    __shared__ double red[kNormT / 64];
+    const size_t row = blockIdx.x;
+    float4* xr = reinterpret_cast<float4*>(x + row * D);
+    const float4* ar = add ? reinterpret_cast<const float4*>(add + row * D) : nullptr;
+    const int D4 = D / 4;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < D4; i += kNormT) {
+        float4 v = xr[i];
+        if (ar) {
+            const float4 a = ar[i];
+            v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+            xr[i] = v;
+        }
+        ss = fma(static_cast<double>(v.x), static_cast<double>(v.x), ss);
+        ss = fma(static_cast<double>(v.y), static_cast<double>(v.y), ss);
+        ss = fma(static_cast<double>(v.z), static_cast<double>(v.z), ss);
+        ss = fma(static_cast<double>(v.w), static_cast<double>(v.w), ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = red[0];
+#pragma unroll
+    for (int k = 1; k < kNormT / 64; ++k) ss += red[k];
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(ss / static_cast<double>(D)) + eps));
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4* nr = reinterpret_cast<float4*>(n + row * D);
+    for (int i = threadIdx.x; i < D4; i += kNormT) {  // D4 % 8 == 0: 8-lane groups are whole blocks
+        const float4 v = xr[i], g = w4[i];
+        const float4 o = make_float4((v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z, (v.w * inv) * g.w);
+        nr[i] = o;
+        if (q) {
+            float d;
+            int s;
+            const uint32_t packed = quantize_q8_x4(o, d, s);
+            reinterpret_cast<uint32_t*>(q + row * D)[i] = packed;
+            if ((i & 7) == 0) qd[row * (D / 32) + (i >> 3)] = d;
+        }
+    }
+}
+
+// RoPE (LlamaModel::rope_ptr, src/llama_model.cpp:238; half-split pairs,
+// GCC's contraction fma(x0,c,-(x1*s)) / fma(x0,s,x1*c)) on q and k of B
+// tokens at positions pos..pos+B-1, then PagedKVCache::write of k and v
+// through the reference's fp32_to_fp16 (:22).  One thread per (token, head, i).
+__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
+                                                      const float* __restrict__ v, const float* __restrict__ cos_t,
+                                                      const float* __restrict__ sin_t, const int* __restrict__ d_pos,
+                                                      int pos0, int B, int n_head, int n_kv, int hd,
+                                                      uint16_t* const* __restrict__ pt_k,
+                                                      uint16_t* const* __restrict__ pt_v, int page_tokens) {
+    const int half = hd / 2, heads = n_head + n_kv;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= B * heads * half) return;
+    const int b = idx / (heads * half), rem = idx - b * heads * half, h = rem / half, i = rem - h * half;
+    const int pos = (d_pos ? *d_pos : pos0) + b;
+    const float c = cos_t[static_cast<size_t>(pos) * half + i], s = sin_t[static_cast<size_t>(pos) * half + i];
+    const int D = n_head * hd, KV = n_kv * hd;
+    float* z = h < n_head ? q + static_cast<size_t>(b) * D + h * hd : k + static_cast<size_t>(b) * KV + (h - n_head) * hd;
+    const float x0 = z[i], x1 = z[i + half];
+    const float r0 = fmaf(x0, c, -(x1 * s)), r1 = fmaf(x0, s, x1 * c);
+    z[i] = r0;
+    z[i + half] = r1;
+    if (h >= n_head) {
+        const int kh = h - n_head;
+        const size_t off = static_cast<size_t>(pos % page_tokens) * KV + kh * hd;
+        uint16_t* kp = pt_k[pos / page_tokens] + off;
+        uint16_t* vp = pt_v[pos / page_tokens] + off;
+        const float* vv = v + static_cast<size_t>(b) * KV + kh * hd;
+        kp[i] = f2h_ref(r0);
+        kp[i + half] = f2h_ref(r1);
+        vp[i] = f2h_ref(vv[i]);
+        vp[i + half] = f2h_ref(vv[i + half]);
+    }
+}
+
+// SwiGLU (src/llama_model.cpp:249,257): ff = (g/(1+expf(-g)))*u, with expf as
+// the C library computes it; optionally the Q8 activation of ff.  n % 32 == 0.
+__global__ __launch_bounds__(256) void swiglu_kernel(const float4* __restrict__ g, const float4* __restrict__ u,
+                                                     float4* __restrict__ ff, uint32_t* __restrict__ q,
+                                                     float* __restrict__ qd, int n4) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = i < n4;  // n4 % 8 == 0: 8-lane groups are whole blocks
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) {
+        const float4 a = g[i], b = u[i];
+        auto f = [](float z, float up) { return __fdiv_rn(z, 1.0f + mvh_expf(-z)) * up; };
+        o = make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
+        ff[i] = o;
+    }
+    if (q) {
+        float d;
+        int s;
+        const uint32_t packed = quantize_q8_x4(o, d, s);
+        if (live) {
+            q[i] = packed;
+            if ((i & 7) == 0) qd[i >> 3] = d;
+        }
+    }
+}
+
+// Greedy sampling (Sampler, src/llama_model.cpp:60: first index of the max)
+// of each of B rows; writes token ids and, when d_pos != null, records the
+// token in hist[*d_pos] (if hist) and advances *d_pos.
+constexpr int kArgT = 1024;
+__global__ __launch_bounds__(kArgT) void argmax_kernel(const float* __restrict__ logits, int V, int* __restrict__ out,
+                                                       int* __restrict__ d_pos, int* __restrict__ hist) {
+    __shared__ float sv[kArgT / 64];
+    __shared__ int si[kArgT / 64];
+    const float* l = logits + static_cast<size_t>(blockIdx.x) * V;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += kArgT) {
+        const float v = l[i];
+        if (v > best || bi == 0x7fffffff) {  // indices increase: strict > keeps the first max
+            best = v;
+            bi = i;
+        }
+    }
+    auto better = [](float v, int i, float bv, int bj) { return v > bv || (v == bv && i < bj); };
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(best, m);
+        const int oi = __shfl_xor(bi, m);
+        if (better(ov, oi, best, bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kArgT / 64; ++k)
+            if (better(sv[k], si[k], best, bi)) {
+                best = sv[k];
+                bi = si[k];
+            }
+        out[blockIdx.x] = bi;
+        if (d_pos && blockIdx.x == 0) {  // decode loop: record the token at its position, advance
+            if (hist) hist[*d_pos] = bi;
+            *d_pos += 1;
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int* tokens, size_t B, float* out,
+                        hipStream_t st) {
+    if (!B) return hipSuccess;
+    embed_kernel<<<dim3(static_cast<unsigned>((cols + 255) / 256), static_cast<unsigned>(B)), 256, 0, st>>>(
+        type, W, static_cast<int>(cols), tokens, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
+                          size_t D, float eps, hipStream_t st) {
+    if (!B) return hipSuccess;
+    rmsnorm_kernel<<<static_cast<unsigned>(B), kNormT, 0, st>>>(x, add, w, n, q, qd, static_cast<int>(D), eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv(float* q, float* k, const float* v, const float* cos_t, const float* sin_t, const int* d_pos,
+                          size_t pos0, size_t B, size_t n_head, size_t n_kv, size_t hd, uint16_t* const* pt_k,
+                          uint16_t* const* pt_v, size_t page_tokens, hipStream_t st) {
+    const size_t n = B * (n_head + n_kv) * (hd / 2);
+    if (!n) return hipSuccess;
+    rope_kv_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(
+        q, k, v, cos_t, sin_t, d_pos, static_cast<int>(pos0), static_cast<int>(B), static_cast<int>(n_head),
+        static_cast<int>(n_kv), static_cast<int>(hd), pt_k, pt_v, static_cast<int>(page_tokens));
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* g, const float* u, float* ff, int8_t* q, float* qd, size_t n, hipStream_t st) {
+    const size_t n4 = n / 4;
+    if (!n4) return hipSuccess;
+    swiglu_kernel<<<static_cast<unsigned>((n4 + 255) / 256), 256, 0, st>>>(
+        reinterpret_cast<const float4*>(g), reinterpret_cast<const float4*>(u), reinterpret_cast<float4*>(ff),
+        reinterpret_cast<uint32_t*>(q), qd, static_cast<int>(n4));
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, size_t V, size_t B, int* out, int* d_pos, int* hist, hipStream_t st) {
+    if (!B) return hipSuccess;
+    argmax_kernel<<<static_cast<unsigned>(B), kArgT, 0, st>>>(logits, static_cast<int>(V), out, d_pos, hist);
+    return hipGetLastError();
+}
+
+}  // namespace mvh

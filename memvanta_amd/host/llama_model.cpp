@@ -1,0 +1,443 @@
+// llama_model.cpp -- device-resident LlamaModel (see llama_model.hpp).
+// Step structure and numerics follow src/llama_model.cpp:222-262 of the
+// reference: decode uses tensor_matvec numerics (Q4_0 with Q8 activations),
+// prefill chunks use tensor_matmul_batch_v06 numerics in the chosen mode.
+#include "llama_model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+#include "gguf.hpp"
+#include "mvh_kernels.hpp"
+
+namespace memvanta {
+namespace hip {
+namespace {
+
+bool is_ffn(const std::string& n) {
+    return n.find(".ffn_gate.") != std::string::npos || n.find(".ffn_up.") != std::string::npos ||
+           n.find(".ffn_down.") != std::string::npos;
+}
+
+float fp16_to_fp32_host(std::uint16_t h) {
+    const std::uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 0x1fu;
+    std::uint32_t f = h & 0x3ffu, out;
+    if (e == 0) {
+        if (f == 0) {
+            out = s << 31;
+        } else {
+            std::uint32_t ee = 113;
+            while ((f & 0x400u) == 0) {
+                f <<= 1;
+                --ee;
+            }
+            out = (s << 31) | (ee << 23) | ((f & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        out = (s << 31) | 0x7f800000u | (f << 13);
+    } else {
+        out = (s << 31) | ((e + 112u) << 23) | (f << 13);
+    }
+    float r;
+    std::memcpy(&r, &out, 4);
+    return r;
+}
+
+}  // namespace
+
+void LlamaModel::check(hipError_t e, const char* what) const {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_override, std::size_t kv_page_tokens,
+                       PrefillMode mode, std::size_t max_batch)
+    : file_(std::make_unique<GgufFile>(path)), device_(device), mode_(mode),
+      page_tokens_(kv_page_tokens ? kv_page_tokens : 128), max_batch_(std::max<std::size_t>(1, max_batch)) {
+    const auto arch = file_->get_string("general.architecture").value_or("");
+    if (arch != "llama")
+        throw std::runtime_error("MemVanta real-model path currently supports GGUF architecture=llama, got: " + arch);
+    auto req = [&](const char* k) {
+        auto v = file_->get_u64(k);
+        if (!v) throw std::runtime_error(std::string("missing GGUF metadata: ") + k);
+        return static_cast<std::size_t>(*v);
+    };
+    c_.n_ctx = req("llama.context_length");
+    c_.n_embd = req("llama.embedding_length");
+    c_.n_ff = req("llama.feed_forward_length");
+    c_.n_layer = req("llama.block_count");
+    c_.n_head = req("llama.attention.head_count");
+    c_.n_head_kv = static_cast<std::size_t>(file_->get_u64("llama.attention.head_count_kv").value_or(c_.n_head));
+    c_.rms_eps = static_cast<float>(file_->get_f64("llama.attention.layer_norm_rms_epsilon").value_or(1e-5));
+    c_.rope_theta = static_cast<float>(file_->get_f64("llama.rope.freq_base").value_or(10000.0));
+    const auto& te = file_->tensor("token_embd.weight");
+    c_.vocab = static_cast<std::size_t>(te.ne(1));
+    if (te.ne(0) != c_.n_embd) throw std::runtime_error("token embedding shape mismatch");
+    if (ctx_override) c_.n_ctx = std::min(c_.n_ctx, ctx_override);
+    if (c_.n_embd % c_.n_head || !c_.n_head_kv || c_.n_head % c_.n_head_kv)
+        throw std::runtime_error("invalid Llama head configuration");
+    if (c_.n_embd % 32 || c_.n_ff % 32 || c_.head_dim() % 8)
+        throw std::runtime_error("device path needs n_embd, n_ff % 32 == 0 and head_dim % 8 == 0");
+
+    check(hipSetDevice(device_), "hipSetDevice");
+    check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    auto dalloc = [&](std::size_t bytes) {
+        void* p = nullptr;
+        check(hipMalloc(&p, std::max<std::size_t>(bytes, 16)), "hipMalloc");
+        allocs_.push_back(p);
+        return p;
+    };
+
+    upload(embd_, "token_embd.weight");
+    if (file_->has_tensor("output.weight")) upload(out_, "output.weight");
+    else out_ = embd_;  // tied output (src/llama_model.cpp:228)
+    out_norm_ = upload_vector("output_norm.weight");
+    layers_.resize(c_.n_layer);
+    for (std::size_t i = 0; i < c_.n_layer; ++i) {
+        auto n = [&](const char* s) { return "blk." + std::to_string(i) + s; };
+        auto& L = layers_[i];
+        L.attn_norm = upload_vector(n(".attn_norm.weight"));
+        upload(L.q, n(".attn_q.weight"));
+        upload(L.k, n(".attn_k.weight"));
+        upload(L.v, n(".attn_v.weight"));
+        upload(L.o, n(".attn_output.weight"));
+        L.ffn_norm = upload_vector(n(".ffn_norm.weight"));
+        upload(L.gate, n(".ffn_gate.weight"));
+        upload(L.up, n(".ffn_up.weight"));
+        upload(L.down, n(".ffn_down.weight"));
+    }
+
+    // RoPE table computed on the host with the C library, as the reference
+    // does (src/llama_model.cpp:233), then uploaded
+    const std::size_t hd = c_.head_dim(), half = hd / 2;
+    std::vector<float> co(c_.n_ctx * half), si(c_.n_ctx * half);
+    for (std::size_t p = 0; p < c_.n_ctx; ++p)
+        for (std::size_t i = 0; i < half; ++i) {
+            const float inv = std::pow(c_.rope_theta, -2.0f * static_cast<float>(i) / static_cast<float>(hd));
+            const float a = static_cast<float>(p) * inv;
+            co[p * half + i] = std::cos(a);
+            si[p * half + i] = std::sin(a);
+        }
+    rope_cos_ = static_cast<float*>(dalloc(co.size() * 4));
+    rope_sin_ = static_cast<float*>(dalloc(si.size() * 4));
+    check(hipMemcpy(rope_cos_, co.data(), co.size() * 4, hipMemcpyHostToDevice), "upload rope");
+    check(hipMemcpy(rope_sin_, si.data(), si.size() * 4, hipMemcpyHostToDevice), "upload rope");
+
+    // paged F16 KV cache: the pages of every layer preallocated in HBM,
+    // addressed through per-layer page tables
+    max_pages_ = (c_.n_ctx + page_tokens_ - 1) / page_tokens_;
+    const std::size_t page_elems = page_tokens_ * c_.kv_dim();
+    auto* kslab = static_cast<uint16_t*>(dalloc(c_.n_layer * max_pages_ * page_elems * 2));
+    auto* vslab = static_cast<uint16_t*>(dalloc(c_.n_layer * max_pages_ * page_elems * 2));
+    std::vector<uint16_t*> tk(c_.n_layer * max_pages_), tv(c_.n_layer * max_pages_);
+    for (std::size_t i = 0; i < tk.size(); ++i) {
+        tk[i] = kslab + i * page_elems;
+        tv[i] = vslab + i * page_elems;
+    }
+    pt_k_ = static_cast<uint16_t**>(dalloc(tk.size() * sizeof(uint16_t*)));
+    pt_v_ = static_cast<uint16_t**>(dalloc(tv.size() * sizeof(uint16_t*)));
+    check(hipMemcpy(pt_k_, tk.data(), tk.size() * sizeof(uint16_t*), hipMemcpyHostToDevice), "page table");
+    check(hipMemcpy(pt_v_, tv.data(), tv.size() * sizeof(uint16_t*), hipMemcpyHostToDevice), "page table");
+
+    const std::size_t B = max_batch_, D = c_.n_embd, F = c_.n_ff, KV = c_.kv_dim(), W = std::max(D, F);
+    x_ = static_cast<float*>(dalloc(B * D * 4));
+    n_ = static_cast<float*>(dalloc(B * D * 4));
+    q_ = static_cast<float*>(dalloc(B * D * 4));
+    k_ = static_cast<float*>(dalloc(B * KV * 4));
+    v_ = static_cast<float*>(dalloc(B * KV * 4));
+    att_ = static_cast<float*>(dalloc(B * D * 4));
+    proj_ = static_cast<float*>(dalloc(B * D * 4));
+    g_ = static_cast<float*>(dalloc(B * F * 4));
+    u_ = static_cast<float*>(dalloc(B * F * 4));
+    ff_ = static_cast<float*>(dalloc(B * F * 4));
+    scores_ = static_cast<float*>(dalloc(B * c_.n_head * c_.n_ctx * 4));
+    logits_d_ = static_cast<float*>(dalloc(c_.vocab * 4));
+    q8_ = static_cast<int8_t*>(dalloc(B * W));
+    q8d_ = static_cast<float*>(dalloc(B * (W / 32) * 4));
+    d_tok_ = static_cast<int*>(dalloc(16));
+    d_hist_ = static_cast<int*>(dalloc(4 * (c_.n_ctx + 1)));
+    d_pos_ = static_cast<int*>(dalloc(16));
+    d_toks_ = static_cast<int*>(dalloc(B * 4));
+    ffo_ = static_cast<float*>(dalloc(B * D * 4));
+    q8s_ = static_cast<int8_t*>(dalloc(B * W));
+    q8sd_ = static_cast<float*>(dalloc(B * (W / 32) * 4));
+    q8ss_ = static_cast<int*>(dalloc(B * (W / 32) * 4));
+    check(hipHostMalloc(reinterpret_cast<void**>(&pin_), 4 * (c_.n_ctx + B + 8), hipHostMallocDefault),
+          "hipHostMalloc");
+    logits_.resize(c_.vocab);
+    reset();
+}
+
+LlamaModel::~LlamaModel() {
+    (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (graph_) (void)hipGraphExecDestroy(graph_);
+    for (void* p : allocs_) (void)hipFree(p);
+    if (pin_) (void)hipHostFree(pin_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void LlamaModel::upload(Tensor& t, const std::string& name) {
+    const auto& g = file_->tensor(name);
+    if (g.dims.size() < 2) throw std::runtime_error("matvec requires rank-2 tensor: " + name);
+    t.sname = name;
+    t.type = g.type;
+    t.cols = static_cast<std::size_t>(g.ne(0));
+    t.rows = static_cast<std::size_t>(g.ne(1));
+    if (t.type != 2 && t.type != 8 && t.type != 14)
+        throw std::runtime_error(std::string("unsupported device tensor type ") + type_name(t.type) + ": " + name);
+    if (!g.nbytes) throw std::runtime_error("bad tensor size: " + name);
+    check(hipMalloc(&t.d, g.nbytes), "hipMalloc tensor");
+    allocs_.push_back(t.d);
+    check(hipMemcpy(t.d, file_->tensor_data(g), g.nbytes, hipMemcpyHostToDevice), "tensor upload");
+}
+
+float* LlamaModel::upload_vector(const std::string& name) {
+    const auto& g = file_->tensor(name);
+    if (g.elements() != c_.n_embd) throw std::runtime_error("tensor vector size mismatch: " + name);
+    std::vector<float> h(c_.n_embd);
+    const std::byte* p = file_->tensor_data(g);
+    if (g.type == 0) {
+        std::memcpy(h.data(), p, h.size() * 4);
+    } else if (g.type == 1) {
+        for (std::size_t i = 0; i < h.size(); ++i) {
+            std::uint16_t v;
+            std::memcpy(&v, p + 2 * i, 2);
+            h[i] = fp16_to_fp32_host(v);
+        }
+    } else {
+        throw std::runtime_error(std::string("unsupported vector tensor type ") + type_name(g.type) + ": " + name);
+    }
+    void* d = nullptr;
+    check(hipMalloc(&d, h.size() * 4), "hipMalloc");
+    allocs_.push_back(d);
+    check(hipMemcpy(d, h.data(), h.size() * 4, hipMemcpyHostToDevice), "vector upload");
+    return static_cast<float*>(d);
+}
+
+// tensor_matvec numerics (src/gguf_kernels.cpp:244-253)
+void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y) {
+    const auto* W = static_cast<const uint8_t*>(w.d);
+    hipError_t e;
+    switch (w.type) {
+        case 2:
+            if (q8) {
+                e = mvh::launch_gemv_q4_0(W, q8, q8d, y, w.rows, w.cols, stream_);
+            } else if (mvh::gemv_q4_0_persistent_ok(w.cols)) {
+                e = mvh::launch_gemv_q4_0_persistent(W, x, nullptr, nullptr, y, w.rows, w.cols, stream_);
+            } else {
+                e = mvh::launch_quantize_q8(x, q8s_, q8sd_, q8ss_, 1, w.cols, stream_);
+                if (e == hipSuccess) e = mvh::launch_gemv_q4_0(W, q8s_, q8sd_, y, w.rows, w.cols, stream_);
+            }
+            break;
+        case 8: e = mvh::launch_gemv_q8_0(W, x, y, w.rows, w.cols, 1, stream_); break;
+        default: e = mvh::launch_gemv_q6_k(W, x, y, w.rows, w.cols, 1, stream_); break;
+    }
+    check(e, w.sname.c_str());
+}
+
+// tensor_matmul_batch_v06 numerics (src/gguf_kernels.cpp:261-271) over B rows
+void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B) {
+    const auto* W = static_cast<const uint8_t*>(w.d);
+    const std::size_t rows = w.rows, cols = w.cols, nb = cols / 32;
+    hipError_t e = hipSuccess;
+    if (B < 2 || (w.type != 2 && w.type != 8) || cols % 32) {  // tensor_matmul_batch: fp32 per token
+        if (w.type == 2) e = mvh::launch_gemv_q4_0_f32act(W, x, y, rows, cols, B, stream_);
+        else if (w.type == 8) e = mvh::launch_gemv_q8_0(W, x, y, rows, cols, B, stream_);
+        else e = mvh::launch_gemv_q6_k(W, x, y, rows, cols, B, stream_);
+    } else if (mode_ == PrefillMode::Q8) {
+        if (w.type == 2) {
+            if (!q8) {
+                e = mvh::launch_quantize_q8(x, q8s_, q8sd_, q8ss_, B, cols, stream_);
+                q8 = q8s_;
+                q8d = q8sd_;
+            }
+            for (std::size_t b = 0; b < B && e == hipSuccess; ++b)
+                e = mvh::launch_gemv_q4_0(W, q8 + b * cols, q8d + b * nb, y + b * rows, rows, cols, stream_);
+        } else {
+            e = mvh::launch_gemv_q8_0(W, x, y, rows, cols, B, stream_);
+        }
+    } else {
+        const std::size_t step = is_ffn(w.sname) ? 8 : 4, blocked = B / step * step;
+        e = mvh::launch_batch4_f32act(w.type, W, x, y, rows, cols, blocked, stream_);
+        if (e == hipSuccess && blocked < B) {
+            if (w.type == 2)
+                e = mvh::launch_gemv_q4_0_f32act(W, x + blocked * cols, y + blocked * rows, rows, cols, B - blocked,
+                                                 stream_);
+            else
+                e = mvh::launch_gemv_q8_0(W, x + blocked * cols, y + blocked * rows, rows, cols, B - blocked, stream_);
+        }
+    }
+    check(e, w.sname.c_str());
+}
+
+// One decode step (LlamaModel::forward, src/llama_model.cpp:253-259) for the
+// token in *d_token at position *d_pos_.
+void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
+    const std::size_t D = c_.n_embd, F = c_.n_ff, hd = c_.head_dim();
+    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_token, 1, x_, stream_), "embed");
+    for (std::size_t li = 0; li < c_.n_layer; ++li) {
+        auto& L = layers_[li];
+        const bool q8_in = L.q.type == 2 || L.k.type == 2 || L.v.type == 2;
+        check(mvh::launch_rmsnorm(x_, li ? ffo_ : nullptr, L.attn_norm, n_, q8_in ? q8_ : nullptr, q8d_, 1, D,
+                                  c_.rms_eps, stream_),
+              "rmsnorm");
+        gemv(L.q, n_, L.q.type == 2 ? q8_ : nullptr, q8d_, q_);
+        gemv(L.k, n_, L.k.type == 2 ? q8_ : nullptr, q8d_, k_);
+        gemv(L.v, n_, L.v.type == 2 ? q8_ : nullptr, q8d_, v_);
+        uint16_t* const* pk = pt_k_ + li * max_pages_;
+        uint16_t* const* pv = pt_v_ + li * max_pages_;
+        check(mvh::launch_rope_kv(q_, k_, v_, rope_cos_, rope_sin_, d_pos_, 0, 1, c_.n_head, c_.n_head_kv, hd, pk, pv,
+                                  page_tokens_, stream_),
+              "rope/kv");
+        check(mvh::launch_attn(pk, pv, q_, scores_, att_, d_pos_, 0, c_.n_ctx, 1, c_.n_head, c_.n_head_kv, hd,
+                               c_.kv_dim(), page_tokens_, stream_),
+              "attention");
+        gemv(L.o, att_, nullptr, nullptr, proj_);
+        const bool q8_ffn = L.gate.type == 2 || L.up.type == 2;
+        check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8_ffn ? q8_ : nullptr, q8d_, 1, D, c_.rms_eps, stream_),
+              "rmsnorm");
+        gemv(L.gate, n_, L.gate.type == 2 ? q8_ : nullptr, q8d_, g_);
+        gemv(L.up, n_, L.up.type == 2 ? q8_ : nullptr, q8d_, u_);
+        check(mvh::launch_swiglu(g_, u_, ff_, L.down.type == 2 ? q8_ : nullptr, q8d_, F, stream_), "swiglu");
+        gemv(L.down, ff_, L.down.type == 2 ? q8_ : nullptr, q8d_, ffo_);
+    }
+    if (logits || argmax) {
+        check(mvh::launch_rmsnorm(x_, ffo_, out_norm_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, 1, D, c_.rms_eps,
+                                  stream_),
+              "rmsnorm");
+        gemv(out_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, logits_d_);
+    }
+    if (argmax) check(mvh::launch_argmax(logits_d_, c_.vocab, 1, d_tok_, d_pos_, d_hist_, stream_), "argmax");
+}
+
+// One prefill chunk (LlamaModel::forward_batch_impl, src/llama_model.cpp:240-252).
+void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
+    const std::size_t D = c_.n_embd, F = c_.n_ff, hd = c_.head_dim(), KV = c_.kv_dim();
+    (void)KV;
+    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_tokens, B, x_, stream_), "embed");
+    const bool q8mode = mode_ == PrefillMode::Q8 && B >= 2;
+    for (std::size_t li = 0; li < c_.n_layer; ++li) {
+        auto& L = layers_[li];
+        check(mvh::launch_rmsnorm(x_, li ? ffo_ : nullptr, L.attn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D,
+                                  c_.rms_eps, stream_),
+              "rmsnorm");
+        gemm(L.q, n_, q8mode ? q8_ : nullptr, q8d_, q_, B);
+        gemm(L.k, n_, q8mode ? q8_ : nullptr, q8d_, k_, B);
+        gemm(L.v, n_, q8mode ? q8_ : nullptr, q8d_, v_, B);
+        uint16_t* const* pk = pt_k_ + li * max_pages_;
+        uint16_t* const* pv = pt_v_ + li * max_pages_;
+        check(mvh::launch_rope_kv(q_, k_, v_, rope_cos_, rope_sin_, nullptr, pos_, B, c_.n_head, c_.n_head_kv, hd, pk,
+                                  pv, page_tokens_, stream_),
+              "rope/kv");
+        check(mvh::launch_attn(pk, pv, q_, scores_, att_, nullptr, pos_, pos_ + B, B, c_.n_head, c_.n_head_kv, hd,
+                               c_.kv_dim(), page_tokens_, stream_),
+              "attention");
+        gemm(L.o, att_, nullptr, nullptr, proj_, B);
+        check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D, c_.rms_eps, stream_),
+              "rmsnorm");
+        gemm(L.gate, n_, q8mode ? q8_ : nullptr, q8d_, g_, B);
+        gemm(L.up, n_, q8mode ? q8_ : nullptr, q8d_, u_, B);
+        check(mvh::launch_swiglu(g_, u_, ff_, q8mode ? q8_ : nullptr, q8d_, B * F, stream_), "swiglu");
+        gemm(L.down, ff_, q8mode ? q8_ : nullptr, q8d_, ffo_, B);
+    }
+    if (logits) {
+        float* xl = x_ + (B - 1) * D;
+        check(mvh::launch_rmsnorm(xl, ffo_ + (B - 1) * D, out_norm_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, 1, D,
+                                  c_.rms_eps, stream_),
+              "rmsnorm");
+        gemv(out_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, logits_d_);
+    }
+}
+
+void LlamaModel::reset() {
+    pos_ = 0;
+    kv_hi_ = 0;
+}
+
+std::size_t LlamaModel::kv_bytes_allocated() const {
+    // pages are allocated lazily in the reference (PagedKVCache::ensure):
+    // every page any written position touched, in every layer
+    const std::size_t pages = (kv_hi_ + page_tokens_ - 1) / page_tokens_;
+    return c_.n_layer * pages * 2 * page_tokens_ * c_.kv_dim() * sizeof(uint16_t);
+}
+
+const std::vector<float>& LlamaModel::logits() {
+    check(hipMemcpyAsync(logits_.data(), logits_d_, c_.vocab * 4, hipMemcpyDeviceToHost, stream_), "logits copy");
+    check(hipStreamSynchronize(stream_), "sync");
+    return logits_;
+}
+
+const std::vector<float>& LlamaModel::forward(int token, bool compute_logits) {
+    if (token < 0 || static_cast<std::size_t>(token) >= c_.vocab) throw std::runtime_error("token id out of range");
+    if (pos_ >= c_.n_ctx) throw std::runtime_error("context exhausted");
+    check(hipSetDevice(device_), "hipSetDevice");
+    pin_[0] = token;
+    pin_[1] = static_cast<int>(pos_);
+    check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, stream_), "token upload");
+    check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, stream_), "pos upload");
+    decode_step(d_tok_, compute_logits, false);
+    ++pos_;
+    kv_hi_ = std::max(kv_hi_, pos_);
+    if (compute_logits) return logits();
+    check(hipStreamSynchronize(stream_), "sync");
+    return logits_;
+}
+
+const std::vector<float>& LlamaModel::prefill(const std::vector<int>& tokens, std::size_t batch_size,
+                                              bool compute_logits_last) {
+    if (tokens.empty()) return logits_;
+    batch_size = std::max<std::size_t>(1, batch_size);
+    if (batch_size > max_batch_) throw std::runtime_error("prefill batch larger than the model's max_batch");
+    check(hipSetDevice(device_), "hipSetDevice");
+    for (std::size_t i = 0; i < tokens.size(); i += batch_size) {
+        const std::size_t B = std::min(batch_size, tokens.size() - i);
+        if (pos_ + B > c_.n_ctx) throw std::runtime_error("context exhausted");
+        for (std::size_t b = 0; b < B; ++b)
+            if (tokens[i + b] < 0 || static_cast<std::size_t>(tokens[i + b]) >= c_.vocab)
+                throw std::runtime_error("token id out of range");
+        const bool last = compute_logits_last && i + B == tokens.size();
+        std::memcpy(pin_, tokens.data() + i, B * 4);
+        check(hipMemcpyAsync(d_toks_, pin_, B * 4, hipMemcpyHostToDevice, stream_), "token upload");
+        batch_step(d_toks_, B, last);
+        check(hipStreamSynchronize(stream_), "sync");  // pin_ is reused by the next chunk
+        pos_ += B;
+        kv_hi_ = std::max(kv_hi_, pos_);
+        if (last) logits();
+    }
+    return logits_;
+}
+
+std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
+    if (token < 0 || static_cast<std::size_t>(token) >= c_.vocab) throw std::runtime_error("token id out of range");
+    if (pos_ + n > c_.n_ctx) throw std::runtime_error("context exhausted");
+    std::vector<int> out(n);
+    if (!n) return out;
+    check(hipSetDevice(device_), "hipSetDevice");
+    pin_[0] = token;
+    pin_[1] = static_cast<int>(pos_);
+    check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, stream_), "token upload");
+    check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, stream_), "pos upload");
+    if (!graph_) {
+        // the step reads token and position from device memory and its argmax
+        // writes the next token and advances the position: one graph serves
+        // every step
+        hipGraph_t g{};
+        check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+        decode_step(d_tok_, true, true);
+        check(hipStreamEndCapture(stream_, &g), "end capture");
+        check(hipGraphInstantiate(&graph_, g, nullptr, nullptr, 0), "graph instantiate");
+        (void)hipGraphDestroy(g);
+    }
+    for (std::size_t i = 0; i < n; ++i) check(hipGraphLaunch(graph_, stream_), "graph launch");
+    check(hipMemcpyAsync(pin_, d_hist_ + pos_, n * 4, hipMemcpyDeviceToHost, stream_), "token copy");
+    check(hipStreamSynchronize(stream_), "sync");
+    std::memcpy(out.data(), pin_, n * 4);
+    pos_ += n;
+    kv_hi_ = std::max(kv_hi_, pos_);
+    return out;
+}
+
+}  // namespace hip
+}  // namespace memvanta

@@ -1,0 +1,99 @@
+// llama_model.hpp -- device-resident Llama decode/prefill with the public
+// surface of MemVanta's LlamaModel (include/memvanta/llama_model.hpp:100-138):
+// construct from a GGUF path, reset(), forward(token), prefill(tokens, batch,
+// logits_last), position(), kv_bytes_allocated().  Numerics follow the
+// reference step for step (src/llama_model.cpp:222-262); the F16 paged KV
+// cache lives in HBM.  generate_greedy() runs the decode loop from a captured
+// HIP graph, the greedy token of each step feeding the next on the device.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace memvanta {
+namespace hip {
+
+class GgufFile;
+
+struct LlamaConfig {
+    std::size_t n_ctx{}, n_embd{}, n_ff{}, n_layer{}, n_head{}, n_head_kv{}, vocab{};
+    float rms_eps{1e-5f}, rope_theta{10000.0f};
+    std::size_t head_dim() const { return n_embd / n_head; }
+    std::size_t kv_dim() const { return n_head_kv * head_dim(); }
+};
+
+// numerics of the batched prefill matmuls (tensor_matmul_batch_v06)
+enum class PrefillMode { Reference = 0, Q8 = 1 };  // Q8 = MEMVANTA_FORCE_Q8_ACT=1
+
+class LlamaModel {
+public:
+    LlamaModel(const std::string& gguf_path, int device = 0, std::size_t ctx_override = 0,
+               std::size_t kv_page_tokens = 128, PrefillMode mode = PrefillMode::Q8, std::size_t max_batch = 64);
+    ~LlamaModel();
+    LlamaModel(const LlamaModel&) = delete;
+    LlamaModel& operator=(const LlamaModel&) = delete;
+
+    const LlamaConfig& config() const { return c_; }
+    void reset();
+    const std::vector<float>& forward(int token, bool compute_logits = true);
+    const std::vector<float>& prefill(const std::vector<int>& tokens, std::size_t batch_size = 64,
+                                      bool compute_logits_last = true);
+    // n greedy steps starting from `token`; returns the n sampled ids
+    std::vector<int> generate_greedy(int token, std::size_t n);
+    std::size_t position() const { return pos_; }
+    std::size_t kv_bytes_allocated() const;
+    hipStream_t stream() const { return stream_; }
+    const std::vector<float>& logits();  // copies the device logits of the last step
+
+private:
+    struct Tensor {
+        std::string sname;
+        std::uint32_t type{};
+        std::size_t rows{}, cols{};
+        void* d{};
+    };
+    struct Layer {
+        Tensor q, k, v, o, gate, up, down;
+        float *attn_norm{}, *ffn_norm{};
+    };
+
+    void upload(Tensor& t, const std::string& name);
+    float* upload_vector(const std::string& name);
+    void gemv(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y);
+    void gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B);
+    void decode_step(const int* d_token, bool logits, bool argmax);
+    void batch_step(const int* tokens, std::size_t B, bool logits);
+    void check(hipError_t e, const char* what) const;
+
+    std::unique_ptr<GgufFile> file_;
+    LlamaConfig c_;
+    int device_{};
+    hipStream_t stream_{};
+    PrefillMode mode_;
+    std::size_t page_tokens_{}, max_pages_{}, max_batch_{}, pos_{}, kv_hi_{};
+    Tensor embd_, out_;
+    float* out_norm_{};
+    std::vector<Layer> layers_;
+    std::vector<void*> allocs_;
+    // paged F16 KV: one slab per layer and kind, page tables per layer
+    uint16_t** pt_k_{};
+    uint16_t** pt_v_{};
+    float *rope_cos_{}, *rope_sin_{};
+    // activations ([max_batch][...] for prefill; row 0 for decode)
+    float *x_{}, *n_{}, *q_{}, *k_{}, *v_{}, *att_{}, *proj_{}, *g_{}, *u_{}, *ff_{}, *logits_d_{}, *scores_{};
+    float* ffo_{};       // down-projection output (the residual added by the next norm)
+    int8_t *q8_{}, *q8s_{};
+    float *q8d_{}, *q8sd_{};
+    int* q8ss_{};        // block sums written by the stand-alone quantizer
+    int *d_tok_{}, *d_pos_{}, *d_toks_{}, *d_hist_{};  // d_hist_[p] = greedy token sampled at position p
+    int* pin_{};         // pinned host staging
+    std::vector<float> logits_;
+    hipGraphExec_t graph_{};
+};
+
+}  // namespace hip
+}  // namespace memvanta

@@ -287,7 +287,10 @@ class ModelConfig:
 TINY = ModelConfig("tiny-llama-288", 288, 768, 6, 6, 6, 32000, 256, Q4_0, Q8_0, Q8_0)
 TINYLLAMA_MIXED = ModelConfig("tinyllama-1.1b-mixed", 2048, 5632, 22, 32, 4, 32000, 2048, Q8_0, Q8_0, Q6_K, Q6_K)
 LLAMA7B = ModelConfig("openllama-7b-v2-q4_0", 4096, 11008, 32, 32, 32, 32000, 2048, Q4_0, Q4_0, Q6_K)
-CONFIGS = {c.name: c for c in (TINY, TINYLLAMA_MIXED, LLAMA7B)}
+# reduced-depth variants of the two large shapes, for end-to-end parity runs
+TINYLLAMA_MIXED_2L = dataclasses.replace(TINYLLAMA_MIXED, name="tinyllama-1.1b-mixed-2layer", layers=2, ctx=256)
+LLAMA7B_1L = dataclasses.replace(LLAMA7B, name="openllama-7b-v2-q4_0-1layer", layers=1, ctx=256)
+CONFIGS = {c.name: c for c in (TINY, TINYLLAMA_MIXED, LLAMA7B, TINYLLAMA_MIXED_2L, LLAMA7B_1L)}
 
 
 def write_model(cfg: ModelConfig, path: str, seed: int = 1234, std: float = 0.02) -> str:
