@@ -16,8 +16,10 @@ LIB = os.path.join(HERE, "libmemvanta_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: every FMA in the kernels is written out, nothing else fuses.
 # -packed-fp32-ops off: no v_pk_*_f32 in the generated code.
+# -fhip-fp32-correctly-rounded-divide-sqrt (hipcc's default, stated): f32 `/`
+# and __builtin_sqrtf round to nearest even, as the reference's do.
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-shared", "-ffp-contract=off",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+             "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
 def _run(cmd, cwd=ROOT):

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* 
 #pragma unroll
     for (int e = 1; e < 8; ++e) sum = sum + acc[e];
     for (; c < hd; ++c) sum = fmaf(s_q[c], h2f(krow[c]), sum);
-    scores[(static_cast<size_t>(b) * n_head + h) * score_pitch + t] = __fdiv_rn(sum, __fsqrt_rn(static_cast<float>(hd)));
+    scores[(static_cast<size_t>(b) * n_head + h) * score_pitch + t] = __fdiv_rn(sum, sqrt_rn(static_cast<float>(hd)));
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -38,6 +38,15 @@ __device__ __forceinline__ uint16_t f2h_ref(float f) {
     return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | ((mant + 0x1000u) >> 13));
 }
 
+// ---- correctly rounded sqrt ---------------------------------------------------
+
+// sqrtf rounded to nearest even.  HIP's __fsqrt_rn is the native v_sqrt_f32
+// (within 1 ulp) unless OCML_BASIC_ROUNDED_OPERATIONS is defined; the
+// llvm.sqrt.f32 lowering behind __builtin_sqrtf is correctly rounded under
+// hipcc's default -fhip-fp32-correctly-rounded-divide-sqrt (checked equal to
+// the host's sqrtf on every positive normal float on gfx950).
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
 // ---- cross-lane --------------------------------------------------------------
 
 // ds_swizzle in bit-mask mode (offset[15]=0): lane' = ((lane & and) | or) ^ xor

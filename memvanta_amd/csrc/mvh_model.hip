@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
     ss = red[0];
 #pragma unroll
     for (int k = 1; k < kNormT / 64; ++k) ss += red[k];
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(ss / static_cast<double>(D)) + eps));
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(static_cast<float>(ss / static_cast<double>(D)) + eps));
     const float4* w4 = reinterpret_cast<const float4*>(w);
     float4* nr = reinterpret_cast<float4*>(n + row * D);
     for (int i = threadIdx.x; i < D4; i += kNormT) {  // D4 % 8 == 0: 8-lane groups are whole blocks
