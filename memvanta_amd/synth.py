@@ -118,6 +118,59 @@ def quantize_q6_k(x: np.ndarray) -> np.ndarray:
     return out.reshape(rows, -1)
 
 
+def quantize_torch(ty: int, x):
+    """The same quantizers on a torch float32 [rows, cols] tensor, on any device
+    (byte-identical to the numpy ones for the same input); returns uint8
+    [rows, row_bytes] on x's device.  Used to synthesize multi-GB models fast."""
+    import torch
+
+    rows, cols = x.shape
+    u8 = torch.uint8
+    if ty == Q4_0:
+        b = x.reshape(rows, cols // 32, 32)
+        v = b.gather(2, b.abs().argmax(dim=2, keepdim=True))[..., 0]
+        d = v / -8.0
+        inv = torch.where(d != 0, 1.0 / d, torch.zeros_like(d))
+        q = torch.clamp_max((b * inv[..., None] + 8.5).to(torch.int8), 15).to(u8)
+        out = torch.empty((rows, cols // 32, 18), dtype=u8, device=x.device)
+        out[..., 0:2] = d.to(torch.float16).view(u8).reshape(rows, cols // 32, 2)
+        out[..., 2:18] = q[..., :16] | (q[..., 16:] << 4)
+        return out.reshape(rows, -1)
+    if ty == Q8_0:
+        b = x.reshape(rows, cols // 32, 32)
+        d = b.abs().amax(dim=2) / 127.0
+        inv = torch.where(d != 0, 1.0 / d, torch.zeros_like(d))
+        q = torch.clamp(torch.round(b * inv[..., None]), -127, 127).to(torch.int8)
+        out = torch.empty((rows, cols // 32, 34), dtype=u8, device=x.device)
+        out[..., 0:2] = d.to(torch.float16).view(u8).reshape(rows, cols // 32, 2)
+        out[..., 2:34] = q.view(u8)
+        return out.reshape(rows, -1)
+    if ty == Q6_K:
+        nsb = cols // 256
+        b = x.reshape(rows * nsb, 16, 16)
+        scale = b.abs().amax(dim=2) / 31.0
+        d16 = (scale.amax(dim=1) / 127.0).to(torch.float16)
+        df = d16.float()[:, None]
+        sc = torch.where(df != 0, torch.round(scale / df), torch.zeros_like(scale))
+        sc = torch.clamp(sc, -128, 127).to(torch.int8)
+        eff = (df * sc.float())[..., None]
+        q = torch.where(eff != 0, torch.round(b / eff), torch.zeros_like(b))
+        q = (torch.clamp(q, -32, 31) + 32).to(u8).reshape(-1, 256)
+        lo, hi = q & 15, q >> 4
+        ql = torch.as_tensor(_QL_SRC, device=x.device)
+        qh = torch.as_tensor(_QH_SRC, device=x.device)
+        out = torch.empty((rows * nsb, 210), dtype=u8, device=x.device)
+        out[:, 0:128] = lo[:, ql[:, 0]] | (lo[:, ql[:, 1]] << 4)
+        out[:, 128:192] = (hi[:, qh[:, 0]] | (hi[:, qh[:, 1]] << 2) | (hi[:, qh[:, 2]] << 4)
+                           | (hi[:, qh[:, 3]] << 6))
+        out[:, 192:208] = sc.view(u8)
+        out[:, 208:210] = d16.view(u8).reshape(-1, 2)
+        return out.reshape(rows, -1)
+    if ty == F32:
+        return x.contiguous().view(u8).reshape(rows, -1)
+    raise ValueError(f"unsupported type {ty}")
+
+
 def quantize(ty: int, x: np.ndarray) -> np.ndarray:
     if ty == Q4_0:
         return quantize_q4_0(x)
@@ -260,6 +313,22 @@ def normal_quantized(ty: int, rows: int, cols: int, rng: np.random.Generator, st
     return produce
 
 
+def normal_quantized_torch(ty: int, rows: int, cols: int, gen, std: float = 0.02, chunk_elems: int = 1 << 26):
+    """Producer of N(0, std) weights drawn and quantized on gen's device (a
+    torch.Generator); a different random stream from normal_quantized."""
+    import torch
+
+    chunk_rows = max(1, chunk_elems // cols)
+
+    def produce():
+        for r0 in range(0, rows, chunk_rows):
+            n = min(chunk_rows, rows - r0)
+            x = torch.randn((n, cols), generator=gen, device=gen.device, dtype=torch.float32) * std
+            yield quantize_torch(ty, x).cpu().numpy().tobytes()
+
+    return produce
+
+
 # --------------------------------------------------------------------------
 # model + matrix configurations
 # --------------------------------------------------------------------------
@@ -293,9 +362,19 @@ LLAMA7B_1L = dataclasses.replace(LLAMA7B, name="openllama-7b-v2-q4_0-1layer", la
 CONFIGS = {c.name: c for c in (TINY, TINYLLAMA_MIXED, LLAMA7B, TINYLLAMA_MIXED_2L, LLAMA7B_1L)}
 
 
-def write_model(cfg: ModelConfig, path: str, seed: int = 1234, std: float = 0.02) -> str:
-    """Random-init llama GGUF; returns the sha256 of the file."""
+def write_model(cfg: ModelConfig, path: str, seed: int = 1234, std: float = 0.02, device: str | None = None,
+                digest: bool = True) -> str | None:
+    """Random-init llama GGUF; returns the sha256 of the file (None when
+    digest=False).  With `device` (e.g. "cuda"), weights are drawn and
+    quantized there by torch: seconds for a 7B shape instead of minutes, but a
+    different random stream from the default numpy one."""
     rng = np.random.default_rng(seed)
+    gen = None
+    if device is not None:
+        import torch
+
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
     w = GgufWriter()
     w.add_str("general.architecture", "llama")
     w.add_str("general.name", cfg.name)
@@ -313,7 +392,9 @@ def write_model(cfg: ModelConfig, path: str, seed: int = 1234, std: float = 0.02
     D, F, kv = cfg.dim, cfg.ffn, cfg.kv_heads * cfg.head_dim
 
     def mat(name, rows, cols, ty):
-        w.add_tensor(name, (cols, rows), ty, rows * row_bytes(ty, cols), normal_quantized(ty, rows, cols, rng, std))
+        prod = (normal_quantized(ty, rows, cols, rng, std) if gen is None
+                else normal_quantized_torch(ty, rows, cols, gen, std))
+        w.add_tensor(name, (cols, rows), ty, rows * row_bytes(ty, cols), prod)
 
     def ones(name, n):
         w.add_tensor(name, (n,), F32, 4 * n, lambda: iter([np.ones(n, np.float32).tobytes()]))
@@ -332,7 +413,7 @@ def write_model(cfg: ModelConfig, path: str, seed: int = 1234, std: float = 0.02
     ones("output_norm.weight", D)
     mat("output.weight", cfg.vocab, D, cfg.out_type)
     w.write(path)
-    return file_sha256(path)
+    return file_sha256(path) if digest else None
 
 
 def write_matrices(path: str, mats: list[tuple[str, int, int, int]], seed: int = 7, std: float = 0.02) -> None:
