@@ -32,7 +32,8 @@ __global__ __launch_bounds__(256) void kv_write_kernel(uint16_t* const* __restri
 // fma-accumulated into the sum.  pos comes from *d_pos when d_pos != null, so
 // the launch (sized for the largest position) can be replayed from a graph.
 __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* __restrict__ pt_k,
-                                                         const float* __restrict__ q, float* __restrict__ scores,
+                                                         const float* __restrict__ q, int q_pitch,
+                                                         float* __restrict__ scores,
                                                          const int* __restrict__ d_pos, int pos_arg, int n_head,
                                                          int group, int hd, int kv_dim, int page_tokens,
                                                          int score_pitch) {
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* 
     const int upto = (d_pos ? *d_pos : pos_arg) + b;
     const int t0 = blockIdx.y * blockDim.x;
     if (t0 > upto) return;  // whole block past the causal limit
-    const float* qh = q + (static_cast<size_t>(b) * n_head + h) * hd;
+    const float* qh = q + static_cast<size_t>(b) * q_pitch + h * hd;
     for (int i = threadIdx.x; i < hd; i += blockDim.x) s_q[i] = qh[i];
     __syncthreads();
     const int t = t0 + threadIdx.x;
@@ -120,6 +121,190 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* cons
     out[(static_cast<size_t>(b) * n_head + h) * hd + d] = acc;
 }
 
+
+// ---- fused decode attention --------------------------------------------------
+//
+// One decode token, one launch.  Workgroup (head h, slice j) owns output
+// elements [j*SW, (j+1)*SW) of head h:
+//  1. RoPE of q (head h) and k (kv head h/group) at position p = *d_pos
+//     (LlamaModel::rope_ptr numerics), k and v rounded through the
+//     reference's fp32_to_fp16; the first workgroup of each kv head writes
+//     the K/V row of position p into its page; every workgroup keeps the
+//     rounded values of position p in LDS and uses them for t = p;
+//  2. s_t = dot_key(q, K_t) / sqrtf(hd) for t = 0..p (thread per position,
+//     lane-of-8 fma accumulation, t0+..+t7);
+//  3. mx, e_t = expf(s_t - mx), den = double sum, a_t = e_t * float(1/den);
+//  4. out[d] = fma(a_t, V_t[d], out[d]) for t = 0..p in order, one lane per
+//     output element, the V slice staged through LDS in rounds of kRV rows
+//     (the loads of round r+1 are in flight while round r is summed);
+//  5. with SW == 32 the slice is one Q8 block of the output: quantize_q8 of
+//     it (the o-projection's activation) is written beside it.
+// The scores are recomputed by every slice of a head (K is read from L2).
+constexpr int kAT = 256;
+constexpr int kRV = 512;  // V rows per staging round
+
+template <int SW>
+__global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int* __restrict__ d_pos,
+    uint16_t* const* __restrict__ pt_k, uint16_t* const* __restrict__ pt_v, int page_tokens,
+    float* __restrict__ out, int8_t* __restrict__ q8, float* __restrict__ q8d, int group, int hd, int kv_dim,
+    int ctx_pad, int nslice) {
+    constexpr int kCh = SW / 8;                          // 16-byte chunks per V row slice
+    constexpr int kVPT = (kRV * kCh + kAT - 1) / kAT;    // chunks per thread per round
+    extern __shared__ __align__(16) float sm[];
+    float* s_q = sm;
+    float* s_k = sm + hd;
+    float* s_v = sm + 2 * hd;
+    float* s_a = sm + 3 * hd;
+    uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_a + ctx_pad);  // [kRV][SW]
+    __shared__ float red_f[kAT / 64];
+    __shared__ double red_d[kAT / 64];
+
+    const int h = blockIdx.x / nslice, slice = blockIdx.x - h * nslice;
+    const int kh = h / group, t = threadIdx.x, half = hd >> 1;
+    const int pos = *d_pos;
+    const int dbase = slice * SW;
+    auto vsrc = [&](int row, int c) {
+        return reinterpret_cast<const uint4*>(pt_v[row / page_tokens] + static_cast<size_t>(row % page_tokens) * kv_dim +
+                                              kh * hd + dbase + c * 8);
+    };
+    // round 0 of the V slice goes out first
+    uint4 vr[kVPT];
+    auto load_round = [&](int r0) {
+        const int rows = min(kRV, pos - r0);
+#pragma unroll
+        for (int i = 0; i < kVPT; ++i) {
+            const int c = i * kAT + t;
+            if (c < rows * kCh) vr[i] = *vsrc(r0 + c / kCh, c % kCh);
+        }
+    };
+    if (pos > 0) load_round(0);
+
+    // 1. RoPE, K/V of the current position
+    {
+        const size_t off = static_cast<size_t>(pos % page_tokens) * kv_dim + kh * hd;
+        uint16_t* kc = pt_k[pos / page_tokens] + off;
+        uint16_t* vc = pt_v[pos / page_tokens] + off;
+        const bool writer = slice == 0 && h % group == 0;
+        const float* qh = q + static_cast<size_t>(h) * hd;
+        const float* kk = k + static_cast<size_t>(kh) * hd;
+        const float* vv = v + static_cast<size_t>(kh) * hd;
+        for (int i = t; i < half; i += kAT) {
+            const float c = cos_t[static_cast<size_t>(pos) * half + i], s = sin_t[static_cast<size_t>(pos) * half + i];
+            const float q0 = qh[i], q1 = qh[i + half], k0 = kk[i], k1 = kk[i + half];
+            s_q[i] = fmaf(q0, c, -(q1 * s));
+            s_q[i + half] = fmaf(q0, s, q1 * c);
+            const uint16_t hk0 = f2h_ref(fmaf(k0, c, -(k1 * s))), hk1 = f2h_ref(fmaf(k0, s, k1 * c));
+            const uint16_t hv0 = f2h_ref(vv[i]), hv1 = f2h_ref(vv[i + half]);
+            s_k[i] = h2f(hk0);
+            s_k[i + half] = h2f(hk1);
+            s_v[i] = h2f(hv0);
+            s_v[i + half] = h2f(hv1);
+            if (writer) {
+                kc[i] = hk0;
+                kc[i + half] = hk1;
+                vc[i] = hv0;
+                vc[i + half] = hv1;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. scores
+    const float scale = sqrt_rn(static_cast<float>(hd));
+    float mx = -INFINITY;
+    for (int tt = t; tt <= pos; tt += kAT) {
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+        if (tt == pos) {
+            for (int c = 0; c < hd; c += 8) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] = fmaf(s_q[c + e], s_k[c + e], acc[e]);
+            }
+        } else {
+            const uint16_t* krow = pt_k[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
+            for (int c = 0; c < hd; c += 8) {
+                const uint4 kv8 = *reinterpret_cast<const uint4*>(krow + c);
+                const uint32_t w[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    acc[e] = fmaf(s_q[c + e], h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
+            }
+        }
+        float sum = acc[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) sum = sum + acc[e];
+        const float sc = __fdiv_rn(sum, scale);
+        s_a[tt] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red_f[t >> 6] = mx;
+    __syncthreads();
+    mx = red_f[0];
+#pragma unroll
+    for (int w = 1; w < kAT / 64; ++w) mx = fmaxf(mx, red_f[w]);
+
+    // 3. softmax weights
+    double den = 0.0;
+    for (int tt = t; tt <= pos; tt += kAT) {
+        const float e = mvh_expf(s_a[tt] - mx);
+        s_a[tt] = e;
+        den += static_cast<double>(e);
+    }
+    den = wave_sum(den);
+    if ((t & 63) == 0) red_d[t >> 6] = den;
+    __syncthreads();
+    den = red_d[0];
+#pragma unroll
+    for (int w = 1; w < kAT / 64; ++w) den += red_d[w];
+    const float inv = static_cast<float>(1.0 / den);
+    for (int tt = t; tt <= pos; tt += kAT) s_a[tt] = s_a[tt] * inv;
+
+    // 4. value chain over t = 0..pos in order
+    float acc = 0.0f;
+    for (int r0 = 0; r0 < pos; r0 += kRV) {
+        const int rows = min(kRV, pos - r0);
+#pragma unroll
+        for (int i = 0; i < kVPT; ++i) {
+            const int c = i * kAT + t;
+            if (c < rows * kCh) reinterpret_cast<uint4*>(s_vt)[c] = vr[i];
+        }
+        __syncthreads();  // also orders the s_a writes above before their reads
+        if (r0 + kRV < pos) load_round(r0 + kRV);
+        if (t < SW) {
+            int j = 0;
+            for (; j + 8 <= rows; j += 8) {
+                float vv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vv[e] = h2f(s_vt[(j + e) * SW + t]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = fmaf(s_a[r0 + j + e], vv[e], acc);
+            }
+            for (; j < rows; ++j) acc = fmaf(s_a[r0 + j], h2f(s_vt[j * SW + t]), acc);
+        }
+        __syncthreads();
+    }
+    if (pos == 0) __syncthreads();  // s_a writes before the read below
+    if (t < SW) {
+        acc = fmaf(s_a[pos], s_v[dbase + t], acc);
+        const size_t o = static_cast<size_t>(h) * hd + dbase + t;
+        out[o] = acc;
+        if constexpr (SW == 32) {
+            if (q8) {  // quantize_q8 of this 32-element block of the output
+                const float m = group_max<32>(fabsf(acc));
+                const float d = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+                const float id = __fdiv_rn(1.0f, d);
+                const float rq = fminf(fmaxf(roundf(acc * id), -127.0f), 127.0f);
+                q8[o] = static_cast<int8_t>(rq);
+                if (t == 0) q8d[o / 32] = d;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
@@ -132,14 +317,15 @@ hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const f
     return hipGetLastError();
 }
 
-hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
-                       float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
-                       size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st) {
+hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, size_t q_pitch,
+                       float* scores, float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B,
+                       size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st) {
     if (!B) return hipSuccess;
     const int group = static_cast<int>(n_head / n_head_kv);
     const int pitch = static_cast<int>(max_pos);  // scores row pitch >= last position + 1
     const dim3 g1(static_cast<unsigned>(n_head), static_cast<unsigned>((max_pos + 63) / 64), static_cast<unsigned>(B));
-    attn_scores_kernel<<<g1, 64, hd * sizeof(float), st>>>(pt_k, q, scores, d_pos, static_cast<int>(pos),
+    attn_scores_kernel<<<g1, 64, hd * sizeof(float), st>>>(pt_k, q, static_cast<int>(q_pitch), scores, d_pos,
+                                                           static_cast<int>(pos),
                                                            static_cast<int>(n_head), group, static_cast<int>(hd),
                                                            static_cast<int>(kv_dim), static_cast<int>(page_tokens),
                                                            pitch);
@@ -156,8 +342,36 @@ hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v,
 hipError_t launch_attn_decode(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
                               float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim,
                               size_t page_tokens, hipStream_t st) {
-    return launch_attn(pt_k, pt_v, q, scores, out, nullptr, pos, pos + 1, 1, n_head, n_head_kv, hd, kv_dim,
-                       page_tokens, st);
+    return launch_attn(pt_k, pt_v, q, n_head * hd, scores, out, nullptr, pos, pos + 1, 1, n_head, n_head_kv, hd,
+                       kv_dim, page_tokens, st);
+}
+
+hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* cos_t,
+                                    const float* sin_t, const int* d_pos, uint16_t* const* pt_k,
+                                    uint16_t* const* pt_v, size_t page_tokens, float* out, int8_t* q8, float* q8d,
+                                    size_t n_head, size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st) {
+    if (!attn_decode_fused_ok(hd, max_ctx)) return hipErrorInvalidValue;
+    const int sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
+    const int nslice = static_cast<int>(hd) / sw;
+    const int ctx_pad = static_cast<int>((max_ctx + 3) / 4 * 4);
+    const size_t lds = (3 * hd + ctx_pad) * sizeof(float) + static_cast<size_t>(kRV) * sw * sizeof(uint16_t);
+    const dim3 grid(static_cast<unsigned>(n_head * nslice));
+    const int group = static_cast<int>(n_head / n_head_kv), kvd = static_cast<int>(n_head_kv * hd);
+#define MVH_ATTN_FUSED(SW_)                                                                                          \
+    attn_decode_fused_kernel<SW_><<<grid, kAT, lds, st>>>(q, k, v, cos_t, sin_t, d_pos, pt_k, pt_v,                 \
+                                                          static_cast<int>(page_tokens), out, q8, q8d, group,      \
+                                                          static_cast<int>(hd), kvd, ctx_pad, nslice)
+    if (sw == 32) MVH_ATTN_FUSED(32);
+    else if (sw == 16) MVH_ATTN_FUSED(16);
+    else MVH_ATTN_FUSED(8);
+#undef MVH_ATTN_FUSED
+    return hipGetLastError();
+}
+
+bool attn_decode_fused_ok(size_t hd, size_t max_ctx) {
+    const size_t sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
+    const size_t lds = (3 * hd + (max_ctx + 3) / 4 * 4) * sizeof(float) + kRV * sw * sizeof(uint16_t);
+    return hd >= 8 && hd % 8 == 0 && hd <= 1024 && max_ctx >= 1 && lds <= 64 * 1024;
 }
 
 }  // namespace mvh

@@ -39,10 +39,20 @@ hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x,
 hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
                            size_t n_tokens, size_t kv_dim, size_t page_tokens, hipStream_t st);
 // B query tokens at positions pos..pos+B-1 (pos = *d_pos when d_pos != null),
-// causal; scores needs B * n_head * max_pos floats, max_pos > last position
-hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
-                       float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
-                       size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st);
+// causal; q of token b at q + b*q_pitch; scores needs B * n_head * max_pos
+// floats, max_pos > last position
+hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, size_t q_pitch,
+                       float* scores, float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B,
+                       size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st);
+// One decode token in one launch: RoPE of q and k at position *d_pos, the
+// F16 K/V write at that position, scores, softmax and the value sum, and
+// (when q8 != null, hd % 32 == 0) the Q8 activation of the output.  One
+// workgroup per query head; max_ctx bounds the position.
+bool attn_decode_fused_ok(size_t hd, size_t max_ctx);  // LDS and shape limits of the fused kernel
+hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* cos_t,
+                                    const float* sin_t, const int* d_pos, uint16_t* const* pt_k,
+                                    uint16_t* const* pt_v, size_t page_tokens, float* out, int8_t* q8, float* q8d,
+                                    size_t n_head, size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st);
 // scores needs n_head * (pos+1) floats of scratch
 hipError_t launch_attn_decode(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
                               float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim,
@@ -54,10 +64,14 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
 // x += add (if add), n = rmsnorm(x)*w, and q/qd = Q8 of n (if q); B rows of D
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
                           size_t D, float eps, hipStream_t st);
-hipError_t launch_rope_kv(float* q, float* k, const float* v, const float* cos_t, const float* sin_t, const int* d_pos,
-                          size_t pos0, size_t B, size_t n_head, size_t n_kv, size_t hd, uint16_t* const* pt_k,
-                          uint16_t* const* pt_v, size_t page_tokens, hipStream_t st);
-hipError_t launch_swiglu(const float* g, const float* u, float* ff, int8_t* q, float* qd, size_t n, hipStream_t st);
+// q/k/v of token b at q + b*q_pitch, k + b*kv_pitch, v + b*kv_pitch
+hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, size_t kv_pitch, const float* cos_t,
+                          const float* sin_t, const int* d_pos, size_t pos0, size_t B, size_t n_head, size_t n_kv,
+                          size_t hd, uint16_t* const* pt_k, uint16_t* const* pt_v, size_t page_tokens,
+                          hipStream_t st);
+// B rows: g/u row b at g + b*pitch, u + b*pitch; ff/q rows of F
+hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff, int8_t* q, float* qd, size_t B,
+                         size_t F, hipStream_t st);
 hipError_t launch_argmax(const float* logits, size_t V, size_t B, int* out, int* d_pos, int* hist, hipStream_t st);
 
 }  // namespace mvh

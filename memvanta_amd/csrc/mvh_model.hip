@@ -49,7 +49,7 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t
 // workgroup per row; D % 32 == 0.  The double sum is added as a tree, not in
 // the reference's element order; the two can differ only when the exact sum
 // of squares lies within ~1e-15 (relative) of an f32 rounding boundary of ss/D.
-constexpr int kNormT = 256;
+constexpr int kNormT = 1024;
 __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                          const float* __restrict__ w, float* __restrict__ n,
                                                          int8_t* __restrict__ q, float* __restrict__ qd, int D,
@@ -99,8 +99,9 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
 // GCC's contraction fma(x0,c,-(x1*s)) / fma(x0,s,x1*c)) on q and k of B
 // tokens at positions pos..pos+B-1, then PagedKVCache::write of k and v
 // through the reference's fp32_to_fp16 (:22).  One thread per (token, head, i).
-__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
-                                                      const float* __restrict__ v, const float* __restrict__ cos_t,
+__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int q_pitch, float* __restrict__ k,
+                                                      const float* __restrict__ v, int kv_pitch,
+                                                      const float* __restrict__ cos_t,
                                                       const float* __restrict__ sin_t, const int* __restrict__ d_pos,
                                                       int pos0, int B, int n_head, int n_kv, int hd,
                                                       uint16_t* const* __restrict__ pt_k,
@@ -111,8 +112,9 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, flo
     const int b = idx / (heads * half), rem = idx - b * heads * half, h = rem / half, i = rem - h * half;
     const int pos = (d_pos ? *d_pos : pos0) + b;
     const float c = cos_t[static_cast<size_t>(pos) * half + i], s = sin_t[static_cast<size_t>(pos) * half + i];
-    const int D = n_head * hd, KV = n_kv * hd;
-    float* z = h < n_head ? q + static_cast<size_t>(b) * D + h * hd : k + static_cast<size_t>(b) * KV + (h - n_head) * hd;
+    const int KV = n_kv * hd;
+    float* z = h < n_head ? q + static_cast<size_t>(b) * q_pitch + h * hd
+                          : k + static_cast<size_t>(b) * kv_pitch + (h - n_head) * hd;
     const float x0 = z[i], x1 = z[i + half];
     const float r0 = fmaf(x0, c, -(x1 * s)), r1 = fmaf(x0, s, x1 * c);
     z[i] = r0;
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, flo
         const size_t off = static_cast<size_t>(pos % page_tokens) * KV + kh * hd;
         uint16_t* kp = pt_k[pos / page_tokens] + off;
         uint16_t* vp = pt_v[pos / page_tokens] + off;
-        const float* vv = v + static_cast<size_t>(b) * KV + kh * hd;
+        const float* vv = v + static_cast<size_t>(b) * kv_pitch + kh * hd;
         kp[i] = f2h_ref(r0);
         kp[i + half] = f2h_ref(r1);
         vp[i] = f2h_ref(vv[i]);
@@ -131,26 +133,29 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, flo
 }
 
 // SwiGLU (src/llama_model.cpp:249,257): ff = (g/(1+expf(-g)))*u, with expf as
-// the C library computes it; optionally the Q8 activation of ff.  n % 32 == 0.
-__global__ __launch_bounds__(256) void swiglu_kernel(const float4* __restrict__ g, const float4* __restrict__ u,
-                                                     float4* __restrict__ ff, uint32_t* __restrict__ q,
-                                                     float* __restrict__ qd, int n4) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+// the C library computes it; optionally the Q8 activation of ff.  Row b of
+// g/u at g + b*pitch, u + b*pitch; ff and q rows are F long.  F % 32 == 0.
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                     int pitch, float* __restrict__ ff, int8_t* __restrict__ q,
+                                                     float* __restrict__ qd, int F) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
+    const int n4 = F / 4;
     const bool live = i < n4;  // n4 % 8 == 0: 8-lane groups are whole blocks
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) {
-        const float4 a = g[i], b = u[i];
+        const float4 a = reinterpret_cast<const float4*>(g + static_cast<size_t>(b) * pitch)[i];
+        const float4 c = reinterpret_cast<const float4*>(u + static_cast<size_t>(b) * pitch)[i];
         auto f = [](float z, float up) { return __fdiv_rn(z, 1.0f + mvh_expf(-z)) * up; };
-        o = make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
-        ff[i] = o;
+        o = make_float4(f(a.x, c.x), f(a.y, c.y), f(a.z, c.z), f(a.w, c.w));
+        reinterpret_cast<float4*>(ff + static_cast<size_t>(b) * F)[i] = o;
     }
     if (q) {
         float d;
         int s;
         const uint32_t packed = quantize_q8_x4(o, d, s);
         if (live) {
-            q[i] = packed;
-            if ((i & 7) == 0) qd[i >> 3] = d;
+            reinterpret_cast<uint32_t*>(q + static_cast<size_t>(b) * F)[i] = packed;
+            if ((i & 7) == 0) qd[static_cast<size_t>(b) * (F / 32) + (i >> 3)] = d;
         }
     }
 }
@@ -219,23 +224,25 @@ hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, 
     return hipGetLastError();
 }
 
-hipError_t launch_rope_kv(float* q, float* k, const float* v, const float* cos_t, const float* sin_t, const int* d_pos,
-                          size_t pos0, size_t B, size_t n_head, size_t n_kv, size_t hd, uint16_t* const* pt_k,
-                          uint16_t* const* pt_v, size_t page_tokens, hipStream_t st) {
+hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, size_t kv_pitch, const float* cos_t,
+                          const float* sin_t, const int* d_pos, size_t pos0, size_t B, size_t n_head, size_t n_kv,
+                          size_t hd, uint16_t* const* pt_k, uint16_t* const* pt_v, size_t page_tokens,
+                          hipStream_t st) {
     const size_t n = B * (n_head + n_kv) * (hd / 2);
     if (!n) return hipSuccess;
     rope_kv_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(
-        q, k, v, cos_t, sin_t, d_pos, static_cast<int>(pos0), static_cast<int>(B), static_cast<int>(n_head),
-        static_cast<int>(n_kv), static_cast<int>(hd), pt_k, pt_v, static_cast<int>(page_tokens));
+        q, static_cast<int>(q_pitch), k, v, static_cast<int>(kv_pitch), cos_t, sin_t, d_pos, static_cast<int>(pos0),
+        static_cast<int>(B), static_cast<int>(n_head), static_cast<int>(n_kv), static_cast<int>(hd), pt_k, pt_v,
+        static_cast<int>(page_tokens));
     return hipGetLastError();
 }
 
-hipError_t launch_swiglu(const float* g, const float* u, float* ff, int8_t* q, float* qd, size_t n, hipStream_t st) {
-    const size_t n4 = n / 4;
-    if (!n4) return hipSuccess;
-    swiglu_kernel<<<static_cast<unsigned>((n4 + 255) / 256), 256, 0, st>>>(
-        reinterpret_cast<const float4*>(g), reinterpret_cast<const float4*>(u), reinterpret_cast<float4*>(ff),
-        reinterpret_cast<uint32_t*>(q), qd, static_cast<int>(n4));
+hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff, int8_t* q, float* qd, size_t B,
+                         size_t F, hipStream_t st) {
+    const size_t n4 = F / 4;
+    if (!n4 || !B) return hipSuccess;
+    swiglu_kernel<<<dim3(static_cast<unsigned>((n4 + 255) / 256), static_cast<unsigned>(B)), 256, 0, st>>>(
+        g, u, static_cast<int>(pitch), ff, q, qd, static_cast<int>(F));
     return hipGetLastError();
 }
 

@@ -98,14 +98,26 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
         auto n = [&](const char* s) { return "blk." + std::to_string(i) + s; };
         auto& L = layers_[i];
         L.attn_norm = upload_vector(n(".attn_norm.weight"));
-        upload(L.q, n(".attn_q.weight"));
-        upload(L.k, n(".attn_k.weight"));
-        upload(L.v, n(".attn_v.weight"));
+        L.fused_qkv = upload_fused(L.qkv, {n(".attn_q.weight"), n(".attn_k.weight"), n(".attn_v.weight")});
+        if (!L.fused_qkv) {
+            upload(L.q, n(".attn_q.weight"));
+            upload(L.k, n(".attn_k.weight"));
+            upload(L.v, n(".attn_v.weight"));
+        }
         upload(L.o, n(".attn_output.weight"));
         L.ffn_norm = upload_vector(n(".ffn_norm.weight"));
-        upload(L.gate, n(".ffn_gate.weight"));
-        upload(L.up, n(".ffn_up.weight"));
+        L.fused_gu = upload_fused(L.gate_up, {n(".ffn_gate.weight"), n(".ffn_up.weight")});
+        if (!L.fused_gu) {
+            upload(L.gate, n(".ffn_gate.weight"));
+            upload(L.up, n(".ffn_up.weight"));
+        }
         upload(L.down, n(".ffn_down.weight"));
+        const auto rows = [&](const Tensor& f, const Tensor& a) { return f.d ? f.rows : a.rows; };
+        if (rows(L.qkv, L.q) != (L.fused_qkv ? c_.n_embd + 2 * c_.kv_dim() : c_.n_embd) ||
+            (!L.fused_qkv && (L.k.rows != c_.kv_dim() || L.v.rows != c_.kv_dim())) || L.o.rows != c_.n_embd ||
+            rows(L.gate_up, L.gate) != (L.fused_gu ? 2 * c_.n_ff : c_.n_ff) || L.down.rows != c_.n_embd ||
+            L.down.cols != c_.n_ff)
+            throw std::runtime_error("layer " + std::to_string(i) + ": weight shapes do not match the config");
     }
 
     // RoPE table computed on the host with the C library, as the reference
@@ -143,13 +155,10 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     const std::size_t B = max_batch_, D = c_.n_embd, F = c_.n_ff, KV = c_.kv_dim(), W = std::max(D, F);
     x_ = static_cast<float*>(dalloc(B * D * 4));
     n_ = static_cast<float*>(dalloc(B * D * 4));
-    q_ = static_cast<float*>(dalloc(B * D * 4));
-    k_ = static_cast<float*>(dalloc(B * KV * 4));
-    v_ = static_cast<float*>(dalloc(B * KV * 4));
+    qkv_ = static_cast<float*>(dalloc(B * (D + 2 * KV) * 4));
     att_ = static_cast<float*>(dalloc(B * D * 4));
     proj_ = static_cast<float*>(dalloc(B * D * 4));
-    g_ = static_cast<float*>(dalloc(B * F * 4));
-    u_ = static_cast<float*>(dalloc(B * F * 4));
+    gu_ = static_cast<float*>(dalloc(B * 2 * F * 4));
     ff_ = static_cast<float*>(dalloc(B * F * 4));
     scores_ = static_cast<float*>(dalloc(B * c_.n_head * c_.n_ctx * 4));
     logits_d_ = static_cast<float*>(dalloc(c_.vocab * 4));
@@ -166,6 +175,7 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     check(hipHostMalloc(reinterpret_cast<void**>(&pin_), 4 * (c_.n_ctx + B + 8), hipHostMallocDefault),
           "hipHostMalloc");
     logits_.resize(c_.vocab);
+    fused_attn_ = mvh::attn_decode_fused_ok(c_.head_dim(), c_.n_ctx);
     reset();
 }
 
@@ -191,6 +201,39 @@ void LlamaModel::upload(Tensor& t, const std::string& name) {
     check(hipMalloc(&t.d, g.nbytes), "hipMalloc tensor");
     allocs_.push_back(t.d);
     check(hipMemcpy(t.d, file_->tensor_data(g), g.nbytes, hipMemcpyHostToDevice), "tensor upload");
+}
+
+// One allocation holding the rows of `names` back to back (same type and K).
+bool LlamaModel::upload_fused(Tensor& t, const std::vector<std::string>& names) {
+    std::size_t bytes = 0, rows = 0;
+    const auto& g0 = file_->tensor(names[0]);
+    for (const auto& nm : names) {
+        const auto& g = file_->tensor(nm);
+        if (g.dims.size() < 2 || g.type != g0.type || g.ne(0) != g0.ne(0) || !g.nbytes) return false;
+        if (g.type != 2 && g.type != 8 && g.type != 14) return false;
+        bytes += g.nbytes;
+        rows += static_cast<std::size_t>(g.ne(1));
+    }
+    t.sname = names[0];
+    t.type = g0.type;
+    t.cols = static_cast<std::size_t>(g0.ne(0));
+    t.rows = rows;
+    check(hipMalloc(&t.d, bytes), "hipMalloc tensor");
+    allocs_.push_back(t.d);
+    std::size_t off = 0;
+    for (const auto& nm : names) {
+        const auto& g = file_->tensor(nm);
+        check(hipMemcpy(static_cast<uint8_t*>(t.d) + off, file_->tensor_data(g), g.nbytes, hipMemcpyHostToDevice),
+              "tensor upload");
+        off += g.nbytes;
+    }
+    return true;
+}
+
+LlamaModel::QkvLayout LlamaModel::qkv_layout(const Layer& L, std::size_t B) const {
+    const std::size_t D = c_.n_embd, KV = c_.kv_dim();
+    if (L.fused_qkv) return {qkv_, qkv_ + D, qkv_ + D + KV, D + 2 * KV, D + 2 * KV};
+    return {qkv_, qkv_ + B * D, qkv_ + B * (D + KV), D, KV};
 }
 
 float* LlamaModel::upload_vector(const std::string& name) {
@@ -279,28 +322,47 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
     check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_token, 1, x_, stream_), "embed");
     for (std::size_t li = 0; li < c_.n_layer; ++li) {
         auto& L = layers_[li];
-        const bool q8_in = L.q.type == 2 || L.k.type == 2 || L.v.type == 2;
+        const auto lay = qkv_layout(L, 1);
+        const bool q8_in = L.fused_qkv ? L.qkv.type == 2 : (L.q.type == 2 || L.k.type == 2 || L.v.type == 2);
         check(mvh::launch_rmsnorm(x_, li ? ffo_ : nullptr, L.attn_norm, n_, q8_in ? q8_ : nullptr, q8d_, 1, D,
                                   c_.rms_eps, stream_),
               "rmsnorm");
-        gemv(L.q, n_, L.q.type == 2 ? q8_ : nullptr, q8d_, q_);
-        gemv(L.k, n_, L.k.type == 2 ? q8_ : nullptr, q8d_, k_);
-        gemv(L.v, n_, L.v.type == 2 ? q8_ : nullptr, q8d_, v_);
+        if (L.fused_qkv) {
+            gemv(L.qkv, n_, L.qkv.type == 2 ? q8_ : nullptr, q8d_, qkv_);
+        } else {
+            gemv(L.q, n_, L.q.type == 2 ? q8_ : nullptr, q8d_, lay.q);
+            gemv(L.k, n_, L.k.type == 2 ? q8_ : nullptr, q8d_, lay.k);
+            gemv(L.v, n_, L.v.type == 2 ? q8_ : nullptr, q8d_, lay.v);
+        }
         uint16_t* const* pk = pt_k_ + li * max_pages_;
         uint16_t* const* pv = pt_v_ + li * max_pages_;
-        check(mvh::launch_rope_kv(q_, k_, v_, rope_cos_, rope_sin_, d_pos_, 0, 1, c_.n_head, c_.n_head_kv, hd, pk, pv,
-                                  page_tokens_, stream_),
-              "rope/kv");
-        check(mvh::launch_attn(pk, pv, q_, scores_, att_, d_pos_, 0, c_.n_ctx, 1, c_.n_head, c_.n_head_kv, hd,
-                               c_.kv_dim(), page_tokens_, stream_),
-              "attention");
-        gemv(L.o, att_, nullptr, nullptr, proj_);
-        const bool q8_ffn = L.gate.type == 2 || L.up.type == 2;
+        const bool o_q8 = fused_attn_ && L.o.type == 2 && hd % 32 == 0;
+        if (fused_attn_) {
+            check(mvh::launch_attn_decode_fused(lay.q, lay.k, lay.v, rope_cos_, rope_sin_, d_pos_, pk, pv, page_tokens_,
+                                                att_, o_q8 ? q8_ : nullptr, q8d_, c_.n_head, c_.n_head_kv, hd,
+                                                c_.n_ctx, stream_),
+                  "attention");
+        } else {
+            check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, d_pos_, 0,
+                                      1, c_.n_head, c_.n_head_kv, hd, pk, pv, page_tokens_, stream_),
+                  "rope/kv");
+            check(mvh::launch_attn(pk, pv, lay.q, lay.q_pitch, scores_, att_, d_pos_, 0, c_.n_ctx, 1, c_.n_head,
+                                   c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_),
+                  "attention");
+        }
+        gemv(L.o, att_, o_q8 ? q8_ : nullptr, q8d_, proj_);
+        const bool q8_ffn = L.fused_gu ? L.gate_up.type == 2 : (L.gate.type == 2 || L.up.type == 2);
         check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8_ffn ? q8_ : nullptr, q8d_, 1, D, c_.rms_eps, stream_),
               "rmsnorm");
-        gemv(L.gate, n_, L.gate.type == 2 ? q8_ : nullptr, q8d_, g_);
-        gemv(L.up, n_, L.up.type == 2 ? q8_ : nullptr, q8d_, u_);
-        check(mvh::launch_swiglu(g_, u_, ff_, L.down.type == 2 ? q8_ : nullptr, q8d_, F, stream_), "swiglu");
+        float* g = gu_;
+        float* u = gu_ + F;  // one token: the fused and the separate layouts coincide
+        if (L.fused_gu) {
+            gemv(L.gate_up, n_, L.gate_up.type == 2 ? q8_ : nullptr, q8d_, gu_);
+        } else {
+            gemv(L.gate, n_, L.gate.type == 2 ? q8_ : nullptr, q8d_, g);
+            gemv(L.up, n_, L.up.type == 2 ? q8_ : nullptr, q8d_, u);
+        }
+        check(mvh::launch_swiglu(g, u, 2 * F, ff_, L.down.type == 2 ? q8_ : nullptr, q8d_, 1, F, stream_), "swiglu");
         gemv(L.down, ff_, L.down.type == 2 ? q8_ : nullptr, q8d_, ffo_);
     }
     if (logits || argmax) {
@@ -314,32 +376,43 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
 
 // One prefill chunk (LlamaModel::forward_batch_impl, src/llama_model.cpp:240-252).
 void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
-    const std::size_t D = c_.n_embd, F = c_.n_ff, hd = c_.head_dim(), KV = c_.kv_dim();
-    (void)KV;
+    const std::size_t D = c_.n_embd, F = c_.n_ff, hd = c_.head_dim();
     check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_tokens, B, x_, stream_), "embed");
     const bool q8mode = mode_ == PrefillMode::Q8 && B >= 2;
     for (std::size_t li = 0; li < c_.n_layer; ++li) {
         auto& L = layers_[li];
+        const auto lay = qkv_layout(L, B);
         check(mvh::launch_rmsnorm(x_, li ? ffo_ : nullptr, L.attn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D,
                                   c_.rms_eps, stream_),
               "rmsnorm");
-        gemm(L.q, n_, q8mode ? q8_ : nullptr, q8d_, q_, B);
-        gemm(L.k, n_, q8mode ? q8_ : nullptr, q8d_, k_, B);
-        gemm(L.v, n_, q8mode ? q8_ : nullptr, q8d_, v_, B);
+        if (L.fused_qkv) {
+            gemm(L.qkv, n_, q8mode ? q8_ : nullptr, q8d_, qkv_, B);
+        } else {
+            gemm(L.q, n_, q8mode ? q8_ : nullptr, q8d_, lay.q, B);
+            gemm(L.k, n_, q8mode ? q8_ : nullptr, q8d_, lay.k, B);
+            gemm(L.v, n_, q8mode ? q8_ : nullptr, q8d_, lay.v, B);
+        }
         uint16_t* const* pk = pt_k_ + li * max_pages_;
         uint16_t* const* pv = pt_v_ + li * max_pages_;
-        check(mvh::launch_rope_kv(q_, k_, v_, rope_cos_, rope_sin_, nullptr, pos_, B, c_.n_head, c_.n_head_kv, hd, pk,
-                                  pv, page_tokens_, stream_),
+        check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, nullptr, pos_,
+                                  B, c_.n_head, c_.n_head_kv, hd, pk, pv, page_tokens_, stream_),
               "rope/kv");
-        check(mvh::launch_attn(pk, pv, q_, scores_, att_, nullptr, pos_, pos_ + B, B, c_.n_head, c_.n_head_kv, hd,
-                               c_.kv_dim(), page_tokens_, stream_),
+        check(mvh::launch_attn(pk, pv, lay.q, lay.q_pitch, scores_, att_, nullptr, pos_, pos_ + B, B, c_.n_head,
+                               c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_),
               "attention");
         gemm(L.o, att_, nullptr, nullptr, proj_, B);
         check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D, c_.rms_eps, stream_),
               "rmsnorm");
-        gemm(L.gate, n_, q8mode ? q8_ : nullptr, q8d_, g_, B);
-        gemm(L.up, n_, q8mode ? q8_ : nullptr, q8d_, u_, B);
-        check(mvh::launch_swiglu(g_, u_, ff_, q8mode ? q8_ : nullptr, q8d_, B * F, stream_), "swiglu");
+        float* g = gu_;
+        float* u = L.fused_gu ? gu_ + F : gu_ + B * F;
+        const std::size_t pitch = L.fused_gu ? 2 * F : F;
+        if (L.fused_gu) {
+            gemm(L.gate_up, n_, q8mode ? q8_ : nullptr, q8d_, gu_, B);
+        } else {
+            gemm(L.gate, n_, q8mode ? q8_ : nullptr, q8d_, g, B);
+            gemm(L.up, n_, q8mode ? q8_ : nullptr, q8d_, u, B);
+        }
+        check(mvh::launch_swiglu(g, u, pitch, ff_, q8mode ? q8_ : nullptr, q8d_, B, F, stream_), "swiglu");
         gemm(L.down, ff_, q8mode ? q8_ : nullptr, q8d_, ffo_, B);
     }
     if (logits) {

@@ -58,10 +58,21 @@ private:
     };
     struct Layer {
         Tensor q, k, v, o, gate, up, down;
+        // q|k|v and gate|up with rows concatenated in one allocation when the
+        // parts share type and K (one GEMV launch each)
+        Tensor qkv, gate_up;
+        bool fused_qkv{}, fused_gu{};
         float *attn_norm{}, *ffn_norm{};
     };
+    // where the q/k/v (or gate/up) rows of B tokens land in qkv_ (gu_)
+    struct QkvLayout {
+        float *q, *k, *v;
+        std::size_t q_pitch, kv_pitch;
+    };
+    QkvLayout qkv_layout(const Layer& L, std::size_t B) const;
 
     void upload(Tensor& t, const std::string& name);
+    bool upload_fused(Tensor& t, const std::vector<std::string>& names);
     float* upload_vector(const std::string& name);
     void gemv(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y);
     void gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B);
@@ -84,7 +95,7 @@ private:
     uint16_t** pt_v_{};
     float *rope_cos_{}, *rope_sin_{};
     // activations ([max_batch][...] for prefill; row 0 for decode)
-    float *x_{}, *n_{}, *q_{}, *k_{}, *v_{}, *att_{}, *proj_{}, *g_{}, *u_{}, *ff_{}, *logits_d_{}, *scores_{};
+    float *x_{}, *n_{}, *qkv_{}, *att_{}, *proj_{}, *gu_{}, *ff_{}, *logits_d_{}, *scores_{};
     float* ffo_{};       // down-projection output (the residual added by the next norm)
     int8_t *q8_{}, *q8s_{};
     float *q8d_{}, *q8sd_{};
@@ -93,6 +104,7 @@ private:
     int* pin_{};         // pinned host staging
     std::vector<float> logits_;
     hipGraphExec_t graph_{};
+    bool fused_attn_{};  // decode attention in one launch (launch_attn_decode_fused)
 };
 
 }  // namespace hip

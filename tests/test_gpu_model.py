@@ -98,3 +98,24 @@ def test_large_shapes_vs_oracle(tmp_path, oracle, cfg_name, mode):
         cur = int(np.argmax(want))
     assert m.kv_bytes() == mo.kv_bytes()
     m.close()
+
+
+@pytest.mark.parametrize("cfg_name,n_prompt", [("tiny-long", 600), ("openllama-7b-v2-q4_0-1layer-long", 530)])
+def test_long_context_vs_oracle(tmp_path, oracle, cfg_name, n_prompt):
+    """Positions past 512: the decode attention stages V in rounds of 512 rows."""
+    base = synth.TINY if cfg_name.startswith("tiny") else synth.LLAMA7B_1L
+    cfg = synth.dataclasses.replace(base, name=cfg_name, ctx=1024, layers=min(base.layers, 2))
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=17)
+    prompt = synth.prompt_tokens(3, n_prompt)
+    mo = oracle.model(path, ctx=1024, force_q8=True)
+    m = capi.Model(path, ctx=1024, act_mode=1, max_batch=32)
+    close(m.prefill(prompt, 32), mo.prefill(prompt, 32), f"{cfg_name} prefill")
+    cur = 9
+    for _ in range(3):
+        want = mo.forward(cur)
+        got = m.forward(cur)
+        close(got, want, f"{cfg_name} decode")
+        cur = int(np.argmax(want))
+        assert int(np.argmax(got)) == cur
+    m.close()
