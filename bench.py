@@ -17,8 +17,9 @@ real_model_bench (benchmarks/real_model_bench.cpp:20-27):
 * prompt ids follow the reference bench's fixed_tokens: (i*1543+17) % vocab.
 
 `roofline` times the dominant kernel, the Q4_0 x Q8 decode GEMV, alone at the
-7B decode shapes (per layer 4x [4096->4096], 2x [4096->11008],
-1x [11008->4096]; plus the [4096->32000] shape of the isolated-GEMV config),
+launches of one 7B decode layer (q|k|v fused [4096->12288], o [4096->4096],
+gate|up fused [4096->22016], down [11008->4096]; the isolated-GEMV shapes
+[4096->4096], [4096->11008], [11008->4096], [4096->32000] are timed beside),
 with HIP events on the backend's stream over graph replays that rotate weight
 copies so every launch streams its weights from HBM.  `cpu_baseline` runs the
 compiled reference's LlamaModel (oracle/_ref; else the C restatement) on the
@@ -39,9 +40,9 @@ sys.path.insert(0, ROOT)
 METRIC = "tg128 tok/s + achieved HBM GB/s (7B-shape Q4_0); pp512 prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 CTX, BATCH, PAGE, SEED_TOKENS, PROMPT_TOKENS, FIRST_TOKEN = 768, 32, 128, 128, 512, 17
-# per-layer decode GEMVs of the 7B shape (K, N, launches per layer)
-DECODE_GEMVS = [(4096, 4096, 4), (4096, 11008, 2), (11008, 4096, 1)]
-ISOLATED_GEMVS = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]
+# per-layer decode GEMV launches of the 7B shape (K, N, launches per layer)
+DECODE_GEMVS = [(4096, 12288, 1), (4096, 4096, 1), (4096, 22016, 1), (11008, 4096, 1)]
+ISOLATED_GEMVS = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000), (4096, 12288), (4096, 22016)]
 REF_TG128_TOKS = 1.52  # published reference tg128, OpenLLaMA-7B-v2 Q4_0, 4-thread Xeon 8573C, ctx 768
 
 
@@ -299,7 +300,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(mix_us / launches, 3),
                      "algorithmic_bytes_per_launch": mix_bytes // launches,
-                     "launch_mix": "7B decode layer: 4x 4096->4096, 2x 4096->11008, 1x 11008->4096"},
+                     "launch_mix": "7B decode layer: 4096->12288 (q|k|v), 4096->4096 (o), 4096->22016 "
+                                       "(gate|up), 11008->4096 (down)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -84,6 +84,9 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* cons
                                                             int group, int hd, int kv_dim, int page_tokens,
                                                             int score_pitch) {
     extern __shared__ float s_a[];
+    __shared__ uint64_t s_tab[32];
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
+    __syncthreads();
     const int h = blockIdx.x, b = blockIdx.z;
     const int n = (d_pos ? *d_pos : pos_arg) + b + 1;
     const float* sc = scores + (static_cast<size_t>(b) * n_head + h) * score_pitch;
@@ -92,7 +95,7 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* cons
     mx = wave_max(mx);
     double den = 0.0;
     for (int t = threadIdx.x; t < n; t += 64) {
-        const float e = mvh_expf(sc[t] - mx);
+        const float e = mvh_expf_tabbed(sc[t] - mx, s_tab);
         s_a[t] = e;
         den += static_cast<double>(e);
     }
@@ -160,6 +163,8 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_a + ctx_pad);  // [kRV][SW]
     __shared__ float red_f[kAT / 64];
     __shared__ double red_d[kAT / 64];
+    __shared__ uint64_t s_tab[32];
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
 
     const int h = blockIdx.x / nslice, slice = blockIdx.x - h * nslice;
     const int kh = h / group, t = threadIdx.x, half = hd >> 1;
@@ -224,13 +229,22 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
                 for (int e = 0; e < 8; ++e) acc[e] = fmaf(s_q[c + e], s_k[c + e], acc[e]);
             }
         } else {
+            // the row's 16-byte chunks are loaded 16 at a time (one memory
+            // round trip for hd <= 128), then consumed in order
             const uint16_t* krow = pt_k[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
-            for (int c = 0; c < hd; c += 8) {
-                const uint4 kv8 = *reinterpret_cast<const uint4*>(krow + c);
-                const uint32_t w[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
+            for (int c0 = 0; c0 < hd; c0 += 128) {
+                uint4 kv[16];
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    acc[e] = fmaf(s_q[c + e], h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
+                for (int j = 0; j < 16; ++j)
+                    if (c0 + 8 * j < hd) kv[j] = *reinterpret_cast<const uint4*>(krow + c0 + 8 * j);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    if (c0 + 8 * j >= hd) break;
+                    const uint32_t w[4] = {kv[j].x, kv[j].y, kv[j].z, kv[j].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        acc[e] = fmaf(s_q[c0 + 8 * j + e], h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
+                }
             }
         }
         float sum = acc[0];
@@ -250,7 +264,7 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     // 3. softmax weights
     double den = 0.0;
     for (int tt = t; tt <= pos; tt += kAT) {
-        const float e = mvh_expf(s_a[tt] - mx);
+        const float e = mvh_expf_tabbed(s_a[tt] - mx, s_tab);
         s_a[tt] = e;
         den += static_cast<double>(e);
     }

@@ -45,7 +45,9 @@ MVH_EXPF_QUAL uint64_t mvh_expf_tab(uint32_t i) {
     }
 }
 
-MVH_EXPF_QUAL float mvh_expf(float x) {
+/* tab != NULL: the 32 entries of mvh_expf_tab (a GPU kernel keeps them in
+ * LDS, so the lookup is not a global-memory round trip). */
+MVH_EXPF_QUAL float mvh_expf_tabbed(float x, const uint64_t* tab) {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
@@ -64,7 +66,7 @@ MVH_EXPF_QUAL float mvh_expf(float x) {
     memcpy(&ki, &kd, 8);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = mvh_expf_tab((uint32_t)(ki % 32));
+    uint64_t t = tab ? tab[ki % 32] : mvh_expf_tab((uint32_t)(ki % 32));
     t += ki << 47;
     double s;
     memcpy(&s, &t, 8);
@@ -75,5 +77,7 @@ MVH_EXPF_QUAL float mvh_expf(float x) {
     y = y * s;
     return (float)y;
 }
+
+MVH_EXPF_QUAL float mvh_expf(float x) { return mvh_expf_tabbed(x, 0); }
 
 #endif

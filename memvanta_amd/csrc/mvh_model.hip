@@ -138,14 +138,19 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                      int pitch, float* __restrict__ ff, int8_t* __restrict__ q,
                                                      float* __restrict__ qd, int F) {
+    __shared__ uint64_t s_tab[32];
     const int i = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
     const int n4 = F / 4;
     const bool live = i < n4;  // n4 % 8 == 0: 8-lane groups are whole blocks
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), c = a, o = a;
     if (live) {
-        const float4 a = reinterpret_cast<const float4*>(g + static_cast<size_t>(b) * pitch)[i];
-        const float4 c = reinterpret_cast<const float4*>(u + static_cast<size_t>(b) * pitch)[i];
-        auto f = [](float z, float up) { return __fdiv_rn(z, 1.0f + mvh_expf(-z)) * up; };
+        a = reinterpret_cast<const float4*>(g + static_cast<size_t>(b) * pitch)[i];
+        c = reinterpret_cast<const float4*>(u + static_cast<size_t>(b) * pitch)[i];
+    }
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
+    __syncthreads();
+    if (live) {
+        auto f = [&](float z, float up) { return __fdiv_rn(z, 1.0f + mvh_expf_tabbed(-z, s_tab)) * up; };
         o = make_float4(f(a.x, c.x), f(a.y, c.y), f(a.z, c.z), f(a.w, c.w));
         reinterpret_cast<float4*>(ff + static_cast<size_t>(b) * F)[i] = o;
     }
