@@ -54,7 +54,7 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* 
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
     int c = 0;
     for (; c + 8 <= hd; c += 8) {
-        const uint4 kv8 = *reinterpret_cast<const uint4*>(krow + c);
+        const uint4 kv8 = ld_global16(krow + c);
         const uint32_t w[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = fmaf(s_q[c + e], h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
@@ -138,80 +138,114 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* cons
 //     lane-of-8 fma accumulation, t0+..+t7);
 //  3. mx, e_t = expf(s_t - mx), den = double sum, a_t = e_t * float(1/den);
 //  4. out[d] = fma(a_t, V_t[d], out[d]) for t = 0..p in order, one lane per
-//     output element, the V slice staged through LDS in rounds of kRV rows
-//     (the loads of round r+1 are in flight while round r is summed);
+//     output element, the V slice staged through LDS in rounds of kRV rows,
+//     transposed so a lane reads 8 rows with one 16-byte LDS load (the
+//     global loads of round r+1 are in flight while round r is summed);
 //  5. with SW == 32 the slice is one Q8 block of the output: quantize_q8 of
 //     it (the o-projection's activation) is written beside it.
-// The scores are recomputed by every slice of a head (K is read from L2).
+// Memory round trips on the critical path: (position, page tables, q/k/v)
+// then (cos/sin, the first K row of each thread, V round 0), all issued
+// together.  The scores are recomputed by every slice of a head (K is read
+// from L2).
 constexpr int kAT = 256;
-constexpr int kRV = 512;  // V rows per staging round
+constexpr int kRV = 512;        // V rows per staging round
+constexpr int kMaxPages = 128;  // page-table entries staged in LDS
 
 template <int SW>
 __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int* __restrict__ d_pos,
-    uint16_t* const* __restrict__ pt_k, uint16_t* const* __restrict__ pt_v, int page_tokens,
+    uint16_t* const* __restrict__ pt_k, uint16_t* const* __restrict__ pt_v, int page_tokens, int max_pages,
     float* __restrict__ out, int8_t* __restrict__ q8, float* __restrict__ q8d, int group, int hd, int kv_dim,
     int ctx_pad, int nslice) {
-    constexpr int kCh = SW / 8;                          // 16-byte chunks per V row slice
-    constexpr int kVPT = (kRV * kCh + kAT - 1) / kAT;    // chunks per thread per round
+    constexpr int kCh = SW / 8;                        // 16-byte chunks per V row slice
+    constexpr int kVPT = (kRV * kCh + kAT - 1) / kAT;  // chunks per thread per round
     extern __shared__ __align__(16) float sm[];
     float* s_q = sm;
     float* s_k = sm + hd;
     float* s_v = sm + 2 * hd;
     float* s_a = sm + 3 * hd;
-    uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_a + ctx_pad);  // [kRV][SW]
+    uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_a + ctx_pad);  // [SW][kRV]
     __shared__ float red_f[kAT / 64];
     __shared__ double red_d[kAT / 64];
     __shared__ uint64_t s_tab[32];
-    if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
+    __shared__ uint16_t* s_pk[kMaxPages];
+    __shared__ uint16_t* s_pv[kMaxPages];
 
     const int h = blockIdx.x / nslice, slice = blockIdx.x - h * nslice;
     const int kh = h / group, t = threadIdx.x, half = hd >> 1;
-    const int pos = *d_pos;
     const int dbase = slice * SW;
-    auto vsrc = [&](int row, int c) {
-        return reinterpret_cast<const uint4*>(pt_v[row / page_tokens] + static_cast<size_t>(row % page_tokens) * kv_dim +
-                                              kh * hd + dbase + c * 8);
+
+    // round trip 1: position, page tables, q/k/v of this token
+    const int pos = *d_pos;
+    for (int i = t; i < max_pages; i += kAT) {
+        s_pk[i] = pt_k[i];
+        s_pv[i] = pt_v[i];
+    }
+    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+    if (t < half) {
+        const float* qh = q + static_cast<size_t>(h) * hd;
+        const float* kk = k + static_cast<size_t>(kh) * hd;
+        const float* vv = v + static_cast<size_t>(kh) * hd;
+        q0 = qh[t];
+        q1 = qh[t + half];
+        k0 = kk[t];
+        k1 = kk[t + half];
+        v0 = vv[t];
+        v1 = vv[t + half];
+    }
+    __syncthreads();
+
+    // round trip 2: cos/sin, this thread's first K row, V round 0
+    float cs = 0.f, sn = 0.f;
+    if (t < half) {
+        cs = cos_t[static_cast<size_t>(pos) * half + t];
+        sn = sin_t[static_cast<size_t>(pos) * half + t];
+    }
+    auto krow_of = [&](int tt) {
+        return s_pk[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
     };
-    // round 0 of the V slice goes out first
+    uint4 kv[16];
+    auto load_k = [&](int tt, int c0) {
+        const uint16_t* kr = krow_of(tt) + c0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (c0 + 8 * j < hd) kv[j] = ld_global16(kr + 8 * j);
+    };
+    if (t < pos) load_k(t, 0);
     uint4 vr[kVPT];
     auto load_round = [&](int r0) {
-        const int rows = min(kRV, pos - r0);
+        // branch-free: chunks past the round's rows re-read row r0 (ignored)
+        const int lim = min(kRV, pos - r0) * kCh;
 #pragma unroll
         for (int i = 0; i < kVPT; ++i) {
-            const int c = i * kAT + t;
-            if (c < rows * kCh) vr[i] = *vsrc(r0 + c / kCh, c % kCh);
+            const int c = i * kAT + t < lim ? i * kAT + t : 0;
+            const int row = r0 + c / kCh;
+            vr[i] = ld_global16(s_pv[row / page_tokens] + static_cast<size_t>(row % page_tokens) * kv_dim + kh * hd +
+                                dbase + (c % kCh) * 8);
         }
     };
     if (pos > 0) load_round(0);
 
     // 1. RoPE, K/V of the current position
-    {
+    if (t < half) {
         const size_t off = static_cast<size_t>(pos % page_tokens) * kv_dim + kh * hd;
-        uint16_t* kc = pt_k[pos / page_tokens] + off;
-        uint16_t* vc = pt_v[pos / page_tokens] + off;
-        const bool writer = slice == 0 && h % group == 0;
-        const float* qh = q + static_cast<size_t>(h) * hd;
-        const float* kk = k + static_cast<size_t>(kh) * hd;
-        const float* vv = v + static_cast<size_t>(kh) * hd;
-        for (int i = t; i < half; i += kAT) {
-            const float c = cos_t[static_cast<size_t>(pos) * half + i], s = sin_t[static_cast<size_t>(pos) * half + i];
-            const float q0 = qh[i], q1 = qh[i + half], k0 = kk[i], k1 = kk[i + half];
-            s_q[i] = fmaf(q0, c, -(q1 * s));
-            s_q[i + half] = fmaf(q0, s, q1 * c);
-            const uint16_t hk0 = f2h_ref(fmaf(k0, c, -(k1 * s))), hk1 = f2h_ref(fmaf(k0, s, k1 * c));
-            const uint16_t hv0 = f2h_ref(vv[i]), hv1 = f2h_ref(vv[i + half]);
-            s_k[i] = h2f(hk0);
-            s_k[i + half] = h2f(hk1);
-            s_v[i] = h2f(hv0);
-            s_v[i + half] = h2f(hv1);
-            if (writer) {
-                kc[i] = hk0;
-                kc[i + half] = hk1;
-                vc[i] = hv0;
-                vc[i + half] = hv1;
-            }
+        s_q[t] = fmaf(q0, cs, -(q1 * sn));
+        s_q[t + half] = fmaf(q0, sn, q1 * cs);
+        const uint16_t hk0 = f2h_ref(fmaf(k0, cs, -(k1 * sn))), hk1 = f2h_ref(fmaf(k0, sn, k1 * cs));
+        const uint16_t hv0 = f2h_ref(v0), hv1 = f2h_ref(v1);
+        s_k[t] = h2f(hk0);
+        s_k[t + half] = h2f(hk1);
+        s_v[t] = h2f(hv0);
+        s_v[t + half] = h2f(hv1);
+        if (slice == 0 && h % group == 0) {  // one writer per kv head
+            uint16_t* kc = s_pk[pos / page_tokens] + off;
+            uint16_t* vc = s_pv[pos / page_tokens] + off;
+            kc[t] = hk0;
+            kc[t + half] = hk1;
+            vc[t] = hv0;
+            vc[t + half] = hv1;
         }
     }
     __syncthreads();
@@ -229,21 +263,17 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
                 for (int e = 0; e < 8; ++e) acc[e] = fmaf(s_q[c + e], s_k[c + e], acc[e]);
             }
         } else {
-            // the row's 16-byte chunks are loaded 16 at a time (one memory
-            // round trip for hd <= 128), then consumed in order
-            const uint16_t* krow = pt_k[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
             for (int c0 = 0; c0 < hd; c0 += 128) {
-                uint4 kv[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    if (c0 + 8 * j < hd) kv[j] = *reinterpret_cast<const uint4*>(krow + c0 + 8 * j);
+                if (tt != t || c0 != 0) load_k(tt, c0);  // the first group of the first row is in flight already
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     if (c0 + 8 * j >= hd) break;
-                    const uint32_t w[4] = {kv[j].x, kv[j].y, kv[j].z, kv[j].w};
+                    const half8 hk = as_half8(kv[j]);
+                    const float4 qa = *reinterpret_cast<const float4*>(s_q + c0 + 8 * j);
+                    const float4 qb = *reinterpret_cast<const float4*>(s_q + c0 + 8 * j + 4);
+                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        acc[e] = fmaf(s_q[c0 + 8 * j + e], h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
+                    for (int e = 0; e < 8; ++e) acc[e] = fmaf(qv[e], static_cast<float>(hk[e]), acc[e]);
                 }
             }
         }
@@ -281,23 +311,48 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     float acc = 0.0f;
     for (int r0 = 0; r0 < pos; r0 += kRV) {
         const int rows = min(kRV, pos - r0);
+        // transpose into [dim][row] so each lane's rows are contiguous
 #pragma unroll
         for (int i = 0; i < kVPT; ++i) {
             const int c = i * kAT + t;
-            if (c < rows * kCh) reinterpret_cast<uint4*>(s_vt)[c] = vr[i];
+            if (c < rows * kCh) {
+                const int row = c / kCh, d0 = (c % kCh) * 8;
+                const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    s_vt[(d0 + e) * kRV + row] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+            }
         }
         __syncthreads();  // also orders the s_a writes above before their reads
         if (r0 + kRV < pos) load_round(r0 + kRV);
         if (t < SW) {
+            const uint16_t* vl = s_vt + t * kRV;
+            const float* al = s_a + r0;
             int j = 0;
-            for (; j + 8 <= rows; j += 8) {
-                float vv[8];
+            if (rows >= 16) {
+                // software pipeline over 16-row steps: the next 16 rows are
+                // read from LDS while the current 16 are summed
+                uint4 v0 = *reinterpret_cast<const uint4*>(vl), v1 = *reinterpret_cast<const uint4*>(vl + 8);
+                float4 a[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vv[e] = h2f(s_vt[(j + e) * SW + t]);
+                for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(al + 4 * i);
+                for (; j + 16 <= rows; j += 16) {
+                    const half8 h0 = as_half8(v0), h1 = as_half8(v1);
+                    const float av[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
+                                          a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
+                    if (j + 32 <= rows) {
+                        v0 = *reinterpret_cast<const uint4*>(vl + j + 16);
+                        v1 = *reinterpret_cast<const uint4*>(vl + j + 24);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc = fmaf(s_a[r0 + j + e], vv[e], acc);
+                        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(al + j + 16 + 4 * i);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = fmaf(av[e], static_cast<float>(h0[e]), acc);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = fmaf(av[8 + e], static_cast<float>(h1[e]), acc);
+                }
             }
-            for (; j < rows; ++j) acc = fmaf(s_a[r0 + j], h2f(s_vt[j * SW + t]), acc);
+            for (; j < rows; ++j) acc = fmaf(al[j], h2f(vl[j]), acc);
         }
         __syncthreads();
     }
@@ -364,7 +419,8 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
                                     const float* sin_t, const int* d_pos, uint16_t* const* pt_k,
                                     uint16_t* const* pt_v, size_t page_tokens, float* out, int8_t* q8, float* q8d,
                                     size_t n_head, size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st) {
-    if (!attn_decode_fused_ok(hd, max_ctx)) return hipErrorInvalidValue;
+    if (!attn_decode_fused_ok(hd, max_ctx, page_tokens)) return hipErrorInvalidValue;
+    const int max_pages = static_cast<int>((max_ctx + page_tokens - 1) / page_tokens);
     const int sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
     const int nslice = static_cast<int>(hd) / sw;
     const int ctx_pad = static_cast<int>((max_ctx + 3) / 4 * 4);
@@ -373,8 +429,8 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
     const int group = static_cast<int>(n_head / n_head_kv), kvd = static_cast<int>(n_head_kv * hd);
 #define MVH_ATTN_FUSED(SW_)                                                                                          \
     attn_decode_fused_kernel<SW_><<<grid, kAT, lds, st>>>(q, k, v, cos_t, sin_t, d_pos, pt_k, pt_v,                 \
-                                                          static_cast<int>(page_tokens), out, q8, q8d, group,      \
-                                                          static_cast<int>(hd), kvd, ctx_pad, nslice)
+                                                          static_cast<int>(page_tokens), max_pages, out, q8, q8d,  \
+                                                          group, static_cast<int>(hd), kvd, ctx_pad, nslice)
     if (sw == 32) MVH_ATTN_FUSED(32);
     else if (sw == 16) MVH_ATTN_FUSED(16);
     else MVH_ATTN_FUSED(8);
@@ -382,10 +438,11 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
     return hipGetLastError();
 }
 
-bool attn_decode_fused_ok(size_t hd, size_t max_ctx) {
+bool attn_decode_fused_ok(size_t hd, size_t max_ctx, size_t page_tokens) {
     const size_t sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
     const size_t lds = (3 * hd + (max_ctx + 3) / 4 * 4) * sizeof(float) + kRV * sw * sizeof(uint16_t);
-    return hd >= 8 && hd % 8 == 0 && hd <= 1024 && max_ctx >= 1 && lds <= 64 * 1024;
+    return hd >= 8 && hd % 8 == 0 && hd <= 2 * kAT && max_ctx >= 1 && page_tokens >= 1 &&
+           (max_ctx + page_tokens - 1) / page_tokens <= kMaxPages && lds <= 56 * 1024;
 }
 
 }  // namespace mvh

@@ -122,6 +122,24 @@ __device__ __forceinline__ uint32_t quantize_q8_x4(float4 v, float& d, int& s) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Eight binary16 values of a 16-byte load; fmaf(a, float(h[e]), c) on them
+// compiles to v_fma_mix_f32 (exact f16->f32 conversion fused into the FMA,
+// one rounding, as cvt + fmaf).
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ half8 as_half8(uint4 w) {
+    const u32x4 v = {w.x, w.y, w.z, w.w};
+    return __builtin_bit_cast(half8, v);
+}
+
+// 16-byte load through a pointer that is known to address global memory but
+// was itself loaded from memory (a page table): the address-space cast makes
+// it a global_load instead of a flat_load, whose LDS/VMEM counter coupling
+// serialises consecutive loads.
+__device__ __forceinline__ uint4 ld_global16(const void* p) {
+    const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)(reinterpret_cast<uintptr_t>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // 16-byte streaming load (weights are read once per call: nontemporal hint).
 __device__ __forceinline__ uint4 ld_stream16(const void* p) {
     const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

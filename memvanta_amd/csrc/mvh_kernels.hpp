@@ -48,7 +48,7 @@ hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v,
 // F16 K/V write at that position, scores, softmax and the value sum, and
 // (when q8 != null, hd % 32 == 0) the Q8 activation of the output.  One
 // workgroup per query head; max_ctx bounds the position.
-bool attn_decode_fused_ok(size_t hd, size_t max_ctx);  // LDS and shape limits of the fused kernel
+bool attn_decode_fused_ok(size_t hd, size_t max_ctx, size_t page_tokens);  // LDS and shape limits of the fused kernel
 hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* cos_t,
                                     const float* sin_t, const int* d_pos, uint16_t* const* pt_k,
                                     uint16_t* const* pt_v, size_t page_tokens, float* out, int8_t* q8, float* q8d,

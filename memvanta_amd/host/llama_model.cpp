@@ -175,7 +175,7 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     check(hipHostMalloc(reinterpret_cast<void**>(&pin_), 4 * (c_.n_ctx + B + 8), hipHostMallocDefault),
           "hipHostMalloc");
     logits_.resize(c_.vocab);
-    fused_attn_ = mvh::attn_decode_fused_ok(c_.head_dim(), c_.n_ctx);
+    fused_attn_ = mvh::attn_decode_fused_ok(c_.head_dim(), c_.n_ctx, page_tokens_);
     reset();
 }
 
