@@ -158,6 +158,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--model", default=None, help="existing GGUF to use instead of the synthetic 7B shape")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the isolated GEMV kernel timing plus a 256 MiB device copy (for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU (no multi-GPU path); "
@@ -171,6 +173,17 @@ def main():
     import torch
 
     from memvanta_amd import capi, synth
+
+    if args.kernels_only:
+        us = time_gemv_kernels(args.kernel_launches, args.copies)
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written by one copy kernel
+        torch.cuda.synchronize()
+        print(json.dumps({"gemv_us": {f"{k}->{n}": round(v, 3) for (k, n), v in us.items()},
+                          "copy_bytes": src.numel() * 4}))
+        return
 
     cfg = synth.LLAMA7B
     tmpdir = None
