@@ -119,6 +119,50 @@ def time_gemv_kernels(launches: int, copies: int):
     return out
 
 
+PREFILL_GEMMS = [(4096, 4096), (4096, 11008), (11008, 4096)]  # (K, N) of the GEMM config
+PREFILL_M = [32, 128, 512]
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+
+
+def time_prefill_gemm(reps: int):
+    """Q4_0 x Q8 prefill GEMM (int8 MFMA) at the GEMM config shapes: us, TOP/s, GB/s."""
+    import numpy as np
+    import torch
+
+    from memvanta_amd import capi, synth
+
+    ctx = capi.Context(0)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    rng = np.random.default_rng(5)
+    out = []
+    for k, n in PREFILL_GEMMS:
+        w = synth.quantize_torch(synth.Q4_0, torch.randn((n, k), generator=gen, device="cuda") * 0.02)
+        t = ctx.upload("blk.0.ffn_up.weight", synth.Q4_0, k, n, w.cpu().numpy())
+        for m in PREFILL_M:
+            x = torch.from_numpy(synth.activations(rng, m, k)).cuda()
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8, y=y)  # warm-up (includes the activation quantizer)
+            ctx.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                a.record(stream)
+                for _ in range(reps):
+                    ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8, y=y)
+                b.record(stream)
+            b.synchronize()
+            us = a.elapsed_time(b) * 1e3 / reps
+            ops = 2.0 * m * n * k
+            byts = n * (k // 32) * 18 + m * (k + k // 8) + 4 * m * n
+            out.append({"K": k, "N": n, "M": m, "us": round(us, 2), "TOP/s": round(ops / us / 1e6, 2),
+                        "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+                        "GB/s": round(byts / us / 1e3, 1)})
+        t.free()
+    ctx.close()
+    return out
+
+
 def cpu_baseline(path: str, budget_s: float):
     """The reference CPU LlamaModel on the same GGUF: greedy decode after a short seed."""
     from oracle import pyoracle
@@ -175,6 +219,8 @@ def main():
     from memvanta_amd import capi, synth
 
     if args.kernels_only:
+        gemm = time_prefill_gemm(10)
+        print(json.dumps({"prefill_gemm": gemm}))
         us = time_gemv_kernels(args.kernel_launches, args.copies)
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)

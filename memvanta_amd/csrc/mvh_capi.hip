@@ -466,8 +466,13 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
             ActView a;
             if (int rc = act_buffers(c, batch, cols, &a)) return rc;
             MVH_HIP(mvh::launch_quantize_q8(xd, a.q, a.d, a.s, batch, cols, c->stream));
-            for (size_t b = 0; b < batch; ++b)
-                MVH_HIP(mvh::launch_gemv_q4_0(W, a.q + b * cols, a.d + b * nb, yd + b * rows, rows, cols, c->stream));
+            if (mvh::gemm_q4_0_mfma_ok(cols)) {  // int8 MFMA tiles, same per-block chain
+                MVH_HIP(mvh::launch_gemm_q4_0_q8_mfma(W, a.q, a.d, yd, rows, cols, batch, c->stream));
+            } else {
+                for (size_t b = 0; b < batch; ++b)
+                    MVH_HIP(mvh::launch_gemv_q4_0(W, a.q + b * cols, a.d + b * nb, yd + b * rows, rows, cols,
+                                                  c->stream));
+            }
         } else {
             MVH_HIP(mvh::launch_gemv_q8_0(W, xd, yd, rows, cols, batch, c->stream));
         }

@@ -35,6 +35,14 @@ hipError_t launch_gemv_q4_0_f32act(const uint8_t* W, const float* x, float* y, s
 hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,
                                 size_t batch, hipStream_t st);
 
+// ---- batched prefill on int8 MFMA (mvh_gemm_q4.hip) ----
+// y[b*rows + r] = dot_q4_q8(W row r, Q8 activation row b) for b < batch
+// (MEMVANTA_FORCE_Q8_ACT numerics); aq [batch][cols] int8 (16-byte aligned
+// rows), ad [batch][cols/32]; needs cols % 256 == 0.
+bool gemm_q4_0_mfma_ok(size_t cols);
+hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows,
+                                    size_t cols, size_t batch, hipStream_t st);
+
 // ---- paged F16 KV + decode attention (mvh_attn.hip) ----
 hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
                            size_t n_tokens, size_t kv_dim, size_t page_tokens, hipStream_t st);

@@ -156,6 +156,21 @@ def test_matmul_v06_q8_mode_bitexact(ctx, oracle, ty, batch, k, n):
     t.free()
 
 
+@pytest.mark.parametrize("batch,k,n", [(32, 4096, 4096), (128, 4096, 1024), (512, 4096, 256), (32, 4096, 11008),
+                                        (32, 11008, 4096), (33, 256, 100), (3, 512, 17), (70, 768, 45)])
+def test_prefill_gemm_int8_mfma_bitexact(ctx, oracle, batch, k, n):
+    """The int8-MFMA Q4_0 x Q8 GEMM (K % 256 == 0) against the FORCE_Q8 reference
+    chain: the GEMM config shapes, plus token and row counts off the 32 x 32 tile."""
+    rng = np.random.default_rng(batch * 7 + k + n)
+    w = _w(rng, synth.Q4_0, n, k)
+    t = ctx.upload("blk.0.ffn_gate.weight", synth.Q4_0, k, n, w)
+    x = synth.activations(rng, batch, k)
+    got = ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8)
+    want = oracle.matmul_batch_v06(w, synth.Q4_0, n, k, x, is_ffn=True, force_q8=True)
+    assert_bitexact(got, want, f"mfma gemm M={batch} K={k} N={n}")
+    t.free()
+
+
 @pytest.mark.parametrize("ty,k", [(synth.Q4_0, 288), (synth.Q8_0, 1024), (synth.Q6_K, 512)])
 def test_matmul_batch_fallback(ctx, oracle, ty, k):
     rng = np.random.default_rng(k + ty)
