@@ -18,8 +18,9 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops off: no v_pk_*_f32 in the generated code.
 # -fhip-fp32-correctly-rounded-divide-sqrt (hipcc's default, stated): f32 `/`
 # and __builtin_sqrtf round to nearest even, as the reference's do.
+# -amdgpu-mfma-vgpr-form: MFMA results land in VGPRs (no accvgpr reads).
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-shared", "-ffp-contract=off",
-             "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+             "-fhip-fp32-correctly-rounded-divide-sqrt", "-mllvm", "-amdgpu-mfma-vgpr-form", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
 def _run(cmd, cwd=ROOT):

@@ -10,18 +10,18 @@
 // the reference's fma for its 4 outputs, block after block, so every output
 // is the reference's chain bit for bit.  No split-K, no reassociation.
 //
-// Data path per K-chunk of 8 blocks (256 elements), workgroup tile = 32 rows
-// x 32 tokens, 4 waves = (row half, token half):
-//   1. coalesced 16-byte loads of the tile's raw Q4_0 bytes (32 rows x 144 B,
-//      rows of a chunk are 16-byte aligned when K % 256 == 0), of the int8
-//      activations (32 tokens x 256 B, stored [block][token][32] so operand
-//      reads are conflict-free) and of the activation scales;
+// Work split: one wave per tile of 16 weight rows x 16*TG tokens, independent
+// of every other wave (wave-private LDS, no workgroup barriers).  Per K-chunk
+// of 8 blocks (256 elements):
+//   1. the tile's raw Q4_0 bytes (16 rows x 144 B; a row's chunk is 16-byte
+//      aligned when K % 256 == 0) come in with 16-byte loads, the int8
+//      activation operands straight into registers (8 bytes per lane and
+//      block), the activation scales as one 16-byte load per lane -- the
+//      next chunk's loads are in flight while this chunk is computed;
 //   2. the raw blocks are expanded in LDS to int8 (q - 8) in element order
-//      plus an f32 weight scale per (block, row) -- one (row, block) per thread;
-//   3. every wave runs 8 MFMAs (one per block) with operands read from LDS
-//      (8-byte reads) and folds each block's 4 products into its accumulators.
-// The loads of chunks c+1 and c+2 are in flight while chunk c is expanded
-// and summed.
+//      plus an f32 weight scale per (block, row), two (row, block) per lane;
+//   3. per block TG MFMAs (token groups) share the expanded weight operand;
+//      each lane then applies the reference's fma to its 4 outputs per group.
 #include "mvh_kernels.hpp"
 
 namespace mvh {
@@ -29,77 +29,89 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kGT = 256;        // threads per workgroup
-constexpr int kRows = 32;       // weight rows per workgroup
-constexpr int kToks = 32;       // tokens per workgroup
-constexpr int kChunk = 8;       // blocks per K-chunk
-constexpr int kUnit = 144;      // bytes of 8 Q4_0 blocks of one row
-constexpr int kWPieces = kRows * kUnit / 16;   // 288 16-byte pieces of raw weights per chunk
-constexpr int kAPieces = kToks * kChunk * 2;   // 512 16-byte pieces of activations per chunk
+constexpr int kRows = 16;   // weight rows per wave
+constexpr int kChunk = 8;   // blocks per K-chunk
+constexpr int kUnit = 144;  // bytes of 8 Q4_0 blocks of one row
+constexpr int kWPieces = kRows * kUnit / 16;  // 144 16-byte pieces of raw weights per chunk
 
 // bytes (q - 8) of four nibbles held one per byte (0..15): (n + 120) ^ 0x80
 __device__ __forceinline__ uint32_t nib_to_s8(uint32_t n) {
     return ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
 }
 
-__global__ __launch_bounds__(kGT) void gemm_q4_0_q8_mfma_kernel(const uint8_t* __restrict__ W,
-                                                                const int8_t* __restrict__ aq,
-                                                                const float* __restrict__ ad,
-                                                                float* __restrict__ y, int N, int nb, int B) {
-    __shared__ __align__(16) uint8_t s_raw[kRows * kUnit];             // raw Q4_0 blocks [row][8 blocks]
-    __shared__ __align__(16) uint8_t s_exp[kChunk * kRows * 32];       // int8 (q-8) [block][row][32]
-    __shared__ float s_dw[kChunk * kRows];                             // weight scales [block][row]
-    __shared__ __align__(16) uint8_t s_act[kChunk * kToks * 32];       // int8 activations [block][token][32]
-    __shared__ __align__(16) float s_da[kChunk * kToks];               // activation scales [block][token]
+template <int TG>
+struct ChunkRegs {
+    uint4 w[3];           // raw weight pieces l, l+64, l+128
+    long a[TG][kChunk];   // A operands: token group g, block j
+    float4 d;             // activation scales of 16*TG tokens x 8 blocks
+};
 
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+// TG token groups of 16 per wave: TG = 1 gives twice the waves (small
+// batches, where the per-wave chain length bounds the time), TG = 2 shares
+// each expanded weight operand between two MFMAs.
+template <int TG>
+__global__ __launch_bounds__(64) void gemm_q4_0_q8_mfma_kernel(const uint8_t* __restrict__ W,
+                                                               const int8_t* __restrict__ aq,
+                                                               const float* __restrict__ ad,
+                                                               float* __restrict__ y, int N, int nb, int B) {
+    constexpr int kToks = 16 * TG;
+    __shared__ __align__(16) uint8_t s_raw[kRows * kUnit];        // raw blocks [row][8 blocks]
+    __shared__ __align__(16) uint8_t s_exp[kChunk * kRows * 32];  // int8 (q-8) [block][row][32]
+    __shared__ float s_dw[kChunk * kRows];                        // weight scales [block][row]
+    __shared__ __align__(16) float s_da[kChunk * kToks];          // activation scales [block][token]
+
+    const int l = threadIdx.x, li = l & 15, h = l >> 4;
     const int r0 = blockIdx.x * kRows, t0 = blockIdx.y * kToks;
     const size_t row_bytes = static_cast<size_t>(nb) * 18, K = static_cast<size_t>(nb) * 32;
     const int nchunks = nb / kChunk;
 
-    // global -> register prefetch of one chunk (two register sets: chunks
-    // c+1 and c+2 are in flight while chunk c is expanded and summed)
-    struct Regs {
-        uint4 w[2], a[2];
-        float d;
-    };
-    auto fetch = [&](Regs& r, int c) {
+    auto fetch = [&](ChunkRegs<TG>& r, int c) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = t + i * kGT;
-            if (idx < kWPieces) {
-                const int row = min(r0 + idx / 9, N - 1), piece = idx % 9;
+        for (int i = 0; i < 3; ++i) {
+            const int p = l + 64 * i;
+            if (p < kWPieces) {
+                const int row = min(r0 + p / 9, N - 1);
                 r.w[i] = ld_global16(W + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(c) * kUnit +
-                                     piece * 16);
+                                     (p % 9) * 16);
             }
-            const int tok = min(t0 + idx / 16, B - 1), piece = idx % 16;
-            r.a[i] = ld_global16(aq + static_cast<size_t>(tok) * K + static_cast<size_t>(c) * 256 + piece * 16);
         }
-        const int tok = min(t0 + t / kChunk, B - 1);
-        r.d = ad[static_cast<size_t>(tok) * nb + c * kChunk + t % kChunk];
-    };
-    auto store = [&](const Regs& r) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = t + i * kGT;
-            if (idx < kWPieces) *reinterpret_cast<uint4*>(s_raw + (idx / 9) * kUnit + (idx % 9) * 16) = r.w[i];
-            const int tok = idx >> 4, piece = idx & 15;  // piece p = block p/2, half p%2
-            *reinterpret_cast<uint4*>(s_act + ((piece >> 1) * kToks + tok) * 32 + (piece & 1) * 16) = r.a[i];
+        for (int g = 0; g < TG; ++g) {
+            const int tok = min(t0 + 16 * g + li, B - 1);
+            const int8_t* base = aq + static_cast<size_t>(tok) * K + static_cast<size_t>(c) * 256 + 8 * h;
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) r.a[g][j] = *reinterpret_cast<const long*>(base + 32 * j);
         }
-        s_da[(t % kChunk) * kToks + t / kChunk] = r.d;
+        // lane -> (token l/2, blocks 4*(l%2) .. +3); TG = 1 uses lanes 0..31
+        const int tok = min(t0 + min(l >> 1, kToks - 1), B - 1);
+        r.d = *reinterpret_cast<const float4*>(ad + static_cast<size_t>(tok) * nb + c * kChunk + 4 * (l & 1));
     };
 
-    // MFMA lane roles: token group tg, row group rg; operand index i = lane & 15,
-    // k group h = lane >> 4 (elements 8h .. 8h+7 of a block)
-    const int rg = w >> 1, tg = w & 1, li = lane & 15, h = lane >> 4;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[TG][4];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.f;
 
-    // one chunk, its data already in LDS: expand, then MFMA + chains
-    auto compute = [&]() {
-        {
-            // expand (row, block) = (t % 32, t / 32) to int8 (q - 8)
-            const int row = t & 31, j = t >> 5;
-            const uint8_t* blk = s_raw + row * kUnit + 18 * j;
+    auto compute = [&](const ChunkRegs<TG>& r) {
+        // stage the raw bytes and the scales (LDS operations of one wave are
+        // performed in order, so the reads below see these writes)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int p = l + 64 * i;
+            if (p < kWPieces) *reinterpret_cast<uint4*>(s_raw + (p / 9) * kUnit + (p % 9) * 16) = r.w[i];
+        }
+        if ((l >> 1) < kToks) {
+            const int tok = l >> 1, j0 = 4 * (l & 1);
+            s_da[(j0 + 0) * kToks + tok] = r.d.x;
+            s_da[(j0 + 1) * kToks + tok] = r.d.y;
+            s_da[(j0 + 2) * kToks + tok] = r.d.z;
+            s_da[(j0 + 3) * kToks + tok] = r.d.w;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // expand (row li, blocks h and h+4) to int8 (q - 8)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int j = h + 4 * jj;
+            const uint8_t* blk = s_raw + li * kUnit + 18 * j;
             uint32_t q[4], dbits;
             if ((j & 1) == 0) {  // block starts 4-byte aligned: d in bytes 0-1, qs from byte 2
                 const uint32_t* p = reinterpret_cast<const uint32_t*>(blk);
@@ -126,57 +138,61 @@ __global__ __launch_bounds__(kGT) void gemm_q4_0_q8_mfma_kernel(const uint8_t* _
             hi.y = nib_to_s8((q[1] >> 4) & 0x0f0f0f0fu);
             hi.z = nib_to_s8((q[2] >> 4) & 0x0f0f0f0fu);
             hi.w = nib_to_s8((q[3] >> 4) & 0x0f0f0f0fu);
-            uint4* dst = reinterpret_cast<uint4*>(s_exp + (j * kRows + row) * 32);
+            uint4* dst = reinterpret_cast<uint4*>(s_exp + (j * kRows + li) * 32);
             dst[0] = lo;
             dst[1] = hi;
-            s_dw[j * kRows + row] = h2f(dbits);
+            s_dw[j * kRows + li] = h2f(dbits);
         }
-        __syncthreads();
-        const int wrow = 16 * rg + li, atok = 16 * tg + li;
-        // all eight block MFMAs first (independent, back to back), then the
-        // per-block fma chain in block order on their finished results
-        v4i isum[kChunk];
+        __builtin_amdgcn_wave_barrier();
+        // four blocks at a time: their MFMAs back to back, then the chains
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            const long bop = *reinterpret_cast<const long*>(s_exp + (j * kRows + wrow) * 32 + 8 * h);
-            const long aop = *reinterpret_cast<const long*>(s_act + (j * kToks + atok) * 32 + 8 * h);
-            isum[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, v4i{0, 0, 0, 0}, 0, 0, 0);
-        }
+        for (int half = 0; half < kChunk; half += 4) {
+            v4i is[TG][4];
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            const float dw = s_dw[j * kRows + wrow];
-            const float4 da = *reinterpret_cast<const float4*>(s_da + j * kToks + 16 * tg + 4 * h);
-            acc[0] = fmaf(dw * da.x, static_cast<float>(isum[j][0]), acc[0]);
-            acc[1] = fmaf(dw * da.y, static_cast<float>(isum[j][1]), acc[1]);
-            acc[2] = fmaf(dw * da.z, static_cast<float>(isum[j][2]), acc[2]);
-            acc[3] = fmaf(dw * da.w, static_cast<float>(isum[j][3]), acc[3]);
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = half + jj;
+                const long bop = *reinterpret_cast<const long*>(s_exp + (j * kRows + li) * 32 + 8 * h);
+#pragma unroll
+                for (int g = 0; g < TG; ++g)
+                    is[g][jj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(r.a[g][j], bop, v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = half + jj;
+                const float dw = s_dw[j * kRows + li];
+#pragma unroll
+                for (int g = 0; g < TG; ++g) {
+                    const float4 da = *reinterpret_cast<const float4*>(s_da + j * kToks + 16 * g + 4 * h);
+                    acc[g][0] = fmaf(dw * da.x, static_cast<float>(is[g][jj][0]), acc[g][0]);
+                    acc[g][1] = fmaf(dw * da.y, static_cast<float>(is[g][jj][1]), acc[g][1]);
+                    acc[g][2] = fmaf(dw * da.z, static_cast<float>(is[g][jj][2]), acc[g][2]);
+                    acc[g][3] = fmaf(dw * da.w, static_cast<float>(is[g][jj][3]), acc[g][3]);
+                }
+            }
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
     };
 
-    Regs ra, rb;
+    ChunkRegs<TG> ra, rb;
     fetch(ra, 0);
-    if (nchunks > 1) fetch(rb, 1);
     for (int c = 0; c < nchunks; c += 2) {
-        store(ra);
-        __syncthreads();
-        if (c + 2 < nchunks) fetch(ra, c + 2);
-        compute();
+        if (c + 1 < nchunks) fetch(rb, c + 1);
+        compute(ra);
         if (c + 1 >= nchunks) break;
-        store(rb);
-        __syncthreads();
-        if (c + 3 < nchunks) fetch(rb, c + 3);
-        compute();
+        if (c + 2 < nchunks) fetch(ra, c + 2);
+        compute(rb);
     }
 
-    // lane holds outputs (token 16*tg + 4h + v, row 16*rg + li)
-    const int orow = r0 + 16 * rg + li;
+    // lane holds (token 16g + 4h + v, row li) of each token group g
+    const int orow = r0 + li;
     if (orow < N) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int tok = t0 + 16 * tg + 4 * h + v;
-            if (tok < B) y[static_cast<size_t>(tok) * N + orow] = acc[v];
-        }
+        for (int g = 0; g < TG; ++g)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int tk = t0 + 16 * g + 4 * h + v;
+                if (tk < B) y[static_cast<size_t>(tk) * N + orow] = acc[g][v];
+            }
     }
 }
 
@@ -188,9 +204,14 @@ hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const fl
                                     size_t cols, size_t batch, hipStream_t st) {
     if (!rows || !batch) return hipSuccess;
     if (!gemm_q4_0_mfma_ok(cols)) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<unsigned>((rows + kRows - 1) / kRows), static_cast<unsigned>((batch + kToks - 1) / kToks));
-    gemm_q4_0_q8_mfma_kernel<<<grid, kGT, 0, st>>>(W, aq, ad, y, static_cast<int>(rows), static_cast<int>(cols / 32),
-                                                   static_cast<int>(batch));
+    const unsigned gx = static_cast<unsigned>((rows + kRows - 1) / kRows);
+    if (batch <= 32) {  // short chains per wave matter more than operand sharing
+        gemm_q4_0_q8_mfma_kernel<1><<<dim3(gx, static_cast<unsigned>((batch + 15) / 16)), 64, 0, st>>>(
+            W, aq, ad, y, static_cast<int>(rows), static_cast<int>(cols / 32), static_cast<int>(batch));
+    } else {
+        gemm_q4_0_q8_mfma_kernel<2><<<dim3(gx, static_cast<unsigned>((batch + 31) / 32)), 64, 0, st>>>(
+            W, aq, ad, y, static_cast<int>(rows), static_cast<int>(cols / 32), static_cast<int>(batch));
+    }
     return hipGetLastError();
 }
 

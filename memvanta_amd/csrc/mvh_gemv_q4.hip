@@ -235,10 +235,23 @@ hipError_t launch_gemv_q4_0_persistent(const uint8_t* W, const float* x, const i
         gemv_q4_0_persistent<true, T><<<grid, T, lds, st>>>(W, x, nullptr, nullptr, y, static_cast<int>(rows), nb,
                                                             ntiles);
     } else {
-        constexpr int T = 256;
-        const int grid = (waves + T / 64 - 1) / (T / 64);
-        gemv_q4_0_persistent<false, T><<<grid, T, lds, st>>>(W, nullptr, aq, ad, y, static_cast<int>(rows), nb,
-                                                             ntiles);
+        // workgroup size (tuning override): every workgroup stages the
+        // activation once, so larger groups stage it fewer times
+        static const int wg = [] {
+            const char* e = getenv("MVH_GEMV_WG");
+            const int v = e ? atoi(e) : 256;
+            return v == 512 || v == 1024 ? v : 256;
+        }();
+        const int grid = (waves + wg / 64 - 1) / (wg / 64);
+        if (wg == 1024)
+            gemv_q4_0_persistent<false, 1024><<<grid, 1024, lds, st>>>(W, nullptr, aq, ad, y, static_cast<int>(rows),
+                                                                       nb, ntiles);
+        else if (wg == 512)
+            gemv_q4_0_persistent<false, 512><<<grid, 512, lds, st>>>(W, nullptr, aq, ad, y, static_cast<int>(rows),
+                                                                     nb, ntiles);
+        else
+            gemv_q4_0_persistent<false, 256><<<grid, 256, lds, st>>>(W, nullptr, aq, ad, y, static_cast<int>(rows),
+                                                                     nb, ntiles);
     }
     return hipGetLastError();
 }
