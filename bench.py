@@ -305,6 +305,9 @@ def main():
         per_shape = [{"shape": f"{k}->{n}", "us": round(us[(k, n)], 2),
                       "GB/s": round(gemv_bytes(k, n) / us[(k, n)] / 1e3, 1)} for k, n in ISOLATED_GEMVS]
 
+        # batched prefill GEMM (int8 MFMA) at the GEMM config shapes
+        gemm = time_prefill_gemm(10)
+
         traffic = None
         pmc = os.path.join(ROOT, "profiles", "gemv_q4_0_7b_decode_traffic.json")
         if os.path.exists(pmc):
@@ -353,6 +356,9 @@ def main():
                       "device synchronizations; pp: host-driven chunks, wall clock",
             "vs_baseline_basis": "published reference tg128 1.52 tok/s (real OpenLLaMA-7B-v2 Q4_0, CPU, 4 threads)",
             "gemv_kernel_per_shape": per_shape,
+            "prefill_gemm_int8_mfma": gemm,
+            "prefill_gemm_note": "tensor_matmul_batch_v06 FORCE_Q8 numerics incl. the activation quantizer; "
+                                 "frac_int8_peak vs 5 POP/s dense int8",
         },
         "roofline": {"bound": "hbm", "kernel": "gemv_q4_0 (persistent, pre-quantized Q8 input)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
