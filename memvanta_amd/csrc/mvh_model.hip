@@ -50,47 +50,67 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t
 // the reference's element order; the two can differ only when the exact sum
 // of squares lies within ~1e-15 (relative) of an f32 rounding boundary of ss/D.
 constexpr int kNormT = 1024;
+constexpr int kNormV = 4;  // float4s per thread: D <= 16384, all held in registers
 __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                          const float* __restrict__ w, float* __restrict__ n,
                                                          int8_t* __restrict__ q, float* __restrict__ qd, int D,
                                                          float eps) {
     __shared__ double red[kNormT / 64];
     const size_t row = blockIdx.x;
+    const int t = threadIdx.x;
     float4* xr = reinterpret_cast<float4*>(x + row * D);
     const float4* ar = add ? reinterpret_cast<const float4*>(add + row * D) : nullptr;
+    const float4* w4 = reinterpret_cast<const float4*>(w);
     const int D4 = D / 4;
-    double ss = 0.0;
-    for (int i = threadIdx.x; i < D4; i += kNormT) {
-        float4 v = xr[i];
-        if (ar) {
-            const float4 a = ar[i];
-            v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
-            xr[i] = v;
+    // one memory round trip: x, the residual and the norm weights together
+    float4 v[kNormV], g[kNormV], a[kNormV];
+#pragma unroll
+    for (int k = 0; k < kNormV; ++k) {
+        const int i = t + k * kNormT;
+        v[k] = g[k] = a[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < D4) {
+            v[k] = xr[i];
+            g[k] = w4[i];
+            if (ar) a[k] = ar[i];
         }
-        ss = fma(static_cast<double>(v.x), static_cast<double>(v.x), ss);
-        ss = fma(static_cast<double>(v.y), static_cast<double>(v.y), ss);
-        ss = fma(static_cast<double>(v.z), static_cast<double>(v.z), ss);
-        ss = fma(static_cast<double>(v.w), static_cast<double>(v.w), ss);
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < kNormV; ++k) {
+        const int i = t + k * kNormT;
+        if (i >= D4) continue;
+        if (ar) {
+            v[k] = make_float4(v[k].x + a[k].x, v[k].y + a[k].y, v[k].z + a[k].z, v[k].w + a[k].w);
+            xr[i] = v[k];
+        }
+        ss = fma(static_cast<double>(v[k].x), static_cast<double>(v[k].x), ss);
+        ss = fma(static_cast<double>(v[k].y), static_cast<double>(v[k].y), ss);
+        ss = fma(static_cast<double>(v[k].z), static_cast<double>(v[k].z), ss);
+        ss = fma(static_cast<double>(v[k].w), static_cast<double>(v[k].w), ss);
     }
     ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
     ss = red[0];
 #pragma unroll
     for (int k = 1; k < kNormT / 64; ++k) ss += red[k];
     const float inv = __fdiv_rn(1.0f, sqrt_rn(static_cast<float>(ss / static_cast<double>(D)) + eps));
-    const float4* w4 = reinterpret_cast<const float4*>(w);
     float4* nr = reinterpret_cast<float4*>(n + row * D);
-    for (int i = threadIdx.x; i < D4; i += kNormT) {  // D4 % 8 == 0: 8-lane groups are whole blocks
-        const float4 v = xr[i], g = w4[i];
-        const float4 o = make_float4((v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z, (v.w * inv) * g.w);
-        nr[i] = o;
+#pragma unroll
+    for (int k = 0; k < kNormV; ++k) {
+        const int i = t + k * kNormT;
+        if (k * kNormT >= D4) break;  // uniform; D4 % 8 == 0: 8-lane groups are whole blocks
+        const float4 o = make_float4((v[k].x * inv) * g[k].x, (v[k].y * inv) * g[k].y, (v[k].z * inv) * g[k].z,
+                                     (v[k].w * inv) * g[k].w);
+        if (i < D4) nr[i] = o;
         if (q) {
             float d;
             int s;
             const uint32_t packed = quantize_q8_x4(o, d, s);
-            reinterpret_cast<uint32_t*>(q + row * D)[i] = packed;
-            if ((i & 7) == 0) qd[row * (D / 32) + (i >> 3)] = d;
+            if (i < D4) {
+                reinterpret_cast<uint32_t*>(q + row * D)[i] = packed;
+                if ((i & 7) == 0) qd[row * (D / 32) + (i >> 3)] = d;
+            }
         }
     }
 }
@@ -176,11 +196,20 @@ __global__ __launch_bounds__(kArgT) void argmax_kernel(const float* __restrict__
     const float* l = logits + static_cast<size_t>(blockIdx.x) * V;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < V; i += kArgT) {
-        const float v = l[i];
-        if (v > best || bi == 0x7fffffff) {  // indices increase: strict > keeps the first max
-            best = v;
-            bi = i;
+    for (int i0 = threadIdx.x; i0 < V; i0 += 8 * kArgT) {  // eight loads in flight per thread
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = i0 + k * kArgT;
+            v[k] = i < V ? l[i] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = i0 + k * kArgT;
+            if (i < V && (v[k] > best || bi == 0x7fffffff)) {  // indices increase: strict > keeps the first max
+                best = v[k];
+                bi = i;
+            }
         }
     }
     auto better = [](float v, int i, float bv, int bj) { return v > bv || (v == bv && i < bj); };
@@ -225,6 +254,7 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
                           size_t D, float eps, hipStream_t st) {
     if (!B) return hipSuccess;
+    if (D % 32 || D > static_cast<size_t>(4 * kNormT * kNormV)) return hipErrorInvalidValue;
     rmsnorm_kernel<<<static_cast<unsigned>(B), kNormT, 0, st>>>(x, add, w, n, q, qd, static_cast<int>(D), eps);
     return hipGetLastError();
 }

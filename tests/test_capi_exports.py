@@ -26,3 +26,31 @@ def test_version_and_error_channel():
     assert b"null tensor" in lib.mvh_last_error()
     n = ctypes.c_size_t()
     assert lib.mvh_kv_bytes_allocated(None, ctypes.byref(n)) == 1
+
+
+def test_header_compiles_as_c_and_links(tmp_path):
+    """A plain C program (what a cgo / C++ shim sees) compiles against the
+    header alone and links against the library; no call touches a device."""
+    import os
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = tmp_path / "use_abi.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include "memvanta_hip.h"
+int main(void) {
+    size_t bytes = 0;
+    if (mvh_version() < 1) return 1;
+    if (mvh_kv_bytes_allocated(NULL, &bytes) != MVH_E_INVALID) return 2;
+    if (!mvh_last_error()[0]) return 3;
+    puts("ok");
+    return 0;
+}
+''')
+    exe = tmp_path / "use_abi"
+    lib_dir = os.path.join(root, "memvanta_amd")
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(root, "include"), str(src), "-o", str(exe),
+                    "-L", lib_dir, "-lmemvanta_hip", "-Wl,-rpath," + lib_dir], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    assert out.strip() == "ok"
