@@ -464,9 +464,11 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
     if (act_mode == MVH_ACT_Q8) {
         if (w->type == MVH_TYPE_Q4_0) {
             ActView a;
-            if (int rc = act_buffers(c, batch, cols, &a)) return rc;
-            MVH_HIP(mvh::launch_quantize_q8(xd, a.q, a.d, a.s, batch, cols, c->stream));
-            if (mvh::gemm_q4_0_mfma_ok(cols)) {  // int8 MFMA tiles, same per-block chain
+            const bool mfma = mvh::gemm_q4_0_mfma_ok(cols);  // int8 MFMA tiles, same per-block chain
+            // the MFMA path takes the activations in its operand order (whole 16-token slabs)
+            if (int rc = act_buffers(c, mfma ? mvh::q8_op_bytes(batch, cols) / cols : batch, cols, &a)) return rc;
+            MVH_HIP(mvh::launch_quantize_q8(xd, a.q, a.d, a.s, batch, cols, c->stream, mfma));
+            if (mfma) {
                 MVH_HIP(mvh::launch_gemm_q4_0_q8_mfma(W, a.q, a.d, yd, rows, cols, batch, c->stream));
             } else {
                 for (size_t b = 0; b < batch; ++b)

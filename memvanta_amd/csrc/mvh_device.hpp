@@ -151,4 +151,15 @@ __device__ __forceinline__ uint32_t align16(uint32_t hi, uint32_t lo) {
     return __builtin_amdgcn_alignbyte(hi, lo, 2);
 }
 
+// Q8 activations of B tokens x K elements (K % 256 == 0) in the operand
+// order of the prefill GEMM's int8 MFMA: 16-token slabs; within a slab, per
+// 256-element chunk, per block j and 8-byte quarter h, the 16 tokens' bytes
+// 8h .. 8h+7 of block j -- the A operand of one v_mfma_i32_16x16x32_i8 as 512
+// contiguous bytes.  Four consecutive elements (k % 4 == 0) stay contiguous.
+__host__ __device__ constexpr size_t q8_op_offset(size_t t, size_t k, size_t K) {
+    return (t / 16) * 16 * K + (k / 256) * 4096 + ((k % 256) / 32 * 4 + (k % 32) / 8) * 128 + (t % 16) * 8 + k % 8;
+}
+// bytes of that layout for B tokens (the last slab is whole)
+__host__ __device__ constexpr size_t q8_op_bytes(size_t B, size_t K) { return (B + 15) / 16 * 16 * K; }
+
 }  // namespace mvh

@@ -8,7 +8,10 @@ namespace mvh {
 enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ6_K = 14 };
 
 // ---- activation quantization / conversions (mvh_quant.hip) ----
-hipError_t launch_quantize_q8(const float* x, int8_t* q, float* d, int* s, size_t rows, size_t cols, hipStream_t st);
+// q_op: q in the prefill GEMM's operand order (q8_op_offset; cols % 256 == 0,
+// q8_op_bytes(rows, cols) bytes), else row-major
+hipError_t launch_quantize_q8(const float* x, int8_t* q, float* d, int* s, size_t rows, size_t cols, hipStream_t st,
+                              bool q_op = false);
 hipError_t launch_f2h(const float* x, uint16_t* out, size_t n, hipStream_t st);
 hipError_t launch_f2h_bits(uint32_t first, uint16_t* out, size_t n, hipStream_t st);
 hipError_t launch_h2f(const uint16_t* h, float* out, size_t n, hipStream_t st);
@@ -37,8 +40,9 @@ hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x,
 
 // ---- batched prefill on int8 MFMA (mvh_gemm_q4.hip) ----
 // y[b*rows + r] = dot_q4_q8(W row r, Q8 activation row b) for b < batch
-// (MEMVANTA_FORCE_Q8_ACT numerics); aq [batch][cols] int8 (16-byte aligned
-// rows), ad [batch][cols/32]; needs cols % 256 == 0.
+// (MEMVANTA_FORCE_Q8_ACT numerics); aq in operand order (q8_op_offset,
+// q8_op_bytes(batch, cols) bytes, as launch_quantize_q8 with q_op writes it),
+// ad [batch][cols/32]; needs cols % 256 == 0.
 bool gemm_q4_0_mfma_ok(size_t cols);
 hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows,
                                     size_t cols, size_t batch, hipStream_t st);
@@ -71,7 +75,7 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
                         hipStream_t st);
 // x += add (if add), n = rmsnorm(x)*w, and q/qd = Q8 of n (if q); B rows of D
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
-                          size_t D, float eps, hipStream_t st);
+                          size_t D, float eps, hipStream_t st, bool q_op = false);
 // q/k/v of token b at q + b*q_pitch, k + b*kv_pitch, v + b*kv_pitch
 hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, size_t kv_pitch, const float* cos_t,
                           const float* sin_t, const int* d_pos, size_t pos0, size_t B, size_t n_head, size_t n_kv,
@@ -79,7 +83,7 @@ hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, si
                           hipStream_t st);
 // B rows: g/u row b at g + b*pitch, u + b*pitch; ff/q rows of F
 hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff, int8_t* q, float* qd, size_t B,
-                         size_t F, hipStream_t st);
+                         size_t F, hipStream_t st, bool q_op = false);
 hipError_t launch_argmax(const float* logits, size_t V, size_t B, int* out, int* d_pos, int* hist, hipStream_t st);
 
 }  // namespace mvh

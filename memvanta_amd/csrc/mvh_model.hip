@@ -45,8 +45,9 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t
 
 // x += add (when add != null), then LlamaModel::rmsnorm (src/llama_model.cpp:237):
 // ss = sum of x*x in double, inv = 1/sqrtf(float(ss/D) + eps), n = (x*inv)*w;
-// optionally also the Q8 activation of n (quantize_q8, bit-exact).  One
-// workgroup per row; D % 32 == 0.  The double sum is added as a tree, not in
+// optionally also the Q8 activation of n (quantize_q8, bit-exact; row-major,
+// or in the prefill GEMM's operand order when q_op).  One workgroup per row;
+// D % 32 == 0 (D % 256 == 0 with q_op).  The double sum is added as a tree, not in
 // the reference's element order; the two can differ only when the exact sum
 // of squares lies within ~1e-15 (relative) of an f32 rounding boundary of ss/D.
 constexpr int kNormT = 1024;
@@ -54,7 +55,7 @@ constexpr int kNormV = 4;  // float4s per thread: D <= 16384, all held in regist
 __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                          const float* __restrict__ w, float* __restrict__ n,
                                                          int8_t* __restrict__ q, float* __restrict__ qd, int D,
-                                                         float eps) {
+                                                         float eps, bool q_op) {
     __shared__ double red[kNormT / 64];
     const size_t row = blockIdx.x;
     const int t = threadIdx.x;
@@ -108,7 +109,10 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
             int s;
             const uint32_t packed = quantize_q8_x4(o, d, s);
             if (i < D4) {
-                reinterpret_cast<uint32_t*>(q + row * D)[i] = packed;
+                if (q_op)
+                    *reinterpret_cast<uint32_t*>(q + q8_op_offset(row, 4 * static_cast<size_t>(i), D)) = packed;
+                else
+                    reinterpret_cast<uint32_t*>(q + row * D)[i] = packed;
                 if ((i & 7) == 0) qd[row * (D / 32) + (i >> 3)] = d;
             }
         }
@@ -153,11 +157,13 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int
 }
 
 // SwiGLU (src/llama_model.cpp:249,257): ff = (g/(1+expf(-g)))*u, with expf as
-// the C library computes it; optionally the Q8 activation of ff.  Row b of
-// g/u at g + b*pitch, u + b*pitch; ff and q rows are F long.  F % 32 == 0.
+// the C library computes it; optionally the Q8 activation of ff (row-major,
+// or in the prefill GEMM's operand order when q_op).  Row b of g/u at
+// g + b*pitch, u + b*pitch; ff and q rows are F long.  F % 32 == 0
+// (F % 256 == 0 with q_op).
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                      int pitch, float* __restrict__ ff, int8_t* __restrict__ q,
-                                                     float* __restrict__ qd, int F) {
+                                                     float* __restrict__ qd, int F, bool q_op) {
     __shared__ uint64_t s_tab[32];
     const int i = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
     const int n4 = F / 4;
@@ -179,7 +185,10 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
         int s;
         const uint32_t packed = quantize_q8_x4(o, d, s);
         if (live) {
-            reinterpret_cast<uint32_t*>(q + static_cast<size_t>(b) * F)[i] = packed;
+            if (q_op)
+                *reinterpret_cast<uint32_t*>(q + q8_op_offset(b, 4 * static_cast<size_t>(i), F)) = packed;
+            else
+                reinterpret_cast<uint32_t*>(q + static_cast<size_t>(b) * F)[i] = packed;
             if ((i & 7) == 0) qd[static_cast<size_t>(b) * (F / 32) + (i >> 3)] = d;
         }
     }
@@ -252,10 +261,11 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
 }
 
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
-                          size_t D, float eps, hipStream_t st) {
+                          size_t D, float eps, hipStream_t st, bool q_op) {
     if (!B) return hipSuccess;
-    if (D % 32 || D > static_cast<size_t>(4 * kNormT * kNormV)) return hipErrorInvalidValue;
-    rmsnorm_kernel<<<static_cast<unsigned>(B), kNormT, 0, st>>>(x, add, w, n, q, qd, static_cast<int>(D), eps);
+    if (D % 32 || D > static_cast<size_t>(4 * kNormT * kNormV) || (q_op && D % 256)) return hipErrorInvalidValue;
+    rmsnorm_kernel<<<static_cast<unsigned>(B), kNormT, 0, st>>>(x, add, w, n, q, qd, static_cast<int>(D), eps,
+                                                                q && q_op);
     return hipGetLastError();
 }
 
@@ -273,11 +283,12 @@ hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, si
 }
 
 hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff, int8_t* q, float* qd, size_t B,
-                         size_t F, hipStream_t st) {
+                         size_t F, hipStream_t st, bool q_op) {
     const size_t n4 = F / 4;
     if (!n4 || !B) return hipSuccess;
+    if (q_op && F % 256) return hipErrorInvalidValue;
     swiglu_kernel<<<dim3(static_cast<unsigned>((n4 + 255) / 256), static_cast<unsigned>(B)), 256, 0, st>>>(
-        g, u, static_cast<int>(pitch), ff, q, qd, static_cast<int>(F));
+        g, u, static_cast<int>(pitch), ff, q, qd, static_cast<int>(F), q && q_op);
     return hipGetLastError();
 }
 

@@ -5,9 +5,12 @@ namespace mvh {
 
 // quantize_q8 (src/gguf_kernels.cpp:160-172), one 32-element block per 8
 // lanes, 4 elements per lane (one 16-byte load, one 4-byte store).  Besides q
-// and the f32 scale d it writes s = sum of the 32 q values.
+// and the f32 scale d it writes s = sum of the 32 q values.  With op_cols != 0
+// q is written in the prefill GEMM's operand order (q8_op_offset, rows of
+// op_cols elements) instead of row-major.
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float4* __restrict__ x, uint32_t* __restrict__ q,
-                                                          float* __restrict__ d, int* __restrict__ s, size_t n4) {
+                                                          float* __restrict__ d, int* __restrict__ s, size_t n4,
+                                                          int op_cols) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const bool live = i < n4;  // n4 % 8 == 0, so an 8-lane group is all-live or all-dead
     const float4 v = live ? x[i] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -15,7 +18,12 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float4* __restri
     int bsum;
     const uint32_t packed = quantize_q8_x4(v, dd, bsum);
     if (live) {
-        q[i] = packed;
+        if (op_cols) {
+            const size_t K = static_cast<size_t>(op_cols);
+            q[q8_op_offset(4 * i / K, 4 * i % K, K) / 4] = packed;
+        } else {
+            q[i] = packed;
+        }
         if ((threadIdx.x & 7) == 0) {
             d[i >> 3] = dd;
             s[i >> 3] = bsum;
@@ -78,13 +86,14 @@ hipError_t launch_read_row(uint32_t type, const uint8_t* W, size_t cols, size_t 
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_q8(const float* x, int8_t* q, float* d, int* s, size_t rows, size_t cols,
-                              hipStream_t st) {
+hipError_t launch_quantize_q8(const float* x, int8_t* q, float* d, int* s, size_t rows, size_t cols, hipStream_t st,
+                              bool q_op) {
     const size_t n4 = rows * cols / 4;
     if (!n4) return hipSuccess;
+    if (q_op && cols % 256) return hipErrorInvalidValue;
     const unsigned grid = static_cast<unsigned>((n4 + 255) / 256);
     quantize_q8_kernel<<<grid, 256, 0, st>>>(reinterpret_cast<const float4*>(x), reinterpret_cast<uint32_t*>(q), d,
-                                             s, n4);
+                                             s, n4, q_op ? static_cast<int>(cols) : 0);
     return hipGetLastError();
 }
 

@@ -162,14 +162,14 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     ff_ = static_cast<float*>(dalloc(B * F * 4));
     scores_ = static_cast<float*>(dalloc(B * c_.n_head * c_.n_ctx * 4));
     logits_d_ = static_cast<float*>(dalloc(c_.vocab * 4));
-    q8_ = static_cast<int8_t*>(dalloc(B * W));
+    q8_ = static_cast<int8_t*>(dalloc(mvh::q8_op_bytes(B, W)));  // row-major or operand order
     q8d_ = static_cast<float*>(dalloc(B * (W / 32) * 4));
     d_tok_ = static_cast<int*>(dalloc(16));
     d_hist_ = static_cast<int*>(dalloc(4 * (c_.n_ctx + 1)));
     d_pos_ = static_cast<int*>(dalloc(16));
     d_toks_ = static_cast<int*>(dalloc(B * 4));
     ffo_ = static_cast<float*>(dalloc(B * D * 4));
-    q8s_ = static_cast<int8_t*>(dalloc(B * W));
+    q8s_ = static_cast<int8_t*>(dalloc(mvh::q8_op_bytes(B, W)));
     q8sd_ = static_cast<float*>(dalloc(B * (W / 32) * 4));
     q8ss_ = static_cast<int*>(dalloc(B * (W / 32) * 4));
     check(hipHostMalloc(reinterpret_cast<void**>(&pin_), 4 * (c_.n_ctx + B + 8), hipHostMallocDefault),
@@ -280,8 +280,11 @@ void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const f
     check(e, w.sname.c_str());
 }
 
+bool LlamaModel::mfma_gemm(const Tensor& w) { return w.type == 2 && mvh::gemm_q4_0_mfma_ok(w.cols); }
+
 // tensor_matmul_batch_v06 numerics (src/gguf_kernels.cpp:261-271) over B rows
-void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B) {
+void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B,
+                      bool q8_op) {
     const auto* W = static_cast<const uint8_t*>(w.d);
     const std::size_t rows = w.rows, cols = w.cols, nb = cols / 32;
     hipError_t e = hipSuccess;
@@ -292,11 +295,13 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
     } else if (mode_ == PrefillMode::Q8) {
         if (w.type == 2) {
             if (!q8) {
-                e = mvh::launch_quantize_q8(x, q8s_, q8sd_, q8ss_, B, cols, stream_);
+                q8_op = mfma_gemm(w);
+                e = mvh::launch_quantize_q8(x, q8s_, q8sd_, q8ss_, B, cols, stream_, q8_op);
                 q8 = q8s_;
                 q8d = q8sd_;
             }
-            if (e == hipSuccess && mvh::gemm_q4_0_mfma_ok(cols)) {
+            if (q8_op && !mfma_gemm(w)) throw std::logic_error("operand-order activations for a non-MFMA tensor: " + w.sname);
+            if (e == hipSuccess && q8_op) {
                 e = mvh::launch_gemm_q4_0_q8_mfma(W, q8, q8d, y, rows, cols, B, stream_);
             } else {
                 for (std::size_t b = 0; b < B && e == hipSuccess; ++b)
@@ -386,15 +391,21 @@ void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
     for (std::size_t li = 0; li < c_.n_layer; ++li) {
         auto& L = layers_[li];
         const auto lay = qkv_layout(L, B);
+        // the norm / SwiGLU kernels write the Q8 activations in the MFMA
+        // GEMM's operand order when every consumer of them is that GEMM
+        const bool op_qkv = q8mode && (L.fused_qkv ? mfma_gemm(L.qkv)
+                                                   : mfma_gemm(L.q) && mfma_gemm(L.k) && mfma_gemm(L.v));
+        const bool op_gu = q8mode && (L.fused_gu ? mfma_gemm(L.gate_up) : mfma_gemm(L.gate) && mfma_gemm(L.up));
+        const bool op_down = q8mode && mfma_gemm(L.down);
         check(mvh::launch_rmsnorm(x_, li ? ffo_ : nullptr, L.attn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D,
-                                  c_.rms_eps, stream_),
+                                  c_.rms_eps, stream_, op_qkv),
               "rmsnorm");
         if (L.fused_qkv) {
-            gemm(L.qkv, n_, q8mode ? q8_ : nullptr, q8d_, qkv_, B);
+            gemm(L.qkv, n_, q8mode ? q8_ : nullptr, q8d_, qkv_, B, op_qkv);
         } else {
-            gemm(L.q, n_, q8mode ? q8_ : nullptr, q8d_, lay.q, B);
-            gemm(L.k, n_, q8mode ? q8_ : nullptr, q8d_, lay.k, B);
-            gemm(L.v, n_, q8mode ? q8_ : nullptr, q8d_, lay.v, B);
+            gemm(L.q, n_, q8mode ? q8_ : nullptr, q8d_, lay.q, B, op_qkv);
+            gemm(L.k, n_, q8mode ? q8_ : nullptr, q8d_, lay.k, B, op_qkv);
+            gemm(L.v, n_, q8mode ? q8_ : nullptr, q8d_, lay.v, B, op_qkv);
         }
         uint16_t* const* pk = pt_k_ + li * max_pages_;
         uint16_t* const* pv = pt_v_ + li * max_pages_;
@@ -405,19 +416,20 @@ void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
                                c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_),
               "attention");
         gemm(L.o, att_, nullptr, nullptr, proj_, B);
-        check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D, c_.rms_eps, stream_),
+        check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D, c_.rms_eps, stream_,
+                                  op_gu),
               "rmsnorm");
         float* g = gu_;
         float* u = L.fused_gu ? gu_ + F : gu_ + B * F;
         const std::size_t pitch = L.fused_gu ? 2 * F : F;
         if (L.fused_gu) {
-            gemm(L.gate_up, n_, q8mode ? q8_ : nullptr, q8d_, gu_, B);
+            gemm(L.gate_up, n_, q8mode ? q8_ : nullptr, q8d_, gu_, B, op_gu);
         } else {
-            gemm(L.gate, n_, q8mode ? q8_ : nullptr, q8d_, g, B);
-            gemm(L.up, n_, q8mode ? q8_ : nullptr, q8d_, u, B);
+            gemm(L.gate, n_, q8mode ? q8_ : nullptr, q8d_, g, B, op_gu);
+            gemm(L.up, n_, q8mode ? q8_ : nullptr, q8d_, u, B, op_gu);
         }
-        check(mvh::launch_swiglu(g, u, pitch, ff_, q8mode ? q8_ : nullptr, q8d_, B, F, stream_), "swiglu");
-        gemm(L.down, ff_, q8mode ? q8_ : nullptr, q8d_, ffo_, B);
+        check(mvh::launch_swiglu(g, u, pitch, ff_, q8mode ? q8_ : nullptr, q8d_, B, F, stream_, op_down), "swiglu");
+        gemm(L.down, ff_, q8mode ? q8_ : nullptr, q8d_, ffo_, B, op_down);
     }
     if (logits) {
         float* xl = x_ + (B - 1) * D;

@@ -75,7 +75,11 @@ private:
     bool upload_fused(Tensor& t, const std::vector<std::string>& names);
     float* upload_vector(const std::string& name);
     void gemv(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y);
-    void gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B);
+    // q8/q8d: the Q8 activations of x when already quantized (null: quantize
+    // here); q8_op: q8 is in the MFMA GEMM's operand order (mfma_gemm(w) holds)
+    void gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B,
+              bool q8_op = false);
+    static bool mfma_gemm(const Tensor& w);
     void decode_step(const int* d_token, bool logits, bool argmax);
     void batch_step(const int* tokens, std::size_t B, bool logits);
     void check(hipError_t e, const char* what) const;
