@@ -77,12 +77,15 @@ __device__ __forceinline__ float wave_max(float v) {
 // out[d] = fma(e_t*inv, V_t[d], out[d]) over t in order.  One wave per
 // (head, 64-wide slice of head_dim, query token); every output element's
 // value chain runs in t order in its own lane, as in the reference.  The
-// double `den` is added as a tree instead of in t order.
+// double `den` is added as a tree instead of in t order.  With q8 (hd % 32
+// == 0) the output's quantize_q8 blocks are written too, row-major or in the
+// prefill GEMM's operand order (q8_op, rows of n_head*hd).
 __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* const* __restrict__ pt_v,
                                                             const float* __restrict__ scores, float* __restrict__ out,
                                                             const int* __restrict__ d_pos, int pos_arg, int n_head,
                                                             int group, int hd, int kv_dim, int page_tokens,
-                                                            int score_pitch) {
+                                                            int score_pitch, int8_t* __restrict__ q8,
+                                                            float* __restrict__ q8d, bool q8_op) {
     extern __shared__ float s_a[];
     __shared__ uint64_t s_tab[32];
     if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
@@ -105,23 +108,35 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* cons
     for (int t = threadIdx.x; t < n; t += 64) s_a[t] = s_a[t] * inv;
     __syncthreads();
     const int d = blockIdx.y * 64 + threadIdx.x;
-    if (d >= hd) return;
+    const bool live = d < hd;
     const int kh = h / group;
     float acc = 0.0f;
-    for (int p0 = 0; p0 < n; p0 += page_tokens) {
-        const uint16_t* vp = pt_v[p0 / page_tokens] + kh * hd + d;
-        const int m = min(page_tokens, n - p0);
-        int i = 0;
-        for (; i + 8 <= m; i += 8) {
-            float vv[8];
+    if (live) {
+        for (int p0 = 0; p0 < n; p0 += page_tokens) {
+            const uint16_t* vp = pt_v[p0 / page_tokens] + kh * hd + d;
+            const int m = min(page_tokens, n - p0);
+            int i = 0;
+            for (; i + 8 <= m; i += 8) {
+                float vv[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vv[j] = h2f(vp[static_cast<size_t>(i + j) * kv_dim]);
+                for (int j = 0; j < 8; ++j) vv[j] = h2f(vp[static_cast<size_t>(i + j) * kv_dim]);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc = fmaf(s_a[p0 + i + j], vv[j], acc);
+                for (int j = 0; j < 8; ++j) acc = fmaf(s_a[p0 + i + j], vv[j], acc);
+            }
+            for (; i < m; ++i) acc = fmaf(s_a[p0 + i], h2f(vp[static_cast<size_t>(i) * kv_dim]), acc);
         }
-        for (; i < m; ++i) acc = fmaf(s_a[p0 + i], h2f(vp[static_cast<size_t>(i) * kv_dim]), acc);
     }
-    out[(static_cast<size_t>(b) * n_head + h) * hd + d] = acc;
+    const size_t o = (static_cast<size_t>(b) * n_head + h) * hd + d;
+    if (live) out[o] = acc;
+    if (q8 && live) {  // quantize_q8 of this lane's 32-element block (hd % 32 == 0): the o projection's input
+        const float mq = group_max<32>(fabsf(acc));
+        const float dq = mq > 0.0f ? __fdiv_rn(mq, 127.0f) : 1.0f;
+        const float id = __fdiv_rn(1.0f, dq);
+        const float rq = fminf(fmaxf(roundf(acc * id), -127.0f), 127.0f);
+        const int col = h * hd + d, D = n_head * hd;
+        q8[q8_op ? q8_op_offset(b, col, D) : o] = static_cast<int8_t>(rq);
+        if ((threadIdx.x & 31) == 0) q8d[o / 32] = dq;
+    }
 }
 
 
@@ -388,8 +403,10 @@ hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const f
 
 hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, size_t q_pitch,
                        float* scores, float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B,
-                       size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st) {
+                       size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st,
+                       int8_t* q8, float* q8d, bool q8_op) {
     if (!B) return hipSuccess;
+    if (q8 && (hd % 32 || !q8d || (q8_op && (n_head * hd) % 256))) return hipErrorInvalidValue;
     const int group = static_cast<int>(n_head / n_head_kv);
     const int pitch = static_cast<int>(max_pos);  // scores row pitch >= last position + 1
     const dim3 g1(static_cast<unsigned>(n_head), static_cast<unsigned>((max_pos + 63) / 64), static_cast<unsigned>(B));
@@ -404,7 +421,8 @@ hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v,
     attn_softmax_v_kernel<<<g2, 64, max_pos * sizeof(float), st>>>(pt_v, scores, out, d_pos, static_cast<int>(pos),
                                                                     static_cast<int>(n_head), group,
                                                                     static_cast<int>(hd), static_cast<int>(kv_dim),
-                                                                    static_cast<int>(page_tokens), pitch);
+                                                                    static_cast<int>(page_tokens), pitch, q8, q8d,
+                                                                    q8_op);
     return hipGetLastError();
 }
 

@@ -55,7 +55,8 @@ hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const f
 // floats, max_pos > last position
 hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, size_t q_pitch,
                        float* scores, float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B,
-                       size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st);
+                       size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st,
+                       int8_t* q8 = nullptr, float* q8d = nullptr, bool q8_op = false);
 // One decode token in one launch: RoPE of q and k at position *d_pos, the
 // F16 K/V write at that position, scores, softmax and the value sum, and
 // (when q8 != null, hd % 32 == 0) the Q8 activation of the output.  One

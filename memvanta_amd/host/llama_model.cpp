@@ -412,10 +412,16 @@ void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
         check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, nullptr, pos_,
                                   B, c_.n_head, c_.n_head_kv, hd, pk, pv, page_tokens_, stream_),
               "rope/kv");
+        // the softmax-V kernel also writes the o projection's Q8 activations
+        // (32-element head slices are Q8 blocks), in the MFMA GEMM's operand
+        // order when the projection runs there
+        const bool o_q8 = q8mode && L.o.type == 2 && hd % 32 == 0 && L.o.cols == c_.n_head * hd;
+        const bool o_op = o_q8 && mfma_gemm(L.o);
         check(mvh::launch_attn(pk, pv, lay.q, lay.q_pitch, scores_, att_, nullptr, pos_, pos_ + B, B, c_.n_head,
-                               c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_),
+                               c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_, o_q8 ? q8_ : nullptr, q8d_,
+                               o_op),
               "attention");
-        gemm(L.o, att_, nullptr, nullptr, proj_, B);
+        gemm(L.o, att_, o_q8 ? q8_ : nullptr, q8d_, proj_, B, o_op);
         check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D, c_.rms_eps, stream_,
                                   op_gu),
               "rmsnorm");
