@@ -389,6 +389,163 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     }
 }
 
+// ---- prefill chunk attention: scores + softmax once, values shared ----------
+//
+// Scores and softmax weights of query token b (grid y) and head h (grid x)
+// over positions 0..pos0+b, one workgroup: the same arithmetic as
+// attn_scores_kernel (lane-of-8 fma accumulation, t0+..+t7, / sqrtf(hd)) and
+// attn_softmax_v_kernel (mx, e = expf(s - mx), den in double, a = e *
+// float(1/den)); writes a (not s) to a[(b*n_head + h)*pitch + t].  The double
+// den is a tree over the workgroup's threads (not in t order).
+constexpr int kSM = 256;
+__global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const uint16_t* const* __restrict__ pt_k,
+                                                                  const float* __restrict__ q, int q_pitch,
+                                                                  float* __restrict__ a_out,
+                                                                  const int* __restrict__ d_pos, int pos_arg,
+                                                                  int n_head, int group, int hd, int kv_dim,
+                                                                  int page_tokens, int pitch) {
+    extern __shared__ float sm_s[];  // [hd] q, then [pitch] scores / weights
+    float* s_q = sm_s;
+    float* s_s = sm_s + hd;
+    __shared__ float red_f[kSM / 64];
+    __shared__ double red_d[kSM / 64];
+    __shared__ uint64_t s_tab[32];
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const int n = (d_pos ? *d_pos : pos_arg) + b + 1;
+    const int kh = h / group;
+    const float* qh = q + static_cast<size_t>(b) * q_pitch + static_cast<size_t>(h) * hd;
+    for (int i = t; i < hd; i += kSM) s_q[i] = qh[i];
+    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    __syncthreads();
+    const float scale = sqrt_rn(static_cast<float>(hd));
+    float mx = -INFINITY;
+    for (int tt = t; tt < n; tt += kSM) {
+        const uint16_t* krow = pt_k[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+        int c = 0;
+        for (; c + 8 <= hd; c += 8) {
+            const half8 hk = as_half8(ld_global16(krow + c));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(s_q[c + e], static_cast<float>(hk[e]), acc[e]);
+        }
+        float sum = acc[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) sum = sum + acc[e];
+        for (; c < hd; ++c) sum = fmaf(s_q[c], h2f(krow[c]), sum);
+        const float sc = __fdiv_rn(sum, scale);
+        s_s[tt] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red_f[t >> 6] = mx;
+    __syncthreads();
+    mx = red_f[0];
+#pragma unroll
+    for (int w = 1; w < kSM / 64; ++w) mx = fmaxf(mx, red_f[w]);
+    double den = 0.0;
+    for (int tt = t; tt < n; tt += kSM) {
+        const float e = mvh_expf_tabbed(s_s[tt] - mx, s_tab);
+        s_s[tt] = e;
+        den += static_cast<double>(e);
+    }
+    den = wave_sum(den);
+    if ((t & 63) == 0) red_d[t >> 6] = den;
+    __syncthreads();
+    den = red_d[0];
+#pragma unroll
+    for (int w = 1; w < kSM / 64; ++w) den += red_d[w];
+    const float inv = static_cast<float>(1.0 / den);
+    float* ar = a_out + (static_cast<size_t>(b) * n_head + h) * pitch;
+    for (int tt = t; tt < n; tt += kSM) ar[tt] = s_s[tt] * inv;
+}
+
+// Value chains of a prefill chunk: workgroup (head h, 32-element slice of
+// head_dim, group of 32 query tokens); thread = (token b, 4 consecutive
+// elements), out[d] = fma(a_t, V_t[d], out[d]) over t = 0..pos0+b in order,
+// as in the reference.  V rows come in 64-row tiles staged once in LDS for all
+// 32 tokens (the next tile's loads in flight while a tile is summed); the
+// weights of rows past a token's last position are 0 there, an exact no-op
+// (those rows are the chunk's later tokens, finite).  With q8 the output's
+// quantize_q8 blocks (one per token and slice) are written too, row-major or
+// in the prefill GEMM's operand order (q8_op).
+constexpr int kPV = 256;
+constexpr int kPVRows = 64;
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const uint16_t* const* __restrict__ pt_v,
+                                                            const float* __restrict__ a, float* __restrict__ out,
+                                                            int8_t* __restrict__ q8, float* __restrict__ q8d,
+                                                            bool q8_op, const int* __restrict__ d_pos, int pos_arg,
+                                                            int B, int n_head, int group, int hd, int kv_dim,
+                                                            int page_tokens, int pitch) {
+    __shared__ __align__(16) uint16_t s_v[kPVRows][32 + 8];     // V tile: rows x the slice's 32 elements
+    __shared__ __align__(16) float s_at[32][kPVRows + 4];       // weights: token x tile row
+    const int h = blockIdx.x, slice = blockIdx.y, t = threadIdx.x;
+    const int b0 = blockIdx.z * 32, kh = h / group;
+    const int pos0 = d_pos ? *d_pos : pos_arg;
+    const int nmax = pos0 + min(B, b0 + 32);  // rows 0..nmax-1 are written (this chunk's included)
+    const int tb = t >> 3, dq = (t & 7) * 4;  // chain: token b0 + tb, elements dq..dq+3 of the slice
+    const int b = b0 + tb, nb = b < B ? pos0 + b + 1 : 0;
+    const int vr = t >> 2, vc = (t & 3) * 8;  // V staging: tile row vr, elements vc..vc+7
+    const int ar_ = t >> 3, ac = (t & 7) * 8;  // weight staging: token b0 + ar_, tile rows ac..ac+7
+    const int ab = b0 + ar_, nab = ab < B ? pos0 + ab + 1 : 0;
+    const float* arow = a + (static_cast<size_t>(min(ab, B - 1)) * n_head + h) * pitch;
+    uint4 vreg;
+    float areg[8];
+    auto fetch = [&](int r0) {
+        const int r = r0 + vr < nmax ? r0 + vr : 0;  // rows past the written ones re-read row 0 (weight 0)
+        vreg = ld_global16(pt_v[r / page_tokens] + static_cast<size_t>(r % page_tokens) * kv_dim + kh * hd +
+                           slice * 32 + vc);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int rr = r0 + ac + j;
+            areg[j] = rr < nab ? arow[rr] : 0.0f;
+        }
+    };
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    for (int r0 = 0; r0 < nmax; r0 += kPVRows) {
+        *reinterpret_cast<uint4*>(&s_v[vr][vc]) = vreg;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s_at[ar_][ac + j] = areg[j];
+        __syncthreads();
+        if (r0 + kPVRows < nmax) fetch(r0 + kPVRows);
+        // rows past nmax in the last tile carry weight 0 (areg) over finite rows: no-ops
+        const int rows4 = min(kPVRows, (nmax - r0 + 3) & ~3);
+        for (int rr = 0; rr < rows4; rr += 4) {
+            const float4 w4 = *reinterpret_cast<const float4*>(&s_at[tb][rr]);
+            const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // f16 operands straight into v_fma_mix
+                const half4v v = *reinterpret_cast<const half4v*>(&s_v[rr + i][dq]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[k] = fmaf(w[i], static_cast<float>(v[k]), acc[k]);
+            }
+        }
+        __syncthreads();
+    }
+    if (b >= B) return;  // whole 8-lane groups (one token) leave together
+    const int col = h * hd + slice * 32 + dq;
+    const size_t o = static_cast<size_t>(b) * n_head * hd + col;
+    *reinterpret_cast<float4*>(out + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    if (q8) {  // quantize_q8 of the token's 32-element block, 4 elements per lane
+        const float m4 = fmaxf(fmaxf(fabsf(acc[0]), fabsf(acc[1])), fmaxf(fabsf(acc[2]), fabsf(acc[3])));
+        const float mq = group_max<8>(m4);
+        const float dqs = mq > 0.0f ? __fdiv_rn(mq, 127.0f) : 1.0f;
+        const float id = __fdiv_rn(1.0f, dqs);
+        uint32_t packed = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float rq = fminf(fmaxf(roundf(acc[k] * id), -127.0f), 127.0f);
+            packed |= (static_cast<uint32_t>(static_cast<int>(rq)) & 0xffu) << (8 * k);
+        }
+        const size_t qo = q8_op ? q8_op_offset(b, col, static_cast<size_t>(n_head) * hd) : o;
+        *reinterpret_cast<uint32_t*>(q8 + qo) = packed;
+        if ((t & 7) == 0) q8d[o / 32] = dqs;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
@@ -423,6 +580,27 @@ hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v,
                                                                     static_cast<int>(hd), static_cast<int>(kv_dim),
                                                                     static_cast<int>(page_tokens), pitch, q8, q8d,
                                                                     q8_op);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_prefill(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q,
+                               size_t q_pitch, float* a_scratch, float* out, int8_t* q8, float* q8d, bool q8_op,
+                               const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
+                               size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st) {
+    if (!B) return hipSuccess;
+    if (hd % 32 || hd < 32 || (q8 && !q8d) || (q8_op && (n_head * hd) % 256)) return hipErrorInvalidValue;
+    const int group = static_cast<int>(n_head / n_head_kv);
+    const int pitch = static_cast<int>(max_pos);  // weight row pitch >= last position + 1
+    attn_scores_softmax_kernel<<<dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(B)), kSM,
+                                 (hd + max_pos) * sizeof(float), st>>>(
+        pt_k, q, static_cast<int>(q_pitch), a_scratch, d_pos, static_cast<int>(pos), static_cast<int>(n_head), group,
+        static_cast<int>(hd), static_cast<int>(kv_dim), static_cast<int>(page_tokens), pitch);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const dim3 g(static_cast<unsigned>(n_head), static_cast<unsigned>(hd / 32), static_cast<unsigned>((B + 31) / 32));
+    attn_pv_chunk_kernel<<<g, kPV, 0, st>>>(pt_v, a_scratch, out, q8, q8d, q8_op, d_pos, static_cast<int>(pos),
+                                            static_cast<int>(B), static_cast<int>(n_head), group,
+                                            static_cast<int>(hd), static_cast<int>(kv_dim),
+                                            static_cast<int>(page_tokens), pitch);
     return hipGetLastError();
 }
 

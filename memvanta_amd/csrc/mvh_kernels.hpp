@@ -57,6 +57,15 @@ hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v,
                        float* scores, float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B,
                        size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st,
                        int8_t* q8 = nullptr, float* q8d = nullptr, bool q8_op = false);
+// The same attention for a prefill chunk (hd % 32 == 0): scores and softmax
+// weights once per (token, head) into a_scratch (B * n_head * max_pos floats),
+// then the value chains with the V tiles shared by groups of 32 tokens; with
+// q8 also the output's quantize_q8 blocks (row-major, or the prefill GEMM's
+// operand order when q8_op).
+hipError_t launch_attn_prefill(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q,
+                               size_t q_pitch, float* a_scratch, float* out, int8_t* q8, float* q8d, bool q8_op,
+                               const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
+                               size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st);
 // One decode token in one launch: RoPE of q and k at position *d_pos, the
 // F16 K/V write at that position, scores, softmax and the value sum, and
 // (when q8 != null, hd % 32 == 0) the Q8 activation of the output.  One

@@ -417,10 +417,17 @@ void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
         // order when the projection runs there
         const bool o_q8 = q8mode && L.o.type == 2 && hd % 32 == 0 && L.o.cols == c_.n_head * hd;
         const bool o_op = o_q8 && mfma_gemm(L.o);
-        check(mvh::launch_attn(pk, pv, lay.q, lay.q_pitch, scores_, att_, nullptr, pos_, pos_ + B, B, c_.n_head,
-                               c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_, o_q8 ? q8_ : nullptr, q8d_,
-                               o_op),
-              "attention");
+        if (hd % 32 == 0) {  // scores + softmax once per (token, head), V tiles shared by the chunk's tokens
+            check(mvh::launch_attn_prefill(pk, pv, lay.q, lay.q_pitch, scores_, att_, o_q8 ? q8_ : nullptr, q8d_,
+                                           o_op, nullptr, pos_, pos_ + B, B, c_.n_head, c_.n_head_kv, hd,
+                                           c_.kv_dim(), page_tokens_, stream_),
+                  "attention");
+        } else {
+            check(mvh::launch_attn(pk, pv, lay.q, lay.q_pitch, scores_, att_, nullptr, pos_, pos_ + B, B, c_.n_head,
+                                   c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_, o_q8 ? q8_ : nullptr, q8d_,
+                                   o_op),
+                  "attention");
+        }
         gemm(L.o, att_, o_q8 ? q8_ : nullptr, q8d_, proj_, B, o_op);
         check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D, c_.rms_eps, stream_,
                                   op_gu),
