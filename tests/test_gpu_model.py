@@ -119,3 +119,21 @@ def test_long_context_vs_oracle(tmp_path, oracle, cfg_name, n_prompt):
         cur = int(np.argmax(want))
         assert int(np.argmax(got)) == cur
     m.close()
+
+
+@pytest.mark.parametrize("max_batch,chunk", [(48, 45), (48, 17)])
+def test_prefill_ragged_chunks_vs_oracle(tmp_path, oracle, max_batch, chunk):
+    """Prefill chunks that are not multiples of the 16-token GEMM slabs or of the
+    32-token attention groups (partial slabs and groups, two groups per chunk)."""
+    cfg = synth.dataclasses.replace(synth.LLAMA7B_1L, name="openllama-7b-v2-q4_0-1layer-ragged", ctx=256)
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=23)
+    prompt = synth.prompt_tokens(5, 100)
+    mo = oracle.model(path, ctx=256, force_q8=True)
+    m = capi.Model(path, ctx=256, act_mode=1, max_batch=max_batch)
+    close(m.prefill(prompt, chunk), mo.prefill(prompt, chunk), f"prefill chunks of {chunk}")
+    want = mo.forward(11)
+    got = m.forward(11)
+    close(got, want, "decode after ragged prefill")
+    assert int(np.argmax(got)) == int(np.argmax(want))
+    m.close()
