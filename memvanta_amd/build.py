@@ -1,4 +1,4 @@
-"""Build the gfx950 HIP library (and, on request, the CPU checker libraries).
+"""Build the gfx950 HIP library (and, on request, the CPU oracle libraries).
 
     python -m memvanta_amd.build            # libmemvanta_hip.so
     python -m memvanta_amd.build --all      # + oracle/liboracle.so (+ oracle/_ref when the reference exists)

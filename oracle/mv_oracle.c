@@ -1,6 +1,6 @@
 /*
- * mv_oracle.c -- CPU restatement of MemVanta's quantized-matmul + paged F16
- * attention path.  TEST INFRASTRUCTURE ONLY (the checker): used by tests/,
+ * mv_oracle.c -- CPU restatement of MemVanta's quantized-matmul + paged KV
+ * attention path.  TEST INFRASTRUCTURE ONLY: used by tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg; never by the
  * product.  Compiled with -ffp-contract=off: every fused multiply-add the
  * reference's GCC build performs is an explicit fmaf() here, every other
@@ -256,14 +256,20 @@ float mvo_dot_q6_k_fp32(const uint8_t* w, const float* x, size_t n) {
     return (float)sum;
 }
 
-/* dot_f32_simd (src/gguf_kernels.cpp:228-234): 8 fma lanes, t0+..+t7, tail
- * `s += a*b` contracted to fma. */
+/* dot_f32_simd (src/gguf_kernels.cpp:228-234): 8 fma lanes, t0+..+t7, then
+ * the tail. */
 float mvo_dot_f32(const float* a, const float* b, size_t n) {
     float t[8] = {0};
     size_t i = 0;
     for (; i + 8 <= n; i += 8)
         for (int j = 0; j < 8; ++j) t[j] = fmaf(a[i + j], b[i + j], t[j]);
     float s = hsum8(t);
+    /* the scalar tail `s += a*b` as the compiled reference runs it: GCC -O3
+     * vectorizes it 4 elements at a time (products rounded, adds in order),
+     * the last n % 4 are fused (pinned by the reference's F32 KV dots at every
+     * tail length 1..7) */
+    for (; i + 4 <= n; i += 4)
+        for (int j = 0; j < 4; ++j) s = s + a[i + j] * b[i + j];
     for (; i < n; ++i) s = fmaf(a[i], b[i], s);
     return s;
 }
@@ -482,30 +488,67 @@ int mvo_read_row_f32(const void* wv, int type, size_t rows, size_t cols, size_t 
 }
 
 /* ------------------------------------------------------------------ */
-/* paged F16 KV cache (src/llama_model.cpp:18-56)                        */
+/* paged KV cache, F32 / F16 / Q8 pages (src/llama_model.cpp:16-56)      */
 /* ------------------------------------------------------------------ */
+
+/* parse_kv_cache_type / kv_cache_type_name (src/llama_model.cpp:16-17) */
+int mvo_kv_parse_type(const char* s) {
+    if (!strcmp(s, "f32")) return MVO_KV_F32;
+    if (!strcmp(s, "f16")) return MVO_KV_F16;
+    if (!strcmp(s, "q8") || !strcmp(s, "q8_0")) return MVO_KV_Q8;
+    set_err("unknown KV cache type: %s", s);
+    return -1;
+}
+const char* mvo_kv_type_name(int type) {
+    switch (type) {
+    case MVO_KV_F32: return "f32";
+    case MVO_KV_F16: return "f16";
+    case MVO_KV_Q8: return "q8";
+    }
+    return "?";
+}
+
+/* One page of K or V: [page_tokens][kv_dim] elements of the cache type
+ * (float, fp16 bits or int8), and for Q8 one float scale per slot
+ * (PagedKVCache::Page, src/llama_model.cpp:18). */
+typedef struct {
+    uint8_t* e;
+    float* s;
+} kvpage;
 
 struct mvo_kv {
     size_t kv_dim, page_tokens, n_pages;
-    uint16_t** k16; /* page -> [page_tokens][kv_dim] */
-    uint16_t** v16;
+    int type;
+    kvpage* k; /* page -> K page (e == NULL: not allocated) */
+    kvpage* v;
 };
 
-mvo_kv* mvo_kv_create(size_t kv_dim, size_t page_tokens) {
+static size_t kv_elem_bytes(int type) { return type == MVO_KV_F32 ? 4 : type == MVO_KV_F16 ? 2 : 1; }
+
+mvo_kv* mvo_kv_create(size_t kv_dim, size_t page_tokens, int type) {
+    if (type != MVO_KV_F32 && type != MVO_KV_F16 && type != MVO_KV_Q8) {
+        set_err("unknown KV cache type id %d", type);
+        return NULL;
+    }
     mvo_kv* kv = (mvo_kv*)calloc(1, sizeof *kv);
     kv->kv_dim = kv_dim;
     kv->page_tokens = page_tokens ? page_tokens : 128;
+    kv->type = type;
     return kv;
 }
 
+int mvo_kv_type(const mvo_kv* kv) { return kv->type; }
+
 void mvo_kv_reset(mvo_kv* kv) {
     for (size_t p = 0; p < kv->n_pages; ++p) {
-        free(kv->k16[p]);
-        free(kv->v16[p]);
+        free(kv->k[p].e);
+        free(kv->k[p].s);
+        free(kv->v[p].e);
+        free(kv->v[p].s);
     }
-    free(kv->k16);
-    free(kv->v16);
-    kv->k16 = kv->v16 = NULL;
+    free(kv->k);
+    free(kv->v);
+    kv->k = kv->v = NULL;
     kv->n_pages = 0;
 }
 
@@ -518,63 +561,118 @@ void mvo_kv_destroy(mvo_kv* kv) {
 /* PagedKVCache::ensure: pages are allocated lazily, one per page index. */
 static void kv_ensure(mvo_kv* kv, size_t p) {
     if (p >= kv->n_pages) {
-        kv->k16 = (uint16_t**)realloc(kv->k16, (p + 1) * sizeof(uint16_t*));
-        kv->v16 = (uint16_t**)realloc(kv->v16, (p + 1) * sizeof(uint16_t*));
-        for (size_t i = kv->n_pages; i <= p; ++i) kv->k16[i] = kv->v16[i] = NULL;
+        kv->k = (kvpage*)realloc(kv->k, (p + 1) * sizeof(kvpage));
+        kv->v = (kvpage*)realloc(kv->v, (p + 1) * sizeof(kvpage));
+        for (size_t i = kv->n_pages; i <= p; ++i) {
+            kv->k[i].e = kv->v[i].e = NULL;
+            kv->k[i].s = kv->v[i].s = NULL;
+        }
         kv->n_pages = p + 1;
     }
-    if (!kv->k16[p]) {
-        kv->k16[p] = (uint16_t*)calloc(kv->page_tokens * kv->kv_dim, 2);
-        kv->v16[p] = (uint16_t*)calloc(kv->page_tokens * kv->kv_dim, 2);
+    if (!kv->k[p].e) {
+        size_t eb = kv_elem_bytes(kv->type);
+        kv->k[p].e = (uint8_t*)calloc(kv->page_tokens * kv->kv_dim, eb);
+        kv->v[p].e = (uint8_t*)calloc(kv->page_tokens * kv->kv_dim, eb);
+        if (kv->type == MVO_KV_Q8) {
+            kv->k[p].s = (float*)calloc(kv->page_tokens, sizeof(float));
+            kv->v[p].s = (float*)calloc(kv->page_tokens, sizeof(float));
+        }
     }
 }
 
-/* PagedKVCache::write, F16 branch (src/llama_model.cpp:22). */
+/* The Q8 row of one token (src/llama_model.cpp:22, Q8 branch): one scale for
+ * the whole kv_dim row, s = max|x|/127 (1 for an all-zero row; the running
+ * max keeps its value when compared with a NaN, as std::max does), then
+ * q = clamp(lround(x/s), -127, 127) -- a division, not a product with 1/s. */
+static float kv_quant_row(const float* x, size_t n, int8_t* q) {
+    float m = 0.0f;
+    for (size_t d = 0; d < n; ++d) {
+        float a = fabsf(x[d]);
+        if (m < a) m = a;
+    }
+    float s = m > 0.0f ? m / 127.0f : 1.0f;
+    for (size_t d = 0; d < n; ++d) {
+        long r = lroundf(x[d] / s);
+        q[d] = (int8_t)(r < -127 ? -127 : r > 127 ? 127 : r);
+    }
+    return s;
+}
+
+/* PagedKVCache::write (src/llama_model.cpp:22): F32 copies, F16 through the
+ * reference's fp32_to_fp16, Q8 per-token scale + int8. */
 void mvo_kv_write(mvo_kv* kv, size_t pos, const float* k, const float* v) {
     size_t p = pos / kv->page_tokens, i = pos % kv->page_tokens;
     kv_ensure(kv, p);
     size_t off = i * kv->kv_dim;
-    for (size_t d = 0; d < kv->kv_dim; ++d) {
-        kv->k16[p][off + d] = mvo_fp32_to_fp16(k[d]);
-        kv->v16[p][off + d] = mvo_fp32_to_fp16(v[d]);
+    if (kv->type == MVO_KV_F32) {
+        memcpy((float*)kv->k[p].e + off, k, kv->kv_dim * sizeof(float));
+        memcpy((float*)kv->v[p].e + off, v, kv->kv_dim * sizeof(float));
+    } else if (kv->type == MVO_KV_F16) {
+        uint16_t* kh = (uint16_t*)kv->k[p].e + off;
+        uint16_t* vh = (uint16_t*)kv->v[p].e + off;
+        for (size_t d = 0; d < kv->kv_dim; ++d) {
+            kh[d] = mvo_fp32_to_fp16(k[d]);
+            vh[d] = mvo_fp32_to_fp16(v[d]);
+        }
+    } else {
+        kv->k[p].s[i] = kv_quant_row(k, kv->kv_dim, (int8_t*)kv->k[p].e + off);
+        kv->v[p].s[i] = kv_quant_row(v, kv->kv_dim, (int8_t*)kv->v[p].e + off);
     }
 }
 
-const uint16_t* mvo_kv_row(const mvo_kv* kv, size_t pos, int which) {
+/* Raw stored row of `pos`: K (which = 0) or V (which = 1), kv_dim elements
+ * of the cache type; *scale gets the Q8 scale (1 for F32/F16) when non-NULL. */
+const void* mvo_kv_row(const mvo_kv* kv, size_t pos, int which, float* scale) {
     size_t p = pos / kv->page_tokens, i = pos % kv->page_tokens;
-    if (p >= kv->n_pages || !kv->k16[p]) return NULL;
-    return (which ? kv->v16[p] : kv->k16[p]) + i * kv->kv_dim;
+    if (p >= kv->n_pages || !kv->k[p].e) return NULL;
+    const kvpage* pg = which ? &kv->v[p] : &kv->k[p];
+    if (scale) *scale = kv->type == MVO_KV_Q8 ? pg->s[i] : 1.0f;
+    return pg->e + i * kv->kv_dim * kv_elem_bytes(kv->type);
 }
 
-/* PagedKVCache::dot_key, F16 branch (src/llama_model.cpp:23-39): lane j of 8
- * accumulates fma(q[d], k[d]) for d = j, j+8, ...; sum = t0+..+t7; the tail
- * `sum += q*k` is contracted. */
+/* element d of a stored row, converted exactly to float */
+static inline float kv_elem(const void* row, int type, size_t d) {
+    if (type == MVO_KV_F32) return ((const float*)row)[d];
+    if (type == MVO_KV_F16) return mvo_fp16_to_fp32(((const uint16_t*)row)[d]);
+    return (float)((const int8_t*)row)[d];
+}
+
+/* PagedKVCache::dot_key (src/llama_model.cpp:23-39), every type: lane j of 8
+ * accumulates fma(q[d], k[d]) for d = j, j+8, ...; sum = t0+..+t7; the F16
+ * and Q8 tails `sum += q*k` are contracted, F32 is dot_f32_simd (its tail is
+ * not, src/gguf_kernels.cpp:228-233); Q8 returns sum*scale (rounded product). */
 float mvo_kv_dot_key(const mvo_kv* kv, size_t pos, size_t offset, const float* q, size_t n) {
-    const uint16_t* k = mvo_kv_row(kv, pos, 0);
+    float sc;
+    const void* k = mvo_kv_row(kv, pos, 0, &sc);
     if (!k) return NAN;
-    k += offset;
+    if (kv->type == MVO_KV_F32) return mvo_dot_f32(q, (const float*)k + offset, n); /* dot_f32_simd */
     float t[8] = {0};
     size_t d = 0;
     for (; d + 8 <= n; d += 8)
-        for (int j = 0; j < 8; ++j) t[j] = fmaf(q[d + j], mvo_fp16_to_fp32(k[d + j]), t[j]);
+        for (int j = 0; j < 8; ++j) t[j] = fmaf(q[d + j], kv_elem(k, kv->type, offset + d + j), t[j]);
     float sum = hsum8(t);
-    for (; d < n; ++d) sum = fmaf(q[d], mvo_fp16_to_fp32(k[d]), sum);
-    return sum;
+    for (; d < n; ++d) sum = fmaf(q[d], kv_elem(k, kv->type, offset + d), sum);
+    return kv->type == MVO_KV_Q8 ? sum * sc : sum;
 }
 
-/* PagedKVCache::add_value, F16 branch (src/llama_model.cpp:40-48):
- * out[d] = fma(alpha, v[d], out[d]). */
+/* PagedKVCache::add_value (src/llama_model.cpp:40-48): out[d] =
+ * fma(w, v[d], out[d]) with w = alpha (F32, F16) or alpha*scale (Q8,
+ * rounded once before the chain). */
 void mvo_kv_add_value(const mvo_kv* kv, size_t pos, size_t offset, float alpha, float* out, size_t n) {
-    const uint16_t* v = mvo_kv_row(kv, pos, 1);
+    float sc;
+    const void* v = mvo_kv_row(kv, pos, 1, &sc);
     if (!v) return;
-    v += offset;
-    for (size_t d = 0; d < n; ++d) out[d] = fmaf(alpha, mvo_fp16_to_fp32(v[d]), out[d]);
+    float w = kv->type == MVO_KV_Q8 ? alpha * sc : alpha;
+    for (size_t d = 0; d < n; ++d) out[d] = fmaf(w, kv_elem(v, kv->type, offset + d), out[d]);
 }
 
+/* PagedKVCache::bytes_allocated (src/llama_model.cpp:49-55): element bytes of
+ * both arrays of every allocated page, plus 4 bytes per slot per Q8 scale array. */
 size_t mvo_kv_bytes_allocated(const mvo_kv* kv) {
-    size_t n = 0;
+    size_t n = 0, per = 2 * kv->page_tokens * kv->kv_dim * kv_elem_bytes(kv->type);
+    if (kv->type == MVO_KV_Q8) per += 2 * kv->page_tokens * sizeof(float);
     for (size_t p = 0; p < kv->n_pages; ++p)
-        if (kv->k16[p]) n += 2 * 2 * kv->page_tokens * kv->kv_dim;
+        if (kv->k[p].e) n += per;
     return n;
 }
 
@@ -890,7 +988,12 @@ void mvo_model_close(mvo_model* m) {
     free(m);
 }
 
-mvo_model* mvo_model_open(const char* path, size_t ctx_override, size_t page_tokens, int threads, int force_q8) {
+mvo_model* mvo_model_open(const char* path, size_t ctx_override, size_t page_tokens, int kv_type, int threads,
+                          int force_q8) {
+    if (kv_type != MVO_KV_F32 && kv_type != MVO_KV_F16 && kv_type != MVO_KV_Q8) {
+        set_err("unknown KV cache type id %d", kv_type);
+        return NULL;
+    }
     mvo_model* m = (mvo_model*)calloc(1, sizeof *m);
     if (gguf_open(path, &m->g)) { free(m); return NULL; }
     const okv* a = gguf_kv(&m->g, "general.architecture");
@@ -953,7 +1056,7 @@ mvo_model* mvo_model_open(const char* path, size_t ctx_override, size_t page_tok
 #undef T
         m->L[i].attn_norm = norm_vec(an, m->n_embd);
         m->L[i].ffn_norm = norm_vec(fn, m->n_embd);
-        m->kv[i] = mvo_kv_create(m->kv_dim, page_tokens ? page_tokens : 128);
+        m->kv[i] = mvo_kv_create(m->kv_dim, page_tokens ? page_tokens : 128, kv_type);
     }
     size_t half = m->hd / 2;
     m->rope_cos = (float*)malloc(m->n_ctx * half * sizeof(float));

@@ -1,8 +1,8 @@
 /*
- * mv_oracle.h -- CPU restatement of MemVanta's quantized-matmul and paged-F16
- * attention path.  TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke()
- * and bench.py's cpu_baseline leg use it as the checker.  Nothing in the
- * product (memvanta_amd/, include/) links or calls it.
+ * mv_oracle.h -- CPU restatement of MemVanta's quantized-matmul and paged-KV
+ * attention path.  TEST INFRASTRUCTURE ONLY: tests/ and __graft_entry__.smoke()
+ * check results against it, bench.py's cpu_baseline leg times it.  Nothing
+ * in the product (memvanta_amd/, include/) links or calls it.
  *
  * Every function restates one reference function; the citation names the
  * reference file:line it follows (paths relative to the MemVanta repo root).
@@ -20,7 +20,9 @@
  *   matvec / matmul ..... bit-exact golden vectors from the compiled reference,
  *                         plus an fp64 brute-force bound
  *   kv / attention ...... bit-exact golden vectors from the compiled reference
- *                         (single-layer model runs) plus an fp64 softmax bound
+ *                         for F32, F16 and Q8 pages (dots, value sums, one-hot
+ *                         probes of the stored values, bytes), model runs with
+ *                         each cache type, plus an fp64 softmax bound
  *   model ............... bit-exact logits + greedy ids vs the compiled reference
  */
 #ifndef MV_ORACLE_H
@@ -67,17 +69,22 @@ int mvo_matmul_batch_v06(const void* w, int type, size_t rows, size_t cols, int 
                          int force_q8, const float* x, float* y, size_t batch, int threads);
 int mvo_read_row_f32(const void* w, int type, size_t rows, size_t cols, size_t row, float* out);
 
-/* ---- paged F16 KV cache ---- */
+/* ---- paged KV cache: F32, F16 or Q8 pages (PagedKVCache's KVCacheType order) ---- */
+enum { MVO_KV_F32 = 0, MVO_KV_F16 = 1, MVO_KV_Q8 = 2 };
+int         mvo_kv_parse_type(const char* s);   /* -1 (message in mvo_last_error()) when unknown */
+const char* mvo_kv_type_name(int type);
 typedef struct mvo_kv mvo_kv;
-mvo_kv* mvo_kv_create(size_t kv_dim, size_t page_tokens);
+mvo_kv* mvo_kv_create(size_t kv_dim, size_t page_tokens, int type);  /* NULL for an unknown type */
 void    mvo_kv_destroy(mvo_kv* kv);
 void    mvo_kv_reset(mvo_kv* kv);
+int     mvo_kv_type(const mvo_kv* kv);
 void    mvo_kv_write(mvo_kv* kv, size_t pos, const float* k, const float* v);
 float   mvo_kv_dot_key(const mvo_kv* kv, size_t pos, size_t offset, const float* q, size_t n);
 void    mvo_kv_add_value(const mvo_kv* kv, size_t pos, size_t offset, float alpha, float* out, size_t n);
 size_t  mvo_kv_bytes_allocated(const mvo_kv* kv);
-/* raw page access for layout tests: fp16 K (which=0) or V (which=1) row of `pos` */
-const uint16_t* mvo_kv_row(const mvo_kv* kv, size_t pos, int which);
+/* raw page access for layout tests: the stored K (which=0) or V (which=1) row of `pos`
+ * (kv_dim floats, fp16 bits or int8); *scale = the Q8 row scale (1 otherwise) if non-NULL */
+const void* mvo_kv_row(const mvo_kv* kv, size_t pos, int which, float* scale);
 /* decode attention for one layer: q [n_head*hd] -> out [n_head*hd] over positions 0..pos */
 void    mvo_attn_decode(const mvo_kv* kv, const float* q, size_t pos, size_t n_head,
                         size_t n_head_kv, size_t hd, float* out);
@@ -90,10 +97,10 @@ void mvo_rope(float* q, float* k, size_t n_head, size_t n_head_kv, size_t hd,
 void mvo_swiglu(const float* g, const float* u, float* out, size_t n);
 int  mvo_argmax(const float* x, size_t n);
 
-/* ---- whole model (GGUF llama, F16 paged KV) ---- */
+/* ---- whole model (GGUF llama, paged KV of any type) ---- */
 typedef struct mvo_model mvo_model;
 mvo_model* mvo_model_open(const char* gguf_path, size_t ctx_override, size_t page_tokens,
-                          int threads, int force_q8);
+                          int kv_type, int threads, int force_q8);
 void   mvo_model_close(mvo_model* m);
 void   mvo_model_reset(mvo_model* m);
 /* config: n_ctx, n_embd, n_ff, n_layer, n_head, n_head_kv, vocab */

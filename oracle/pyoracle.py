@@ -1,4 +1,4 @@
-"""ctypes bindings of the checker libraries -- TEST INFRASTRUCTURE ONLY.
+"""ctypes bindings of the oracle libraries -- TEST INFRASTRUCTURE ONLY.
 
 * ``Oracle`` wraps liboracle.so, the C restatement of MemVanta's path
   (mv_oracle.c).
@@ -28,6 +28,10 @@ _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 _szp = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
 _sz = C.c_size_t
 
+# KV cache types (PagedKVCache's KVCacheType order) and their stored element types
+KV_F32, KV_F16, KV_Q8 = 0, 1, 2
+KV_DTYPE = {KV_F32: np.float32, KV_F16: np.uint16, KV_Q8: np.int8}
+
 
 def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
@@ -53,8 +57,11 @@ class Oracle:
         L.mvo_matmul_batch.argtypes = [_u8p, C.c_int, _sz, _sz, _f32p, _f32p, _sz, C.c_int]
         L.mvo_matmul_batch_v06.argtypes = [_u8p, C.c_int, _sz, _sz, C.c_int, C.c_int, _f32p, _f32p, _sz, C.c_int]
         L.mvo_read_row_f32.argtypes = [_u8p, C.c_int, _sz, _sz, _sz, _f32p]
+        L.mvo_kv_parse_type.argtypes = [C.c_char_p]
+        L.mvo_kv_type_name.restype = C.c_char_p
+        L.mvo_kv_type_name.argtypes = [C.c_int]
         L.mvo_kv_create.restype = C.c_void_p
-        L.mvo_kv_create.argtypes = [_sz, _sz]
+        L.mvo_kv_create.argtypes = [_sz, _sz, C.c_int]
         L.mvo_kv_destroy.argtypes = [C.c_void_p]
         L.mvo_kv_reset.argtypes = [C.c_void_p]
         L.mvo_kv_write.argtypes = [C.c_void_p, _sz, _f32p, _f32p]
@@ -63,8 +70,8 @@ class Oracle:
         L.mvo_kv_add_value.argtypes = [C.c_void_p, _sz, _sz, C.c_float, _f32p, _sz]
         L.mvo_kv_bytes_allocated.restype = _sz
         L.mvo_kv_bytes_allocated.argtypes = [C.c_void_p]
-        L.mvo_kv_row.restype = C.POINTER(C.c_uint16)
-        L.mvo_kv_row.argtypes = [C.c_void_p, _sz, C.c_int]
+        L.mvo_kv_row.restype = C.c_void_p
+        L.mvo_kv_row.argtypes = [C.c_void_p, _sz, C.c_int, C.POINTER(C.c_float)]
         L.mvo_attn_decode.argtypes = [C.c_void_p, _f32p, _sz, _sz, _sz, _sz, _f32p]
         L.mvo_rmsnorm.argtypes = [_f32p, _f32p, _sz, C.c_float, _f32p]
         L.mvo_rope_table.argtypes = [_sz, _sz, C.c_float, _f32p, _f32p]
@@ -72,7 +79,7 @@ class Oracle:
         L.mvo_swiglu.argtypes = [_f32p, _f32p, _f32p, _sz]
         L.mvo_argmax.argtypes = [_f32p, _sz]
         L.mvo_model_open.restype = C.c_void_p
-        L.mvo_model_open.argtypes = [C.c_char_p, _sz, _sz, C.c_int, C.c_int]
+        L.mvo_model_open.argtypes = [C.c_char_p, _sz, _sz, C.c_int, C.c_int, C.c_int]
         L.mvo_model_close.argtypes = [C.c_void_p]
         L.mvo_model_reset.argtypes = [C.c_void_p]
         L.mvo_model_config.argtypes = [C.c_void_p, _szp]
@@ -162,17 +169,28 @@ class Oracle:
         self.lib.mvo_swiglu(g, _f32(u), out, g.size)
         return out
 
-    def kv(self, kv_dim, page_tokens=128):
-        return OracleKV(self, kv_dim, page_tokens)
+    def kv_parse_type(self, s):
+        t = self.lib.mvo_kv_parse_type(s.encode())
+        if t < 0:
+            raise RuntimeError(self.lib.mvo_last_error().decode())
+        return t
 
-    def model(self, path, ctx=0, page=128, threads=8, force_q8=False):
-        return OracleModel(self, path, ctx, page, threads, force_q8)
+    def kv_type_name(self, t):
+        return self.lib.mvo_kv_type_name(t).decode()
+
+    def kv(self, kv_dim, page_tokens=128, kv_type=KV_F16):
+        return OracleKV(self, kv_dim, page_tokens, kv_type)
+
+    def model(self, path, ctx=0, page=128, threads=8, force_q8=False, kv_type=KV_F16):
+        return OracleModel(self, path, ctx, page, threads, force_q8, kv_type)
 
 
 class OracleKV:
-    def __init__(self, o: Oracle, kv_dim, page_tokens):
-        self.o, self.kv_dim = o, kv_dim
-        self.h = o.lib.mvo_kv_create(kv_dim, page_tokens)
+    def __init__(self, o: Oracle, kv_dim, page_tokens, kv_type=KV_F16):
+        self.o, self.kv_dim, self.kv_type = o, kv_dim, kv_type
+        self.h = o.lib.mvo_kv_create(kv_dim, page_tokens, kv_type)
+        if not self.h:
+            raise RuntimeError(o.lib.mvo_last_error().decode())
 
     def __del__(self):
         if getattr(self, "h", None):
@@ -190,8 +208,14 @@ class OracleKV:
         self.o.lib.mvo_kv_add_value(self.h, pos, offset, alpha, out, out.size)
 
     def row(self, pos, which):
-        p = self.o.lib.mvo_kv_row(self.h, pos, which)
-        return np.ctypeslib.as_array(p, (self.kv_dim,)).copy()
+        """(stored row as floats / fp16 bits / int8, Q8 scale or 1.0)"""
+        sc = C.c_float()
+        p = self.o.lib.mvo_kv_row(self.h, pos, which, C.byref(sc))
+        if not p:
+            raise RuntimeError("KV page missing")
+        dt = np.dtype(KV_DTYPE[self.kv_type])
+        raw = C.string_at(p, self.kv_dim * dt.itemsize)
+        return np.frombuffer(raw, dt).copy(), np.float32(sc.value)
 
     def bytes_allocated(self):
         return self.o.lib.mvo_kv_bytes_allocated(self.h)
@@ -203,9 +227,9 @@ class OracleKV:
 
 
 class OracleModel:
-    def __init__(self, o: Oracle, path, ctx, page, threads, force_q8):
+    def __init__(self, o: Oracle, path, ctx, page, threads, force_q8, kv_type=KV_F16):
         self.o = o
-        self.h = o.lib.mvo_model_open(path.encode(), ctx, page, threads, int(force_q8))
+        self.h = o.lib.mvo_model_open(path.encode(), ctx, page, kv_type, threads, int(force_q8))
         if not self.h:
             raise RuntimeError(o.lib.mvo_last_error().decode())
         cfg = np.zeros(7, np.uint64)
@@ -260,7 +284,10 @@ class Ref:
         L.mvr_matmul_batch_v06.argtypes = [C.c_void_p, C.c_char_p, _f32p, _f32p, _sz, C.c_uint, C.c_int]
         L.mvr_read_row.argtypes = [C.c_void_p, C.c_char_p, _sz, _f32p, _sz]
         L.mvr_kv_create.restype = C.c_void_p
-        L.mvr_kv_create.argtypes = [_sz, _sz]
+        L.mvr_kv_create.argtypes = [_sz, _sz, C.c_int]
+        L.mvr_kv_parse_type.argtypes = [C.c_char_p, C.POINTER(C.c_int)]
+        L.mvr_kv_type_name.restype = C.c_char_p
+        L.mvr_kv_type_name.argtypes = [C.c_int]
         L.mvr_kv_destroy.argtypes = [C.c_void_p]
         L.mvr_kv_write.argtypes = [C.c_void_p, _sz, _f32p, _f32p]
         L.mvr_kv_dot_key.argtypes = [C.c_void_p, _sz, _sz, _f32p, _sz, C.POINTER(C.c_float)]
@@ -268,7 +295,7 @@ class Ref:
         L.mvr_kv_bytes.restype = _sz
         L.mvr_kv_bytes.argtypes = [C.c_void_p]
         L.mvr_model_open.restype = C.c_void_p
-        L.mvr_model_open.argtypes = [C.c_char_p, C.c_uint, _sz, _sz, C.c_int]
+        L.mvr_model_open.argtypes = [C.c_char_p, C.c_uint, _sz, _sz, C.c_int, C.c_int]
         L.mvr_model_close.argtypes = [C.c_void_p]
         L.mvr_model_reset.argtypes = [C.c_void_p]
         L.mvr_model_config.argtypes = [C.c_void_p, _szp]
@@ -291,11 +318,19 @@ class Ref:
     def gguf(self, path):
         return RefGguf(self, path)
 
-    def kv(self, kv_dim, page_tokens=128):
-        return RefKV(self, kv_dim, page_tokens)
+    def kv_parse_type(self, s):
+        t = C.c_int()
+        self._check(self.lib.mvr_kv_parse_type(s.encode(), C.byref(t)))
+        return t.value
 
-    def model(self, path, ctx=0, page=128, threads=8, force_q8=False):
-        return RefModel(self, path, ctx, page, threads, force_q8)
+    def kv_type_name(self, t):
+        return self.lib.mvr_kv_type_name(t).decode()
+
+    def kv(self, kv_dim, page_tokens=128, kv_type=KV_F16):
+        return RefKV(self, kv_dim, page_tokens, kv_type)
+
+    def model(self, path, ctx=0, page=128, threads=8, force_q8=False, kv_type=KV_F16):
+        return RefModel(self, path, ctx, page, threads, force_q8, kv_type)
 
 
 class RefGguf:
@@ -335,9 +370,9 @@ class RefGguf:
 
 
 class RefKV:
-    def __init__(self, r: Ref, kv_dim, page_tokens):
+    def __init__(self, r: Ref, kv_dim, page_tokens, kv_type=KV_F16):
         self.r = r
-        self.h = r.lib.mvr_kv_create(kv_dim, page_tokens)
+        self.h = r.lib.mvr_kv_create(kv_dim, page_tokens, kv_type)
 
     def __del__(self):
         if getattr(self, "h", None):
@@ -361,9 +396,9 @@ class RefKV:
 
 
 class RefModel:
-    def __init__(self, r: Ref, path, ctx, page, threads, force_q8):
+    def __init__(self, r: Ref, path, ctx, page, threads, force_q8, kv_type=KV_F16):
         self.r = r
-        self.h = r.lib.mvr_model_open(path.encode(), threads, ctx, page, int(force_q8))
+        self.h = r.lib.mvr_model_open(path.encode(), threads, ctx, page, kv_type, int(force_q8))
         if not self.h:
             raise RuntimeError(r.lib.mvr_last_error().decode())
         cfg = np.zeros(7, np.uint64)

@@ -83,8 +83,15 @@ int mvr_read_row(void* h, const char* name, size_t row, float* out, size_t cols)
     return guard([&] { memvanta::tensor_read_row_f32(*f, f->tensor(name), row, out, cols); });
 }
 
-void* mvr_kv_create(size_t kv_dim, size_t page_tokens) {
-    return new memvanta::PagedKVCache(kv_dim, page_tokens, memvanta::KVCacheType::F16);
+// type: 0 = F32, 1 = F16, 2 = Q8 (KVCacheType's order)
+void* mvr_kv_create(size_t kv_dim, size_t page_tokens, int type) {
+    return new memvanta::PagedKVCache(kv_dim, page_tokens, static_cast<memvanta::KVCacheType>(type));
+}
+int mvr_kv_parse_type(const char* s, int* type) {
+    return guard([&] { *type = static_cast<int>(memvanta::parse_kv_cache_type(s)); });
+}
+const char* mvr_kv_type_name(int type) {
+    return memvanta::kv_cache_type_name(static_cast<memvanta::KVCacheType>(type));
 }
 void mvr_kv_destroy(void* kv) { delete static_cast<memvanta::PagedKVCache*>(kv); }
 int mvr_kv_write(void* kv, size_t pos, const float* k, const float* v) {
@@ -103,11 +110,12 @@ struct RefModel {
     int force_q8{};
 };
 
-void* mvr_model_open(const char* path, unsigned threads, size_t ctx, size_t page, int force_q8) {
+void* mvr_model_open(const char* path, unsigned threads, size_t ctx, size_t page, int kv_type, int force_q8) {
     auto* r = new RefModel;
     r->force_q8 = force_q8;
     if (guard([&] {
-            r->m = std::make_unique<memvanta::LlamaModel>(path, threads, ctx, page, memvanta::KVCacheType::F16);
+            r->m = std::make_unique<memvanta::LlamaModel>(path, threads, ctx, page,
+                                                          static_cast<memvanta::KVCacheType>(kv_type));
         })) {
         delete r;
         return nullptr;

@@ -193,6 +193,94 @@ def test_kv_golden(oracle):
     assert kv.bytes_allocated() == int(g["bytes"])
 
 
+KV_TYPES = {"f32": 0, "f16": 1, "q8": 2}
+
+
+def _kv_types_check(o, tname):
+    """Replays kv_types.npz for one cache type through oracle `o`."""
+    g = golden("kv_types.npz")
+    kv = o.kv(64, int(g[f"{tname}__page"]), KV_TYPES[tname])
+    k, v = g[f"{tname}__k"], g[f"{tname}__v"]
+    for p in range(k.shape[0]):
+        kv.write(p, k[p], v[p])
+    lens, offs, qs = g[f"{tname}__lens"], g[f"{tname}__offs"], g[f"{tname}__qs"]
+    dots = np.array([[kv.dot_key(p, int(offs[i]), qs[i, :lens[i]]) for i in range(lens.size)]
+                     for p in range(k.shape[0])], np.float32)
+    assert_bitexact(dots, g[f"{tname}__dots"], f"{tname} dot_key (tails 1..23)")
+    onehot = np.zeros_like(g[f"{tname}__onehot"])
+    for p in range(k.shape[0]):
+        for d in range(64):
+            e = np.zeros(8, np.float32)
+            e[d % 8] = 1.0
+            onehot[p, d] = kv.dot_key(p, d - d % 8, e)
+    assert_bitexact(onehot, g[f"{tname}__onehot"], f"{tname} stored values x scale")
+    for ln, off in ((64, 0), (29, 3), (7, 40)):
+        acc = np.zeros(ln, np.float32)
+        for p in range(k.shape[0]):
+            kv.add_value(p, off, np.float32(0.37 / (p + 1)) if p % 3 else np.float32(-1.25), acc)
+        assert_bitexact(acc, g[f"{tname}__acc{ln}"], f"{tname} add_value")
+    assert kv.bytes_allocated() == int(g[f"{tname}__bytes"])
+    return kv
+
+
+@pytest.mark.parametrize("tname", sorted(KV_TYPES))
+def test_kv_types_golden(oracle, tname):
+    _kv_types_check(oracle, tname)
+
+
+def test_kv_type_names(oracle):
+    g = golden("kv_types.npz")
+    assert [oracle.kv_type_name(t) for t in range(3)] == g["names"].tolist()
+    assert [oracle.kv_parse_type(s) for s in ("f32", "f16", "q8", "q8_0")] == g["parsed"].tolist()
+    with pytest.raises(RuntimeError, match="unknown KV cache type: bf16"):
+        oracle.kv_parse_type("bf16")
+
+
+def test_kv_q8_special_cases(oracle):
+    """Closed-form cases of the Q8 row: an all-zero row has scale 1 and
+    stores zeros; a row whose max is 127 has scale exactly 1, so x/s = x and
+    the stored values are x rounded half away from zero; the max element
+    always stores +-127; scales are per token, shared by all heads."""
+    kv = oracle.kv(16, 4, KV_TYPES["q8"])
+    z = np.zeros(16, np.float32)
+    x = np.array([127, -0.5, 0.5, 1.5, -2.5, 2.4999998, 126.5, -126.5] + [0] * 8, np.float32)
+    y = np.linspace(-3, 7, 16).astype(np.float32)
+    kv.write(0, z, x)
+    kv.write(1, y, z)
+    q, s = kv.row(0, 0)
+    assert s == 1.0 and not q.any()
+    q, s = kv.row(0, 1)
+    assert s == 1.0 and q[:8].tolist() == [127, -1, 1, 2, -3, 2, 127, -127]
+    q, s = kv.row(1, 0)
+    assert s == np.float32(7) / np.float32(127) and q[-1] == 127 and np.abs(q).max() == 127
+    # dot with a one-hot query returns float(q) * s, rounded once
+    e = np.zeros(8, np.float32)
+    e[3] = 1
+    assert kv.dot_key(1, 8, e) == np.float32(np.float32(q[11]) * s)
+
+
+def test_kv_types_vs_reference_live(oracle, ref):
+    rng = np.random.default_rng(8)
+    for t in KV_TYPES.values():
+        ko, kr = oracle.kv(48, 5, t), ref.kv(48, 5, t)
+        k = rng.standard_normal((23, 48), dtype=np.float32) * np.float32(4)
+        v = rng.standard_normal((23, 48), dtype=np.float32)
+        for p in range(23):
+            ko.write(p, k[p], v[p])
+            kr.write(p, k[p], v[p])
+        for p in range(23):
+            for ln in range(1, 25):
+                q = rng.standard_normal(ln, dtype=np.float32)
+                off = int(rng.integers(0, 48 - ln + 1))
+                assert bits(ko.dot_key(p, off, q)) == bits(kr.dot_key(p, off, q)), (t, p, ln, off)
+                ao = rng.standard_normal(ln, dtype=np.float32)
+                ar = ao.copy()
+                ko.add_value(p, off, np.float32(0.3), ao)
+                kr.add_value(p, off, np.float32(0.3), ar)
+                assert_bitexact(ao, ar, f"type {t} add_value")
+        assert ko.bytes_allocated() == kr.bytes_allocated()
+
+
 # ----------------------------------------------------------------- model
 
 @pytest.mark.parametrize("mode", [0, 1])
@@ -210,6 +298,22 @@ def test_tiny_model_golden(oracle, tiny_model, mode):
     assert m.kv_bytes() == int(g[f"kv_bytes_m{mode}"])
     m.reset()
     assert_bitexact(m.prefill(g["prompt33"], 32), g[f"prefill33_logits_m{mode}"], "prefill 32+1")
+
+
+@pytest.mark.parametrize("tname", ["f32", "q8"])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_tiny_model_kv_types_golden(oracle, tiny_model, tname, mode):
+    g = golden("model_tiny.npz")
+    m = oracle.model(tiny_model, ctx=256, force_q8=bool(mode), kv_type=KV_TYPES[tname])
+    assert_bitexact(m.prefill(g["prompt"], 32), g[f"kv{tname}_prefill_logits_m{mode}"], "prefill logits")
+    ids, cur = [], 17
+    for _ in range(12):
+        lg = m.forward(cur)
+        cur = int(np.argmax(lg))
+        ids.append(cur)
+    assert ids == g[f"kv{tname}_decode_ids_m{mode}"].tolist()
+    assert_bitexact(lg, g[f"kv{tname}_decode_last_logits_m{mode}"], "decode logits")
+    assert m.kv_bytes() == int(g[f"kv{tname}_kv_bytes_m{mode}"])
 
 
 def test_tiny_model_vs_reference_live(oracle, ref, tiny_model):
@@ -241,6 +345,11 @@ MUTATIONS = {
                          "return (uint16_t)(sign | (((uint32_t)exp << 10) + ((mant + 0x1000u) >> 13)));"),
     "q8_lane_order": ("for (int j = 0; j < 8; ++j) t[j] = fmaf((float)qs[k + j], x[b * 32 + k + j], t[j]);",
                       "for (int j = 0; j < 8; ++j) t[j] = fmaf((float)qs[k + j], x[b * 32 + k + j], t[(j + k / 8) & 7]);"),
+    "kv_q8_multiply_by_inverse": ("long r = lroundf(x[d] / s);", "long r = lroundf(x[d] * (1.0f / s));"),
+    "kv_q8_scale_per_element": ("float w = kv->type == MVO_KV_Q8 ? alpha * sc : alpha;",
+                                "float w = alpha;\n    if (kv->type == MVO_KV_Q8) alpha = sc;"),
+    "f32_tail_all_fused": ("for (int j = 0; j < 4; ++j) s = s + a[i + j] * b[i + j];",
+                           "for (int j = 0; j < 4; ++j) s = fmaf(a[i + j], b[i + j], s);"),
     "batch4_unrounded_scale": ("float q = (float)qi * d;\n                    size_t off = b * 32 + h * 16 + k + j;",
                                "float q = (float)qi;\n                    size_t off = b * 32 + h * 16 + k + j;"),
 }
@@ -281,6 +390,8 @@ def _golden_ok(o, mats, tiny_model):
         m = o.model(tiny_model, ctx=256)
         assert_bitexact(m.prefill(gm["prompt"], 32), gm["prefill_logits_m0"])
         m.close()
+        for tname in KV_TYPES:
+            _kv_types_check(o, tname)
     except AssertionError:
         return False
     return True
