@@ -1,6 +1,6 @@
 /*
  * memvanta_hip.h -- C ABI of the MI355X (gfx950) backend for MemVanta's
- * quantized-matmul + paged F16 attention hot path.
+ * quantized-matmul + paged-KV attention hot path.
  *
  * Plain C: pointers, sizes and int status codes; no exceptions or C++/torch
  * types cross it.  Every call returns MVH_OK (0) or an MVH_E_* code and leaves
@@ -25,6 +25,8 @@
  *   mvh_fp16_to_fp32      fp16_to_fp32             include/memvanta/gguf.hpp:80, src/gguf.cpp:110-119
  *   mvh_kv_*              PagedKVCache             include/memvanta/llama_model.hpp:32-52,
  *                                                  src/llama_model.cpp:18-56
+ *   mvh_kv_parse_type     parse_kv_cache_type      llama_model.hpp:29, src/llama_model.cpp:16
+ *   mvh_kv_type_name      kv_cache_type_name       llama_model.hpp:30, src/llama_model.cpp:17
  *   mvh_attn_decode       the per-head dot_key/softmax/add_value loop of
  *                         LlamaModel::forward      src/llama_model.cpp:256
  *   mvh_tensor_upload     GgufFile::tensor_data    include/memvanta/gguf.hpp:57, src/gguf.cpp:139
@@ -58,6 +60,11 @@ extern "C" {
 /* numerics of the batched (prefill) matmul, tensor_matmul_batch_v06 */
 #define MVH_ACT_REF 0 /* default: fp32 activations, 4/8-token blocking (q4/q8_row_batch4_fp32) */
 #define MVH_ACT_Q8 1  /* MEMVANTA_FORCE_Q8_ACT=1: per-token Q8 activations; Q4_0 on int8 MFMA */
+
+/* KV cache element types (KVCacheType, include/memvanta/llama_model.hpp:28, same order) */
+#define MVH_KV_F32 0
+#define MVH_KV_F16 1 /* LlamaModel's default */
+#define MVH_KV_Q8 2  /* int8 with one float scale per token and K/V row */
 
 /* GGML type ids accepted by mvh_tensor_upload */
 #define MVH_TYPE_F32 0
@@ -114,25 +121,36 @@ int mvh_read_row_f32(mvh_context* ctx, const mvh_tensor* w, size_t row, float* o
 int mvh_fp32_to_fp16(mvh_context* ctx, const float* x, uint16_t* out, size_t n, int ptr_kind);
 int mvh_fp16_to_fp32(mvh_context* ctx, const uint16_t* h, float* out, size_t n, int ptr_kind);
 
-/* ---- paged F16 KV cache: all layers of one model on one device ---- */
+/* ---- paged KV cache (F32 / F16 / Q8 pages): all layers of one model on one device ---- */
+/* parse_kv_cache_type: "f32", "f16", "q8" or "q8_0"; anything else fails with
+ * "unknown KV cache type: <s>" */
+int mvh_kv_parse_type(const char* s, int* kv_type);
+/* kv_cache_type_name: "f32", "f16", "q8", or "?" */
+const char* mvh_kv_type_name(int kv_type);
 int mvh_kv_create(mvh_context* ctx, size_t n_layer, size_t kv_dim, size_t page_tokens, size_t max_tokens,
-                  mvh_kv_cache** out);
+                  int kv_type, mvh_kv_cache** out);
 int mvh_kv_destroy(mvh_kv_cache* kv);
 int mvh_kv_reset(mvh_kv_cache* kv);
+/* PagedKVCache::bytes_allocated: element bytes of K and V of every page any write touched, plus 4 bytes per
+ * slot per Q8 scale array */
 int mvh_kv_bytes_allocated(const mvh_kv_cache* kv, size_t* bytes);
+int mvh_kv_type(const mvh_kv_cache* kv, int* kv_type);
 /* PagedKVCache::write for n_tokens consecutive positions pos..pos+n-1; k/v are [n][kv_dim] fp32 */
 int mvh_kv_write(mvh_context* ctx, mvh_kv_cache* kv, size_t layer, size_t pos, size_t n_tokens, const float* k,
                  const float* v, int ptr_kind);
-/* copy the stored fp16 row of (layer, pos): which = 0 for K, 1 for V; out is host memory [kv_dim] */
-int mvh_kv_read_row(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, size_t pos, int which, uint16_t* out);
+/* copy the stored row of (layer, pos): which = 0 for K, 1 for V; out is host memory for kv_dim elements of the
+ * cache type (float, fp16 bits or int8); scale (may be NULL) receives the Q8 row scale, 1 for F32/F16 */
+int mvh_kv_read_row(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, size_t pos, int which, void* out,
+                    float* scale);
 /* decode attention of one layer over positions 0..pos: q[n_head*hd] -> out[n_head*hd] */
 int mvh_attn_decode(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos,
                     size_t n_head, size_t n_head_kv, size_t head_dim, float* out, int ptr_kind);
 
-/* ---- whole model: LlamaModel on one device (weights, paged F16 KV and activations in HBM) ---- */
-/* act_mode selects the prefill numerics (MVH_ACT_REF / MVH_ACT_Q8); max_batch bounds the prefill chunk */
-int mvh_model_open(const char* gguf_path, int device, size_t ctx_override, size_t kv_page_tokens, int act_mode,
-                   size_t max_batch, mvh_model** out);
+/* ---- whole model: LlamaModel on one device (weights, paged KV and activations in HBM) ---- */
+/* kv_type is LlamaModel's kv_type argument (MVH_KV_F16 is its default); act_mode selects the prefill numerics
+ * (MVH_ACT_REF / MVH_ACT_Q8); max_batch bounds the prefill chunk */
+int mvh_model_open(const char* gguf_path, int device, size_t ctx_override, size_t kv_page_tokens, int kv_type,
+                   int act_mode, size_t max_batch, mvh_model** out);
 int mvh_model_close(mvh_model* m);
 /* n_ctx, n_embd, n_ff, n_layer, n_head, n_head_kv, vocab */
 int mvh_model_config(const mvh_model* m, size_t out[7]);
@@ -146,6 +164,7 @@ int mvh_model_prefill(mvh_model* m, const int* tokens, size_t n, size_t batch, f
 int mvh_model_generate_greedy(mvh_model* m, int token, size_t n, int* out_tokens, float* last_logits);
 int mvh_model_position(const mvh_model* m, size_t* pos);
 int mvh_model_kv_bytes(const mvh_model* m, size_t* bytes);
+int mvh_model_kv_type(const mvh_model* m, int* kv_type); /* LlamaModel::kv_type */
 int mvh_model_stream(mvh_model* m, void** stream);
 
 #ifdef __cplusplus

@@ -18,6 +18,8 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "memvanta_hip.h")
 
 MVH_HOST, MVH_DEVICE = 0, 1
 MVH_ACT_REF, MVH_ACT_Q8 = 0, 1
+MVH_KV_F32, MVH_KV_F16, MVH_KV_Q8 = 0, 1, 2  # KVCacheType order
+KV_DTYPE = {MVH_KV_F32: np.float32, MVH_KV_F16: np.uint16, MVH_KV_Q8: np.int8}
 STATUS = {0: "MVH_OK", 1: "MVH_E_INVALID", 2: "MVH_E_SHAPE", 3: "MVH_E_TYPE", 4: "MVH_E_DEVICE",
           5: "MVH_E_RANGE", 6: "MVH_E_NOMEM"}
 
@@ -58,14 +60,18 @@ _SIGS = {
     "mvh_read_row_f32": (_int, [_vp, _vp, _sz, _vp, _int]),
     "mvh_fp32_to_fp16": (_int, [_vp, _vp, _vp, _sz, _int]),
     "mvh_fp16_to_fp32": (_int, [_vp, _vp, _vp, _sz, _int]),
-    "mvh_kv_create": (_int, [_vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]),
+    "mvh_kv_parse_type": (_int, [C.c_char_p, C.POINTER(_int)]),
+    "mvh_kv_type_name": (C.c_char_p, [_int]),
+    "mvh_kv_create": (_int, [_vp, _sz, _sz, _sz, _sz, _int, C.POINTER(_vp)]),
+    "mvh_kv_type": (_int, [_vp, C.POINTER(_int)]),
     "mvh_kv_destroy": (_int, [_vp]),
     "mvh_kv_reset": (_int, [_vp]),
     "mvh_kv_bytes_allocated": (_int, [_vp, C.POINTER(_sz)]),
     "mvh_kv_write": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
-    "mvh_kv_read_row": (_int, [_vp, _vp, _sz, _sz, _int, _vp]),
+    "mvh_kv_read_row": (_int, [_vp, _vp, _sz, _sz, _int, _vp, C.POINTER(C.c_float)]),
     "mvh_attn_decode": (_int, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _vp, _int]),
-    "mvh_model_open": (_int, [C.c_char_p, _int, _sz, _sz, _int, _sz, C.POINTER(_vp)]),
+    "mvh_model_open": (_int, [C.c_char_p, _int, _sz, _sz, _int, _int, _sz, C.POINTER(_vp)]),
+    "mvh_model_kv_type": (_int, [_vp, C.POINTER(_int)]),
     "mvh_model_close": (_int, [_vp]),
     "mvh_model_config": (_int, [_vp, C.POINTER(_sz)]),
     "mvh_model_reset": (_int, [_vp]),
@@ -232,8 +238,9 @@ class Context:
         self._check(self.lib.mvh_fp16_to_fp32(self.h, _ptr(h), _ptr(out), n, _kind(h, out)))
         return out
 
-    def kv_cache(self, n_layer: int, kv_dim: int, page_tokens: int = 128, max_tokens: int = 2048) -> "KVCache":
-        return KVCache(self, n_layer, kv_dim, page_tokens, max_tokens)
+    def kv_cache(self, n_layer: int, kv_dim: int, page_tokens: int = 128, max_tokens: int = 2048,
+                 kv_type: int = MVH_KV_F16) -> "KVCache":
+        return KVCache(self, n_layer, kv_dim, page_tokens, max_tokens, kv_type)
 
 
 class Tensor:
@@ -258,11 +265,24 @@ class Tensor:
         return ty.value, n0.value, n1.value, nb.value, dp.value
 
 
+def kv_parse_type(s: str) -> int:
+    """parse_kv_cache_type: "f32" / "f16" / "q8" / "q8_0" -> MVH_KV_*."""
+    lib = load_library()
+    t = _int()
+    if lib.mvh_kv_parse_type(s.encode(), C.byref(t)) != 0:
+        raise MvhError(1, lib.mvh_last_error().decode())
+    return t.value
+
+
+def kv_type_name(t: int) -> str:
+    return load_library().mvh_kv_type_name(t).decode()
+
+
 class KVCache:
-    def __init__(self, ctx: Context, n_layer, kv_dim, page_tokens, max_tokens):
-        self.ctx, self.kv_dim = ctx, kv_dim
+    def __init__(self, ctx: Context, n_layer, kv_dim, page_tokens, max_tokens, kv_type: int = MVH_KV_F16):
+        self.ctx, self.kv_dim, self.kv_type = ctx, kv_dim, kv_type
         h = _vp()
-        ctx._check(ctx.lib.mvh_kv_create(ctx.h, n_layer, kv_dim, page_tokens, max_tokens, C.byref(h)))
+        ctx._check(ctx.lib.mvh_kv_create(ctx.h, n_layer, kv_dim, page_tokens, max_tokens, kv_type, C.byref(h)))
         self.h = h.value
 
     def close(self):
@@ -290,9 +310,17 @@ class KVCache:
         self.ctx._check(self.ctx.lib.mvh_kv_write(self.ctx.h, self.h, layer, pos, n, _ptr(k), _ptr(v), _kind(k, v)))
 
     def read_row(self, layer, pos, which):
-        out = np.empty(self.kv_dim, np.uint16)
-        self.ctx._check(self.ctx.lib.mvh_kv_read_row(self.ctx.h, self.h, layer, pos, which, out.ctypes.data))
-        return out
+        """(stored row: float32 / fp16 bits / int8 by cache type, Q8 row scale or 1.0)"""
+        out = np.empty(self.kv_dim, KV_DTYPE[self.kv_type])
+        sc = C.c_float()
+        self.ctx._check(self.ctx.lib.mvh_kv_read_row(self.ctx.h, self.h, layer, pos, which, out.ctypes.data,
+                                                     C.byref(sc)))
+        return out, np.float32(sc.value)
+
+    def type(self) -> int:
+        t = _int()
+        self.ctx._check(self.ctx.lib.mvh_kv_type(self.h, C.byref(t)))
+        return t.value
 
     def attn_decode(self, layer, q, pos, n_head, n_head_kv, head_dim, out=None):
         if out is None:
@@ -307,10 +335,11 @@ class Model:
     """LlamaModel on one device (mvh_model_*)."""
 
     def __init__(self, path: str, device: int = 0, ctx: int = 0, page_tokens: int = 128,
-                 act_mode: int = MVH_ACT_Q8, max_batch: int = 64):
+                 act_mode: int = MVH_ACT_Q8, max_batch: int = 64, kv_type: int = MVH_KV_F16):
         self.lib = load_library()
         h = _vp()
-        rc = self.lib.mvh_model_open(path.encode(), device, ctx, page_tokens, act_mode, max_batch, C.byref(h))
+        rc = self.lib.mvh_model_open(path.encode(), device, ctx, page_tokens, kv_type, act_mode, max_batch,
+                                     C.byref(h))
         self._check(rc)
         self.h = h.value
         cfg = (_sz * 7)()
@@ -354,6 +383,11 @@ class Model:
         p = _sz()
         self._check(self.lib.mvh_model_position(self.h, C.byref(p)))
         return p.value
+
+    def kv_type(self) -> int:
+        t = _int()
+        self._check(self.lib.mvh_model_kv_type(self.h, C.byref(t)))
+        return t.value
 
     def kv_bytes(self) -> int:
         p = _sz()

@@ -1,8 +1,10 @@
-// mvh_attn.hip -- paged F16 KV cache write and decode attention.
+// mvh_attn.hip -- paged KV cache write and attention (decode and prefill).
 //
 // Layout in HBM: per layer a page table of `max_pages` entries; page p holds
-// positions [p*page_tokens, (p+1)*page_tokens) as [slot][kv_dim] fp16, K and V
-// in separate arrays -- the PagedKVCache layout of src/llama_model.cpp:18-22.
+// positions [p*page_tokens, (p+1)*page_tokens) as [slot][kv_dim] elements of
+// the cache type (F32, F16, or Q8 with one float scale per slot after the
+// elements: kv_page_bytes), K and V in separate pages -- the PagedKVCache
+// layout of src/llama_model.cpp:18-22.
 #include "mvh_kernels.hpp"
 #define MVH_EXPF_QUAL __device__ __forceinline__
 #include "mvh_expf.h"
@@ -10,28 +12,112 @@
 namespace mvh {
 namespace {
 
-// PagedKVCache::write, F16 branch (src/llama_model.cpp:22): every element goes
-// through the reference's fp32_to_fp16 routine (f2h_ref).
-__global__ __launch_bounds__(256) void kv_write_kernel(uint16_t* const* __restrict__ pt_k,
-                                                       uint16_t* const* __restrict__ pt_v,
+// PagedKVCache::write, F32 and F16 branches (src/llama_model.cpp:22): F32
+// copies, F16 sends every element through the reference's fp32_to_fp16
+// routine (f2h_ref).  Token t's k/v row at k + t*pitch, v + t*pitch; its
+// position is pos + t, pos = *d_pos when d_pos != null.
+template <int KT>
+__global__ __launch_bounds__(256) void kv_write_kernel(void* const* __restrict__ pt_k, void* const* __restrict__ pt_v,
                                                        const float* __restrict__ k, const float* __restrict__ v,
-                                                       int pos, int n_tokens, int kv_dim, int page_tokens) {
+                                                       int pitch, const int* __restrict__ d_pos, int pos_arg,
+                                                       int n_tokens, int kv_dim, int page_tokens) {
+    typedef typename KvElem<KT>::T E;
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<size_t>(n_tokens) * kv_dim) return;
     const int t = static_cast<int>(i / kv_dim), d = static_cast<int>(i % kv_dim);
-    const int p = pos + t;
+    const int p = (d_pos ? *d_pos : pos_arg) + t;
     const size_t off = static_cast<size_t>(p % page_tokens) * kv_dim + d;
-    pt_k[p / page_tokens][off] = f2h_ref(k[i]);
-    pt_v[p / page_tokens][off] = f2h_ref(v[i]);
+    const float kx = k[static_cast<size_t>(t) * pitch + d], vx = v[static_cast<size_t>(t) * pitch + d];
+    E* kp = static_cast<E*>(pt_k[p / page_tokens]);
+    E* vp = static_cast<E*>(pt_v[p / page_tokens]);
+    if constexpr (KT == kKvF16) {
+        kp[off] = f2h_ref(kx);
+        vp[off] = f2h_ref(vx);
+    } else {
+        kp[off] = kx;
+        vp[off] = vx;
+    }
+}
+
+// PagedKVCache::write, Q8 branch (src/llama_model.cpp:22): one scale per
+// token and row (K, V), s = max|x|/127 over the whole kv_dim row (1 when the
+// row is all zero; fmaxf skips a NaN as std::max(m, NaN) keeps m), then
+// q = clamp(round_half_away(x / s), -127, 127) with an IEEE division (a NaN
+// quotient clamps to -127, as lround's x86 result does).  Workgroup = (token,
+// K or V).
+constexpr int kKW = 256;
+__global__ __launch_bounds__(kKW) void kv_write_q8_kernel(void* const* __restrict__ pt_k,
+                                                          void* const* __restrict__ pt_v,
+                                                          const float* __restrict__ k, const float* __restrict__ v,
+                                                          int pitch, const int* __restrict__ d_pos, int pos_arg,
+                                                          int kv_dim, int page_tokens) {
+    __shared__ float red[kKW / 64];
+    const int t = blockIdx.x, which = blockIdx.y;
+    const float* x = (which ? v : k) + static_cast<size_t>(t) * pitch;
+    float m = 0.0f;
+    for (int d = threadIdx.x; d < kv_dim; d += kKW) m = fmaxf(m, fabsf(x[d]));
+    m = group_max<32>(m);
+    m = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
+              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kKW / 64; ++w) m = fmaxf(m, red[w]);
+    const float s = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    const int p = (d_pos ? *d_pos : pos_arg) + t, slot = p % page_tokens;
+    uint8_t* page = static_cast<uint8_t*>((which ? pt_v : pt_k)[p / page_tokens]);
+    int8_t* row = reinterpret_cast<int8_t*>(page) + static_cast<size_t>(slot) * kv_dim;
+    for (int d = threadIdx.x; d < kv_dim; d += kKW) {
+        const float r = fminf(fmaxf(roundf(__fdiv_rn(x[d], s)), -127.0f), 127.0f);
+        row[d] = static_cast<int8_t>(r);
+    }
+    if (threadIdx.x == 0) reinterpret_cast<float*>(page + kv_scale_offset(page_tokens, kv_dim))[slot] = s;
+}
+
+// PagedKVCache::dot_key (src/llama_model.cpp:23-39) of one stored key row
+// (krow = the head's first element) with q (LDS): lane e of 8 accumulates
+// fma(q[d], k[d]) for d = e, e+8, ...; sum = t0+t1+..+t7; then the tail as
+// the compiled reference runs it -- F16/Q8: fused; F32 (dot_f32_simd): 4
+// elements at a time with rounded products and in-order adds, the last
+// hd % 4 fused.  The Q8 row scale is applied by the caller.
+template <int KT>
+__device__ __forceinline__ float kv_dot_row(const void* krow, const float* q, int hd) {
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    int c = 0;
+    for (; c + 8 <= hd; c += 8) {
+        float kf[8];
+        kv_load8<KT>(krow, c, kf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(q[c + e], kf[e], acc[e]);
+    }
+    float sum = acc[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) sum = sum + acc[e];
+    if constexpr (KT == kKvF32) {
+        for (; c + 4 <= hd; c += 4)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum = sum + q[c + j] * kv_to_f<KT>(krow, c + j);
+    }
+    for (; c < hd; ++c) sum = fmaf(q[c], kv_to_f<KT>(krow, c), sum);
+    return sum;
+}
+
+// Address of element `e` of slot `slot` in a page of the cache type.
+template <int KT>
+__device__ __forceinline__ const void* kv_elem_ptr(const void* page, size_t slot, size_t kv_dim, size_t e) {
+    return static_cast<const typename KvElem<KT>::T*>(page) + slot * kv_dim + e;
 }
 
 // Scores of query token b (grid z) and head h (grid x) against positions
-// 0..upto, upto = pos + b (dot_key, src/llama_model.cpp:23-39, divided by
-// sqrtf(hd) as at :248/:256): lane e of 8 accumulates fma(q[d], k[d]) for
-// d = e, e+8, ...; sum = t0+t1+..+t7; a tail beyond a multiple of 8 is
-// fma-accumulated into the sum.  pos comes from *d_pos when d_pos != null, so
-// the launch (sized for the largest position) can be replayed from a graph.
-__global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* __restrict__ pt_k,
+// 0..upto, upto = pos + b (dot_key, src/llama_model.cpp:23-39, times the Q8
+// row scale, divided by sqrtf(hd) as at :248/:256; kv_dot_row).  pos comes
+// from *d_pos when d_pos != null, so the launch (sized for the largest
+// position) can be replayed from a graph.
+template <int KT>
+__global__ __launch_bounds__(64) void attn_scores_kernel(const void* const* __restrict__ pt_k,
                                                          const float* __restrict__ q, int q_pitch,
                                                          float* __restrict__ scores,
                                                          const int* __restrict__ d_pos, int pos_arg, int n_head,
@@ -48,21 +134,9 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t* const* 
     const int t = t0 + threadIdx.x;
     if (t > upto) return;
     const int kh = h / group;
-    const uint16_t* krow = pt_k[t / page_tokens] + static_cast<size_t>(t % page_tokens) * kv_dim + kh * hd;
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    int c = 0;
-    for (; c + 8 <= hd; c += 8) {
-        const uint4 kv8 = ld_global16(krow + c);
-        const uint32_t w[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = fmaf(s_q[c + e], h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
-    }
-    float sum = acc[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) sum = sum + acc[e];
-    for (; c < hd; ++c) sum = fmaf(s_q[c], h2f(krow[c]), sum);
+    const void* page = pt_k[t / page_tokens];
+    float sum = kv_dot_row<KT>(kv_elem_ptr<KT>(page, t % page_tokens, kv_dim, kh * hd), s_q, hd);
+    if constexpr (KT == kKvQ8) sum = sum * kv_row_scale<KT>(page, t % page_tokens, page_tokens, kv_dim);
     scores[(static_cast<size_t>(b) * n_head + h) * score_pitch + t] = __fdiv_rn(sum, sqrt_rn(static_cast<float>(hd)));
 }
 
@@ -73,14 +147,16 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // Softmax and the value sum (src/llama_model.cpp:248,256): mx = max s,
-// e = expf(s-mx), den = sum of e in double, inv = float(1/den),
-// out[d] = fma(e_t*inv, V_t[d], out[d]) over t in order.  One wave per
+// e = expf(s-mx), den = sum of e in double, inv = float(1/den), a_t = e_t*inv,
+// out[d] = fma(w_t, V_t[d], out[d]) over t in order with w_t = a_t, or
+// a_t * (V_t's row scale) for Q8 (add_value, :40-48).  One wave per
 // (head, 64-wide slice of head_dim, query token); every output element's
 // value chain runs in t order in its own lane, as in the reference.  The
 // double `den` is added as a tree instead of in t order.  With q8 (hd % 32
 // == 0) the output's quantize_q8 blocks are written too, row-major or in the
 // prefill GEMM's operand order (q8_op, rows of n_head*hd).
-__global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* const* __restrict__ pt_v,
+template <int KT>
+__global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* __restrict__ pt_v,
                                                             const float* __restrict__ scores, float* __restrict__ out,
                                                             const int* __restrict__ d_pos, int pos_arg, int n_head,
                                                             int group, int hd, int kv_dim, int page_tokens,
@@ -105,25 +181,29 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const uint16_t* cons
     den = wave_sum(den);
     const float inv = static_cast<float>(1.0 / den);
     __syncthreads();
-    for (int t = threadIdx.x; t < n; t += 64) s_a[t] = s_a[t] * inv;
+    const int kh = h / group;
+    for (int t = threadIdx.x; t < n; t += 64) {
+        float a = s_a[t] * inv;
+        if constexpr (KT == kKvQ8) a = a * kv_row_scale<KT>(pt_v[t / page_tokens], t % page_tokens, page_tokens, kv_dim);
+        s_a[t] = a;
+    }
     __syncthreads();
     const int d = blockIdx.y * 64 + threadIdx.x;
     const bool live = d < hd;
-    const int kh = h / group;
     float acc = 0.0f;
     if (live) {
         for (int p0 = 0; p0 < n; p0 += page_tokens) {
-            const uint16_t* vp = pt_v[p0 / page_tokens] + kh * hd + d;
+            const void* vp = kv_elem_ptr<KT>(pt_v[p0 / page_tokens], 0, kv_dim, kh * hd + d);
             const int m = min(page_tokens, n - p0);
             int i = 0;
             for (; i + 8 <= m; i += 8) {
                 float vv[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) vv[j] = h2f(vp[static_cast<size_t>(i + j) * kv_dim]);
+                for (int j = 0; j < 8; ++j) vv[j] = kv_to_f<KT>(vp, (i + j) * kv_dim);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc = fmaf(s_a[p0 + i + j], vv[j], acc);
             }
-            for (; i < m; ++i) acc = fmaf(s_a[p0 + i], h2f(vp[static_cast<size_t>(i) * kv_dim]), acc);
+            for (; i < m; ++i) acc = fmaf(s_a[p0 + i], kv_to_f<KT>(vp, i * kv_dim), acc);
         }
     }
     const size_t o = (static_cast<size_t>(b) * n_head + h) * hd + d;
@@ -393,12 +473,15 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
 //
 // Scores and softmax weights of query token b (grid y) and head h (grid x)
 // over positions 0..pos0+b, one workgroup: the same arithmetic as
-// attn_scores_kernel (lane-of-8 fma accumulation, t0+..+t7, / sqrtf(hd)) and
+// attn_scores_kernel (kv_dot_row, Q8 row scale, / sqrtf(hd)) and
 // attn_softmax_v_kernel (mx, e = expf(s - mx), den in double, a = e *
-// float(1/den)); writes a (not s) to a[(b*n_head + h)*pitch + t].  The double
-// den is a tree over the workgroup's threads (not in t order).
+// float(1/den), times V_t's row scale for Q8); writes that weight to
+// a[(b*n_head + h)*pitch + t].  The double den is a tree over the
+// workgroup's threads (not in t order).
 constexpr int kSM = 256;
-__global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const uint16_t* const* __restrict__ pt_k,
+template <int KT>
+__global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const void* const* __restrict__ pt_k,
+                                                                  const void* const* __restrict__ pt_v,
                                                                   const float* __restrict__ q, int q_pitch,
                                                                   float* __restrict__ a_out,
                                                                   const int* __restrict__ d_pos, int pos_arg,
@@ -420,20 +503,9 @@ __global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const uint16_t
     const float scale = sqrt_rn(static_cast<float>(hd));
     float mx = -INFINITY;
     for (int tt = t; tt < n; tt += kSM) {
-        const uint16_t* krow = pt_k[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
-        float acc[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-        int c = 0;
-        for (; c + 8 <= hd; c += 8) {
-            const half8 hk = as_half8(ld_global16(krow + c));
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = fmaf(s_q[c + e], static_cast<float>(hk[e]), acc[e]);
-        }
-        float sum = acc[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) sum = sum + acc[e];
-        for (; c < hd; ++c) sum = fmaf(s_q[c], h2f(krow[c]), sum);
+        const void* page = pt_k[tt / page_tokens];
+        float sum = kv_dot_row<KT>(kv_elem_ptr<KT>(page, tt % page_tokens, kv_dim, kh * hd), s_q, hd);
+        if constexpr (KT == kKvQ8) sum = sum * kv_row_scale<KT>(page, tt % page_tokens, page_tokens, kv_dim);
         const float sc = __fdiv_rn(sum, scale);
         s_s[tt] = sc;
         mx = fmaxf(mx, sc);
@@ -458,13 +530,18 @@ __global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const uint16_t
     for (int w = 1; w < kSM / 64; ++w) den += red_d[w];
     const float inv = static_cast<float>(1.0 / den);
     float* ar = a_out + (static_cast<size_t>(b) * n_head + h) * pitch;
-    for (int tt = t; tt < n; tt += kSM) ar[tt] = s_s[tt] * inv;
+    for (int tt = t; tt < n; tt += kSM) {
+        float a = s_s[tt] * inv;
+        if constexpr (KT == kKvQ8)
+            a = a * kv_row_scale<KT>(pt_v[tt / page_tokens], tt % page_tokens, page_tokens, kv_dim);
+        ar[tt] = a;
+    }
 }
 
 // Value chains of a prefill chunk: workgroup (head h, 32-element slice of
 // head_dim, group of 32 query tokens); thread = (token b, 4 consecutive
-// elements), out[d] = fma(a_t, V_t[d], out[d]) over t = 0..pos0+b in order,
-// as in the reference.  V rows come in 64-row tiles staged once in LDS for all
+// elements), out[d] = fma(w_t, V_t[d], out[d]) over t = 0..pos0+b in order,
+// as in the reference (w_t the weights attn_scores_softmax_kernel wrote).  V rows come in 64-row tiles staged once in LDS for all
 // 32 tokens (the next tile's loads in flight while a tile is summed); the
 // weights of rows past a token's last position are 0 there, an exact no-op
 // (those rows are the chunk's later tokens, finite).  With q8 the output's
@@ -473,13 +550,21 @@ __global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const uint16_t
 constexpr int kPV = 256;
 constexpr int kPVRows = 64;
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const uint16_t* const* __restrict__ pt_v,
+// V tile row: the slice's 32 elements plus 16 bytes of padding
+template <int KT>
+struct PvTile {
+    typedef typename KvElem<KT>::T E;
+    static constexpr int kPitch = 32 + 16 / static_cast<int>(sizeof(E));
+};
+template <int KT>
+__global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const void* const* __restrict__ pt_v,
                                                             const float* __restrict__ a, float* __restrict__ out,
                                                             int8_t* __restrict__ q8, float* __restrict__ q8d,
                                                             bool q8_op, const int* __restrict__ d_pos, int pos_arg,
                                                             int B, int n_head, int group, int hd, int kv_dim,
                                                             int page_tokens, int pitch) {
-    __shared__ __align__(16) uint16_t s_v[kPVRows][32 + 8];     // V tile: rows x the slice's 32 elements
+    typedef typename KvElem<KT>::T E;
+    __shared__ __align__(16) E s_v[kPVRows][PvTile<KT>::kPitch];  // V tile: rows x the slice's 32 elements
     __shared__ __align__(16) float s_at[32][kPVRows + 4];       // weights: token x tile row
     const int h = blockIdx.x, slice = blockIdx.y, t = threadIdx.x;
     const int b0 = blockIdx.z * 32, kh = h / group;
@@ -491,12 +576,20 @@ __global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const uint16_t* cons
     const int ar_ = t >> 3, ac = (t & 7) * 8;  // weight staging: token b0 + ar_, tile rows ac..ac+7
     const int ab = b0 + ar_, nab = ab < B ? pos0 + ab + 1 : 0;
     const float* arow = a + (static_cast<size_t>(min(ab, B - 1)) * n_head + h) * pitch;
-    uint4 vreg;
+    uint4 vreg[KT == kKvF32 ? 2 : 1];
+    uint2 vreg8;
     float areg[8];
     auto fetch = [&](int r0) {
         const int r = r0 + vr < nmax ? r0 + vr : 0;  // rows past the written ones re-read row 0 (weight 0)
-        vreg = ld_global16(pt_v[r / page_tokens] + static_cast<size_t>(r % page_tokens) * kv_dim + kh * hd +
-                           slice * 32 + vc);
+        const void* src = kv_elem_ptr<KT>(pt_v[r / page_tokens], r % page_tokens, kv_dim, kh * hd + slice * 32 + vc);
+        if constexpr (KT == kKvF32) {
+            vreg[0] = ld_global16(src);
+            vreg[1] = ld_global16(static_cast<const float*>(src) + 4);
+        } else if constexpr (KT == kKvF16) {
+            vreg[0] = ld_global16(src);
+        } else {
+            vreg8 = ld_global8(src);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int rr = r0 + ac + j;
@@ -506,7 +599,14 @@ __global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const uint16_t* cons
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     fetch(0);
     for (int r0 = 0; r0 < nmax; r0 += kPVRows) {
-        *reinterpret_cast<uint4*>(&s_v[vr][vc]) = vreg;
+        if constexpr (KT == kKvF32) {
+            *reinterpret_cast<uint4*>(&s_v[vr][vc]) = vreg[0];
+            *reinterpret_cast<uint4*>(&s_v[vr][vc + 4]) = vreg[1];
+        } else if constexpr (KT == kKvF16) {
+            *reinterpret_cast<uint4*>(&s_v[vr][vc]) = vreg[0];
+        } else {
+            *reinterpret_cast<uint2*>(&s_v[vr][vc]) = vreg8;
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) s_at[ar_][ac + j] = areg[j];
         __syncthreads();
@@ -517,10 +617,22 @@ __global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const uint16_t* cons
             const float4 w4 = *reinterpret_cast<const float4*>(&s_at[tb][rr]);
             const float w[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {  // f16 operands straight into v_fma_mix
-                const half4v v = *reinterpret_cast<const half4v*>(&s_v[rr + i][dq]);
+            for (int i = 0; i < 4; ++i) {
+                float vf[4];
+                if constexpr (KT == kKvF32) {
+                    const float4 v = *reinterpret_cast<const float4*>(&s_v[rr + i][dq]);
+                    vf[0] = v.x, vf[1] = v.y, vf[2] = v.z, vf[3] = v.w;
+                } else if constexpr (KT == kKvF16) {  // f16 operands straight into v_fma_mix
+                    const half4v v = *reinterpret_cast<const half4v*>(&s_v[rr + i][dq]);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) acc[k] = fmaf(w[i], static_cast<float>(v[k]), acc[k]);
+                    for (int k = 0; k < 4; ++k) vf[k] = static_cast<float>(v[k]);
+                } else {
+                    const uint32_t v = *reinterpret_cast<const uint32_t*>(&s_v[rr + i][dq]);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) vf[k] = static_cast<float>(static_cast<int8_t>(v >> (8 * k)));
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[k] = fmaf(w[i], vf[k], acc[k]);
             }
         }
         __syncthreads();
@@ -548,67 +660,118 @@ __global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const uint16_t* cons
 
 }  // namespace
 
-hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
-                           size_t n_tokens, size_t kv_dim, size_t page_tokens, hipStream_t st) {
-    const size_t n = n_tokens * kv_dim;
-    if (!n) return hipSuccess;
-    kv_write_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(
-        pt_k, pt_v, k, v, static_cast<int>(pos), static_cast<int>(n_tokens), static_cast<int>(kv_dim),
-        static_cast<int>(page_tokens));
+hipError_t launch_kv_write(int kv_type, void* const* pt_k, void* const* pt_v, const float* k, const float* v,
+                           size_t pitch, const int* d_pos, size_t pos, size_t n_tokens, size_t kv_dim,
+                           size_t page_tokens, hipStream_t st) {
+    if (!n_tokens) return hipSuccess;
+    const int ip = static_cast<int>(pitch), ipos = static_cast<int>(pos), nt = static_cast<int>(n_tokens);
+    const int kd = static_cast<int>(kv_dim), pt = static_cast<int>(page_tokens);
+    const unsigned blocks = static_cast<unsigned>((n_tokens * kv_dim + 255) / 256);
+    switch (kv_type) {
+    case kKvF32:
+        kv_write_kernel<kKvF32><<<blocks, 256, 0, st>>>(pt_k, pt_v, k, v, ip, d_pos, ipos, nt, kd, pt);
+        break;
+    case kKvF16:
+        kv_write_kernel<kKvF16><<<blocks, 256, 0, st>>>(pt_k, pt_v, k, v, ip, d_pos, ipos, nt, kd, pt);
+        break;
+    case kKvQ8:
+        kv_write_q8_kernel<<<dim3(static_cast<unsigned>(n_tokens), 2), kKW, 0, st>>>(pt_k, pt_v, k, v, ip, d_pos, ipos,
+                                                                                  kd, pt);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, size_t q_pitch,
+namespace {
+template <int KT>
+hipError_t attn_typed(const void* const* pt_k, const void* const* pt_v, const float* q, size_t q_pitch, float* scores,
+                      float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
+                      size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st, int8_t* q8,
+                      float* q8d, bool q8_op) {
+    const int group = static_cast<int>(n_head / n_head_kv);
+    const int pitch = static_cast<int>(max_pos);  // scores row pitch >= last position + 1
+    const dim3 g1(static_cast<unsigned>(n_head), static_cast<unsigned>((max_pos + 63) / 64), static_cast<unsigned>(B));
+    attn_scores_kernel<KT><<<g1, 64, hd * sizeof(float), st>>>(pt_k, q, static_cast<int>(q_pitch), scores, d_pos,
+                                                               static_cast<int>(pos), static_cast<int>(n_head), group,
+                                                               static_cast<int>(hd), static_cast<int>(kv_dim),
+                                                               static_cast<int>(page_tokens), pitch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 g2(static_cast<unsigned>(n_head), static_cast<unsigned>((hd + 63) / 64), static_cast<unsigned>(B));
+    attn_softmax_v_kernel<KT><<<g2, 64, max_pos * sizeof(float), st>>>(
+        pt_v, scores, out, d_pos, static_cast<int>(pos), static_cast<int>(n_head), group, static_cast<int>(hd),
+        static_cast<int>(kv_dim), static_cast<int>(page_tokens), pitch, q8, q8d, q8_op);
+    return hipGetLastError();
+}
+
+template <int KT>
+hipError_t attn_prefill_typed(const void* const* pt_k, const void* const* pt_v, const float* q, size_t q_pitch,
+                              float* a_scratch, float* out, int8_t* q8, float* q8d, bool q8_op, const int* d_pos,
+                              size_t pos, size_t max_pos, size_t B, size_t n_head, size_t n_head_kv, size_t hd,
+                              size_t kv_dim, size_t page_tokens, hipStream_t st) {
+    const int group = static_cast<int>(n_head / n_head_kv);
+    const int pitch = static_cast<int>(max_pos);  // weight row pitch >= last position + 1
+    attn_scores_softmax_kernel<KT><<<dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(B)), kSM,
+                                     (hd + max_pos) * sizeof(float), st>>>(
+        pt_k, pt_v, q, static_cast<int>(q_pitch), a_scratch, d_pos, static_cast<int>(pos), static_cast<int>(n_head),
+        group, static_cast<int>(hd), static_cast<int>(kv_dim), static_cast<int>(page_tokens), pitch);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const dim3 g(static_cast<unsigned>(n_head), static_cast<unsigned>(hd / 32), static_cast<unsigned>((B + 31) / 32));
+    attn_pv_chunk_kernel<KT><<<g, kPV, 0, st>>>(pt_v, a_scratch, out, q8, q8d, q8_op, d_pos, static_cast<int>(pos),
+                                                static_cast<int>(B), static_cast<int>(n_head), group,
+                                                static_cast<int>(hd), static_cast<int>(kv_dim),
+                                                static_cast<int>(page_tokens), pitch);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_attn(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q, size_t q_pitch,
                        float* scores, float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B,
                        size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st,
                        int8_t* q8, float* q8d, bool q8_op) {
     if (!B) return hipSuccess;
     if (q8 && (hd % 32 || !q8d || (q8_op && (n_head * hd) % 256))) return hipErrorInvalidValue;
-    const int group = static_cast<int>(n_head / n_head_kv);
-    const int pitch = static_cast<int>(max_pos);  // scores row pitch >= last position + 1
-    const dim3 g1(static_cast<unsigned>(n_head), static_cast<unsigned>((max_pos + 63) / 64), static_cast<unsigned>(B));
-    attn_scores_kernel<<<g1, 64, hd * sizeof(float), st>>>(pt_k, q, static_cast<int>(q_pitch), scores, d_pos,
-                                                           static_cast<int>(pos),
-                                                           static_cast<int>(n_head), group, static_cast<int>(hd),
-                                                           static_cast<int>(kv_dim), static_cast<int>(page_tokens),
-                                                           pitch);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const dim3 g2(static_cast<unsigned>(n_head), static_cast<unsigned>((hd + 63) / 64), static_cast<unsigned>(B));
-    attn_softmax_v_kernel<<<g2, 64, max_pos * sizeof(float), st>>>(pt_v, scores, out, d_pos, static_cast<int>(pos),
-                                                                    static_cast<int>(n_head), group,
-                                                                    static_cast<int>(hd), static_cast<int>(kv_dim),
-                                                                    static_cast<int>(page_tokens), pitch, q8, q8d,
-                                                                    q8_op);
-    return hipGetLastError();
+    switch (kv_type) {
+    case kKvF32:
+        return attn_typed<kKvF32>(pt_k, pt_v, q, q_pitch, scores, out, d_pos, pos, max_pos, B, n_head, n_head_kv, hd,
+                                  kv_dim, page_tokens, st, q8, q8d, q8_op);
+    case kKvF16:
+        return attn_typed<kKvF16>(pt_k, pt_v, q, q_pitch, scores, out, d_pos, pos, max_pos, B, n_head, n_head_kv, hd,
+                                  kv_dim, page_tokens, st, q8, q8d, q8_op);
+    case kKvQ8:
+        return attn_typed<kKvQ8>(pt_k, pt_v, q, q_pitch, scores, out, d_pos, pos, max_pos, B, n_head, n_head_kv, hd,
+                                 kv_dim, page_tokens, st, q8, q8d, q8_op);
+    }
+    return hipErrorInvalidValue;
 }
 
-hipError_t launch_attn_prefill(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q,
+hipError_t launch_attn_prefill(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
                                size_t q_pitch, float* a_scratch, float* out, int8_t* q8, float* q8d, bool q8_op,
                                const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
                                size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st) {
     if (!B) return hipSuccess;
     if (hd % 32 || hd < 32 || (q8 && !q8d) || (q8_op && (n_head * hd) % 256)) return hipErrorInvalidValue;
-    const int group = static_cast<int>(n_head / n_head_kv);
-    const int pitch = static_cast<int>(max_pos);  // weight row pitch >= last position + 1
-    attn_scores_softmax_kernel<<<dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(B)), kSM,
-                                 (hd + max_pos) * sizeof(float), st>>>(
-        pt_k, q, static_cast<int>(q_pitch), a_scratch, d_pos, static_cast<int>(pos), static_cast<int>(n_head), group,
-        static_cast<int>(hd), static_cast<int>(kv_dim), static_cast<int>(page_tokens), pitch);
-    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const dim3 g(static_cast<unsigned>(n_head), static_cast<unsigned>(hd / 32), static_cast<unsigned>((B + 31) / 32));
-    attn_pv_chunk_kernel<<<g, kPV, 0, st>>>(pt_v, a_scratch, out, q8, q8d, q8_op, d_pos, static_cast<int>(pos),
-                                            static_cast<int>(B), static_cast<int>(n_head), group,
-                                            static_cast<int>(hd), static_cast<int>(kv_dim),
-                                            static_cast<int>(page_tokens), pitch);
-    return hipGetLastError();
+    switch (kv_type) {
+    case kKvF32:
+        return attn_prefill_typed<kKvF32>(pt_k, pt_v, q, q_pitch, a_scratch, out, q8, q8d, q8_op, d_pos, pos, max_pos,
+                                          B, n_head, n_head_kv, hd, kv_dim, page_tokens, st);
+    case kKvF16:
+        return attn_prefill_typed<kKvF16>(pt_k, pt_v, q, q_pitch, a_scratch, out, q8, q8d, q8_op, d_pos, pos, max_pos,
+                                          B, n_head, n_head_kv, hd, kv_dim, page_tokens, st);
+    case kKvQ8:
+        return attn_prefill_typed<kKvQ8>(pt_k, pt_v, q, q_pitch, a_scratch, out, q8, q8d, q8_op, d_pos, pos, max_pos,
+                                         B, n_head, n_head_kv, hd, kv_dim, page_tokens, st);
+    }
+    return hipErrorInvalidValue;
 }
 
-hipError_t launch_attn_decode(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
-                              float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim,
-                              size_t page_tokens, hipStream_t st) {
-    return launch_attn(pt_k, pt_v, q, n_head * hd, scores, out, nullptr, pos, pos + 1, 1, n_head, n_head_kv, hd,
-                       kv_dim, page_tokens, st);
+hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
+                              float* scores, float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd,
+                              size_t kv_dim, size_t page_tokens, hipStream_t st) {
+    return launch_attn(kv_type, pt_k, pt_v, q, n_head * hd, scores, out, nullptr, pos, pos + 1, 1, n_head, n_head_kv,
+                       hd, kv_dim, page_tokens, st);
 }
 
 hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* cos_t,

@@ -38,13 +38,15 @@ struct mvh_tensor {
 
 struct mvh_kv_cache {
     int device = 0;  // reset/destroy synchronise the device, so they never touch a context
+    int type = mvh::kKvF16;
     size_t n_layer = 0, kv_dim = 0, page_tokens = 0, max_tokens = 0, max_pages = 0;
-    std::vector<uint16_t*> hk, hv;  // host mirror of the page tables, [layer*max_pages + page]
-    uint16_t** dk = nullptr;        // device page tables
-    uint16_t** dv = nullptr;
-    std::vector<uint16_t*> pool;    // released page slabs (K page followed by V page)
+    std::vector<uint8_t*> hk, hv;  // host mirror of the page tables, [layer*max_pages + page]
+    void** dk = nullptr;           // device page tables
+    void** dv = nullptr;
+    std::vector<uint8_t*> pool;    // released page slabs (K page, then V page at page_stride())
     size_t live_pages = 0;
-    size_t page_elems() const { return page_tokens * kv_dim; }
+    size_t page_bytes() const { return mvh::kv_page_bytes(type, page_tokens, kv_dim); }
+    size_t page_stride() const { return (page_bytes() + 255) / 256 * 256; }
 };
 
 namespace {
@@ -187,19 +189,19 @@ int check_kv(const mvh_kv_cache* kv, size_t layer) {
 int ensure_page(mvh_kv_cache* kv, size_t layer, size_t p) {
     const size_t slot = layer * kv->max_pages + p;
     if (kv->hk[slot]) return MVH_OK;
-    uint16_t* slab = nullptr;
+    uint8_t* slab = nullptr;
     if (!kv->pool.empty()) {
         slab = kv->pool.back();
         kv->pool.pop_back();
-    } else if (hipMalloc(&slab, 2 * kv->page_elems() * sizeof(uint16_t)) != hipSuccess) {
+    } else if (hipMalloc(&slab, 2 * kv->page_stride()) != hipSuccess) {
         (void)hipGetLastError();
         return fail(MVH_E_NOMEM, "KV page allocation failed");
     }
     kv->hk[slot] = slab;
-    kv->hv[slot] = slab + kv->page_elems();
+    kv->hv[slot] = slab + kv->page_stride();
     ++kv->live_pages;
-    MVH_HIP(hipMemcpy(kv->dk + slot, &kv->hk[slot], sizeof(uint16_t*), hipMemcpyHostToDevice));
-    MVH_HIP(hipMemcpy(kv->dv + slot, &kv->hv[slot], sizeof(uint16_t*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dk + slot, &kv->hk[slot], sizeof(void*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dv + slot, &kv->hv[slot], sizeof(void*), hipMemcpyHostToDevice));
     return MVH_OK;
 }
 
@@ -537,11 +539,32 @@ int mvh_fp16_to_fp32(mvh_context* c, const uint16_t* h, float* out, size_t n, in
     return finish_out(c, out, od, n * 4, kind);
 }
 
-int mvh_kv_create(mvh_context* c, size_t n_layer, size_t kv_dim, size_t page_tokens, size_t max_tokens,
+int mvh_kv_parse_type(const char* s, int* type) {
+    if (!s || !type) return fail(MVH_E_INVALID, "null argument");
+    const std::string t = s;
+    if (t == "f32") *type = MVH_KV_F32;
+    else if (t == "f16") *type = MVH_KV_F16;
+    else if (t == "q8" || t == "q8_0") *type = MVH_KV_Q8;
+    else return fail(MVH_E_INVALID, "unknown KV cache type: %s", s);
+    return MVH_OK;
+}
+
+const char* mvh_kv_type_name(int type) {
+    switch (type) {
+    case MVH_KV_F32: return "f32";
+    case MVH_KV_F16: return "f16";
+    case MVH_KV_Q8: return "q8";
+    }
+    return "?";
+}
+
+int mvh_kv_create(mvh_context* c, size_t n_layer, size_t kv_dim, size_t page_tokens, size_t max_tokens, int kv_type,
                   mvh_kv_cache** out) {
     CHECK_CTX(c);
     if (!out) return fail(MVH_E_INVALID, "null out");
     *out = nullptr;
+    if (kv_type != MVH_KV_F32 && kv_type != MVH_KV_F16 && kv_type != MVH_KV_Q8)
+        return fail(MVH_E_INVALID, "unknown KV cache type id %d", kv_type);
     if (!page_tokens) page_tokens = 128;  // PagedKVCache default (src/llama_model.cpp:19)
     if (!n_layer || !kv_dim || !max_tokens) return fail(MVH_E_INVALID, "KV cache needs layers, kv_dim and max_tokens");
     if (kv_dim % 8) return fail(MVH_E_SHAPE, "kv_dim must be a multiple of 8");
@@ -549,6 +572,7 @@ int mvh_kv_create(mvh_context* c, size_t n_layer, size_t kv_dim, size_t page_tok
     auto* kv = new (std::nothrow) mvh_kv_cache;
     if (!kv) return fail(MVH_E_NOMEM, "host allocation failed");
     kv->device = c->device;
+    kv->type = kv_type;
     kv->n_layer = n_layer;
     kv->kv_dim = kv_dim;
     kv->page_tokens = page_tokens;
@@ -557,14 +581,14 @@ int mvh_kv_create(mvh_context* c, size_t n_layer, size_t kv_dim, size_t page_tok
     const size_t n = n_layer * kv->max_pages;
     kv->hk.assign(n, nullptr);
     kv->hv.assign(n, nullptr);
-    if (hipMalloc(&kv->dk, n * sizeof(uint16_t*)) != hipSuccess || hipMalloc(&kv->dv, n * sizeof(uint16_t*)) != hipSuccess) {
+    if (hipMalloc(&kv->dk, n * sizeof(void*)) != hipSuccess || hipMalloc(&kv->dv, n * sizeof(void*)) != hipSuccess) {
         (void)hipGetLastError();
         if (kv->dk) (void)hipFree(kv->dk);
         delete kv;
         return fail(MVH_E_NOMEM, "KV page table allocation failed");
     }
-    MVH_HIP(hipMemcpy(kv->dk, kv->hk.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
-    MVH_HIP(hipMemcpy(kv->dv, kv->hv.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dk, kv->hk.data(), n * sizeof(void*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dv, kv->hv.data(), n * sizeof(void*), hipMemcpyHostToDevice));
     *out = kv;
     return MVH_OK;
 }
@@ -580,8 +604,8 @@ int mvh_kv_reset(mvh_kv_cache* kv) {
         }
     kv->live_pages = 0;
     const size_t n = kv->hk.size();
-    MVH_HIP(hipMemcpy(kv->dk, kv->hk.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
-    MVH_HIP(hipMemcpy(kv->dv, kv->hv.data(), n * sizeof(uint16_t*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dk, kv->hk.data(), n * sizeof(void*), hipMemcpyHostToDevice));
+    MVH_HIP(hipMemcpy(kv->dv, kv->hv.data(), n * sizeof(void*), hipMemcpyHostToDevice));
     return MVH_OK;
 }
 
@@ -600,7 +624,13 @@ int mvh_kv_destroy(mvh_kv_cache* kv) {
 
 int mvh_kv_bytes_allocated(const mvh_kv_cache* kv, size_t* bytes) {
     if (!kv || !bytes) return fail(MVH_E_INVALID, "null argument");
-    *bytes = kv->live_pages * 2 * kv->page_elems() * sizeof(uint16_t);
+    *bytes = kv->live_pages * mvh::kv_page_pair_bytes_ref(kv->type, kv->page_tokens, kv->kv_dim);
+    return MVH_OK;
+}
+
+int mvh_kv_type(const mvh_kv_cache* kv, int* type) {
+    if (!kv || !type) return fail(MVH_E_INVALID, "null argument");
+    *type = kv->type;
     return MVH_OK;
 }
 
@@ -627,22 +657,31 @@ int mvh_kv_write(mvh_context* c, mvh_kv_cache* kv, size_t layer, size_t pos, siz
         vd = v;
     }
     const size_t base = layer * kv->max_pages;
-    MVH_HIP(mvh::launch_kv_write(kv->dk + base, kv->dv + base, static_cast<const float*>(kd),
-                                 static_cast<const float*>(vd), pos, n_tokens, kv->kv_dim, kv->page_tokens, c->stream));
+    MVH_HIP(mvh::launch_kv_write(kv->type, kv->dk + base, kv->dv + base, static_cast<const float*>(kd),
+                                 static_cast<const float*>(vd), kv->kv_dim, nullptr, pos, n_tokens, kv->kv_dim,
+                                 kv->page_tokens, c->stream));
     if (kind == MVH_HOST) MVH_HIP(hipStreamSynchronize(c->stream));
     return MVH_OK;
 }
 
-int mvh_kv_read_row(mvh_context* c, const mvh_kv_cache* kv, size_t layer, size_t pos, int which, uint16_t* out) {
+int mvh_kv_read_row(mvh_context* c, const mvh_kv_cache* kv, size_t layer, size_t pos, int which, void* out,
+                    float* scale) {
     CHECK_CTX(c);
     if (int rc = check_kv(kv, layer)) return rc;
     if (!out) return fail(MVH_E_INVALID, "null out");
     if (pos >= kv->max_tokens) return fail(MVH_E_RANGE, "KV position out of range");
-    const size_t slot = layer * kv->max_pages + pos / kv->page_tokens;
-    const uint16_t* page = which ? kv->hv[slot] : kv->hk[slot];
+    const size_t slot = layer * kv->max_pages + pos / kv->page_tokens, i = pos % kv->page_tokens;
+    const uint8_t* page = which ? kv->hv[slot] : kv->hk[slot];
     if (!page) return fail(MVH_E_RANGE, which ? "KV value page missing" : "KV key page missing");
+    const size_t eb = mvh::kv_elem_bytes(kv->type);
     MVH_HIP(hipStreamSynchronize(c->stream));
-    MVH_HIP(hipMemcpy(out, page + (pos % kv->page_tokens) * kv->kv_dim, kv->kv_dim * 2, hipMemcpyDeviceToHost));
+    MVH_HIP(hipMemcpy(out, page + i * kv->kv_dim * eb, kv->kv_dim * eb, hipMemcpyDeviceToHost));
+    if (scale) {
+        *scale = 1.0f;
+        if (kv->type == MVH_KV_Q8)
+            MVH_HIP(hipMemcpy(scale, page + mvh::kv_scale_offset(kv->page_tokens, kv->kv_dim) + 4 * i, 4,
+                              hipMemcpyDeviceToHost));
+    }
     return MVH_OK;
 }
 
@@ -668,7 +707,7 @@ int mvh_attn_decode(mvh_context* c, const mvh_kv_cache* kv, size_t layer, const 
     }
     if (int rc = grow(c, c->scratch, n_head * (pos + 1) * 4)) return rc;
     const size_t base = layer * kv->max_pages;
-    MVH_HIP(mvh::launch_attn_decode(kv->dk + base, kv->dv + base, static_cast<const float*>(qd),
+    MVH_HIP(mvh::launch_attn_decode(kv->type, kv->dk + base, kv->dv + base, static_cast<const float*>(qd),
                                     static_cast<float*>(c->scratch.p), od, pos, n_head, n_head_kv, head_dim,
                                     kv->kv_dim, kv->page_tokens, c->stream));
     return finish_out(c, out, od, qn * 4, kind);
@@ -697,15 +736,24 @@ int guarded(F&& f) {
 
 extern "C" {
 
-int mvh_model_open(const char* path, int device, size_t ctx_override, size_t page_tokens, int act_mode,
+int mvh_model_open(const char* path, int device, size_t ctx_override, size_t page_tokens, int kv_type, int act_mode,
                    size_t max_batch, mvh_model** out) {
     if (!path || !out) return fail(MVH_E_INVALID, "null argument");
     *out = nullptr;
     if (act_mode != MVH_ACT_REF && act_mode != MVH_ACT_Q8) return fail(MVH_E_INVALID, "bad act_mode %d", act_mode);
+    if (kv_type != MVH_KV_F32 && kv_type != MVH_KV_F16 && kv_type != MVH_KV_Q8)
+        return fail(MVH_E_INVALID, "unknown KV cache type id %d", kv_type);
     return guarded([&] {
         auto mode = act_mode == MVH_ACT_Q8 ? memvanta::hip::PrefillMode::Q8 : memvanta::hip::PrefillMode::Reference;
-        *out = reinterpret_cast<mvh_model*>(new ModelT(path, device, ctx_override, page_tokens, mode, max_batch));
+        *out = reinterpret_cast<mvh_model*>(
+            new ModelT(path, device, ctx_override, page_tokens, kv_type, mode, max_batch));
     });
+}
+
+int mvh_model_kv_type(const mvh_model* m, int* type) {
+    if (!m || !type) return fail(MVH_E_INVALID, "null argument");
+    *type = M(m)->kv_type();
+    return MVH_OK;
 }
 
 int mvh_model_close(mvh_model* m) {

@@ -140,6 +140,13 @@ __device__ __forceinline__ uint4 ld_global16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 8-byte form of ld_global16.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ld_global8(const void* p) {
+    const u32x2 v = *(const __attribute__((address_space(1))) u32x2*)(reinterpret_cast<uintptr_t>(p));
+    return make_uint2(v.x, v.y);
+}
+
 // 16-byte streaming load (weights are read once per call: nontemporal hint).
 __device__ __forceinline__ uint4 ld_stream16(const void* p) {
     const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -161,5 +168,79 @@ __host__ __device__ constexpr size_t q8_op_offset(size_t t, size_t k, size_t K) 
 }
 // bytes of that layout for B tokens (the last slab is whole)
 __host__ __device__ constexpr size_t q8_op_bytes(size_t B, size_t K) { return (B + 15) / 16 * 16 * K; }
+
+// ---- paged KV cache element types ------------------------------------------
+//
+// PagedKVCache's KVCacheType (F32, F16, Q8 in that order).  One page of K (or
+// V) is [page_tokens][kv_dim] elements of the type: float, fp16 bits, or int8;
+// a Q8 page then holds its page_tokens float row scales at a 16-byte aligned
+// offset after the elements.
+enum KvType : int { kKvF32 = 0, kKvF16 = 1, kKvQ8 = 2 };
+__host__ __device__ constexpr size_t kv_elem_bytes(int kt) { return kt == kKvF32 ? 4 : kt == kKvF16 ? 2 : 1; }
+__host__ __device__ constexpr size_t kv_scale_offset(size_t page_tokens, size_t kv_dim) {
+    return (page_tokens * kv_dim + 15) / 16 * 16;
+}
+__host__ __device__ constexpr size_t kv_page_bytes(int kt, size_t page_tokens, size_t kv_dim) {
+    return kt == kKvQ8 ? kv_scale_offset(page_tokens, kv_dim) + 4 * page_tokens : page_tokens * kv_dim * kv_elem_bytes(kt);
+}
+// bytes PagedKVCache::bytes_allocated counts per page index (K and V; the
+// Q8 alignment padding is not counted)
+__host__ __device__ constexpr size_t kv_page_pair_bytes_ref(int kt, size_t page_tokens, size_t kv_dim) {
+    return 2 * (page_tokens * kv_dim * kv_elem_bytes(kt) + (kt == kKvQ8 ? 4 * page_tokens : 0));
+}
+
+template <int KT>
+struct KvElem;
+template <>
+struct KvElem<kKvF32> {
+    typedef float T;
+};
+template <>
+struct KvElem<kKvF16> {
+    typedef uint16_t T;
+};
+template <>
+struct KvElem<kKvQ8> {
+    typedef int8_t T;
+};
+
+// Element e of a stored row, converted exactly to float.
+template <int KT>
+__device__ __forceinline__ float kv_to_f(const void* row, int e) {
+    if constexpr (KT == kKvF32) return static_cast<const float*>(row)[e];
+    else if constexpr (KT == kKvF16) return h2f(static_cast<const uint16_t*>(row)[e]);
+    else return static_cast<float>(static_cast<const int8_t*>(row)[e]);
+}
+
+// Eight consecutive elements (16/8/4-byte aligned for F32/F16/Q8) of a stored
+// row, converted exactly.
+template <int KT>
+__device__ __forceinline__ void kv_load8(const void* row, int e, float (&f)[8]) {
+    if constexpr (KT == kKvF32) {
+        const float* p = static_cast<const float*>(row) + e;
+        const uint4 a = ld_global16(p), b = ld_global16(p + 4);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = __uint_as_float(w[j]);
+    } else if constexpr (KT == kKvF16) {
+        const half8 h = as_half8(ld_global16(static_cast<const uint16_t*>(row) + e));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = static_cast<float>(h[j]);
+    } else {
+        const uint2 w = ld_global8(static_cast<const int8_t*>(row) + e);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            f[j] = static_cast<float>(static_cast<int8_t>((j < 4 ? w.x : w.y) >> (8 * (j & 3))));
+    }
+}
+
+// Q8 row scale of slot `slot` of a page (1 for the other types).
+template <int KT>
+__device__ __forceinline__ float kv_row_scale(const void* page, int slot, int page_tokens, int kv_dim) {
+    if constexpr (KT == kKvQ8)
+        return reinterpret_cast<const float*>(static_cast<const uint8_t*>(page) +
+                                              kv_scale_offset(page_tokens, kv_dim))[slot];
+    else return 1.0f;
+}
 
 }  // namespace mvh

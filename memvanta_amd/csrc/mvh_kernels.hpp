@@ -47,13 +47,16 @@ bool gemm_q4_0_mfma_ok(size_t cols);
 hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows,
                                     size_t cols, size_t batch, hipStream_t st);
 
-// ---- paged F16 KV + decode attention (mvh_attn.hip) ----
-hipError_t launch_kv_write(uint16_t* const* pt_k, uint16_t* const* pt_v, const float* k, const float* v, size_t pos,
-                           size_t n_tokens, size_t kv_dim, size_t page_tokens, hipStream_t st);
+// ---- paged KV (F32 / F16 / Q8 pages, KvType) + attention (mvh_attn.hip) ----
+// PagedKVCache::write of n_tokens rows (token t's k/v at k + t*pitch, v + t*pitch)
+// at positions pos..pos+n-1 (pos = *d_pos when d_pos != null)
+hipError_t launch_kv_write(int kv_type, void* const* pt_k, void* const* pt_v, const float* k, const float* v,
+                           size_t pitch, const int* d_pos, size_t pos, size_t n_tokens, size_t kv_dim,
+                           size_t page_tokens, hipStream_t st);
 // B query tokens at positions pos..pos+B-1 (pos = *d_pos when d_pos != null),
 // causal; q of token b at q + b*q_pitch; scores needs B * n_head * max_pos
 // floats, max_pos > last position
-hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, size_t q_pitch,
+hipError_t launch_attn(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q, size_t q_pitch,
                        float* scores, float* out, const int* d_pos, size_t pos, size_t max_pos, size_t B,
                        size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st,
                        int8_t* q8 = nullptr, float* q8d = nullptr, bool q8_op = false);
@@ -62,12 +65,12 @@ hipError_t launch_attn(const uint16_t* const* pt_k, const uint16_t* const* pt_v,
 // then the value chains with the V tiles shared by groups of 32 tokens; with
 // q8 also the output's quantize_q8 blocks (row-major, or the prefill GEMM's
 // operand order when q8_op).
-hipError_t launch_attn_prefill(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q,
+hipError_t launch_attn_prefill(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
                                size_t q_pitch, float* a_scratch, float* out, int8_t* q8, float* q8d, bool q8_op,
                                const int* d_pos, size_t pos, size_t max_pos, size_t B, size_t n_head,
                                size_t n_head_kv, size_t hd, size_t kv_dim, size_t page_tokens, hipStream_t st);
-// One decode token in one launch: RoPE of q and k at position *d_pos, the
-// F16 K/V write at that position, scores, softmax and the value sum, and
+// One decode token in one launch (F16 pages): RoPE of q and k at position
+// *d_pos, the F16 K/V write at that position, scores, softmax and the value sum, and
 // (when q8 != null, hd % 32 == 0) the Q8 activation of the output.  One
 // workgroup per query head; max_ctx bounds the position.
 bool attn_decode_fused_ok(size_t hd, size_t max_ctx, size_t page_tokens);  // LDS and shape limits of the fused kernel
@@ -76,9 +79,9 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
                                     uint16_t* const* pt_v, size_t page_tokens, float* out, int8_t* q8, float* q8d,
                                     size_t n_head, size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st);
 // scores needs n_head * (pos+1) floats of scratch
-hipError_t launch_attn_decode(const uint16_t* const* pt_k, const uint16_t* const* pt_v, const float* q, float* scores,
-                              float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd, size_t kv_dim,
-                              size_t page_tokens, hipStream_t st);
+hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
+                              float* scores, float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd,
+                              size_t kv_dim, size_t page_tokens, hipStream_t st);
 
 // ---- model step pieces (mvh_model.hip) ----
 hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int* tokens, size_t B, float* out,
@@ -86,7 +89,9 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
 // x += add (if add), n = rmsnorm(x)*w, and q/qd = Q8 of n (if q); B rows of D
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
                           size_t D, float eps, hipStream_t st, bool q_op = false);
-// q/k/v of token b at q + b*q_pitch, k + b*kv_pitch, v + b*kv_pitch
+// q/k/v of token b at q + b*q_pitch, k + b*kv_pitch, v + b*kv_pitch; the
+// rotated k and v go to the F16 pages when pt_k != null (k is rotated in place
+// either way)
 hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, size_t kv_pitch, const float* cos_t,
                           const float* sin_t, const int* d_pos, size_t pos0, size_t B, size_t n_head, size_t n_kv,
                           size_t hd, uint16_t* const* pt_k, uint16_t* const* pt_v, size_t page_tokens,

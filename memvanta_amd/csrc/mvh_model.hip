@@ -121,8 +121,9 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
 
 // RoPE (LlamaModel::rope_ptr, src/llama_model.cpp:238; half-split pairs,
 // GCC's contraction fma(x0,c,-(x1*s)) / fma(x0,s,x1*c)) on q and k of B
-// tokens at positions pos..pos+B-1, then PagedKVCache::write of k and v
-// through the reference's fp32_to_fp16 (:22).  One thread per (token, head, i).
+// tokens at positions pos..pos+B-1, in place, then (pt_k != null) the F16
+// PagedKVCache::write of k and v through the reference's fp32_to_fp16 (:22).
+// One thread per (token, head, i).
 __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int q_pitch, float* __restrict__ k,
                                                       const float* __restrict__ v, int kv_pitch,
                                                       const float* __restrict__ cos_t,
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int
     const float r0 = fmaf(x0, c, -(x1 * s)), r1 = fmaf(x0, s, x1 * c);
     z[i] = r0;
     z[i + half] = r1;
-    if (h >= n_head) {
+    if (h >= n_head && pt_k) {
         const int kh = h - n_head;
         const size_t off = static_cast<size_t>(pos % page_tokens) * KV + kh * hd;
         uint16_t* kp = pt_k[pos / page_tokens] + off;

@@ -52,9 +52,11 @@ void LlamaModel::check(hipError_t e, const char* what) const {
 }
 
 LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_override, std::size_t kv_page_tokens,
-                       PrefillMode mode, std::size_t max_batch)
-    : file_(std::make_unique<GgufFile>(path)), device_(device), mode_(mode),
+                       int kv_type, PrefillMode mode, std::size_t max_batch)
+    : file_(std::make_unique<GgufFile>(path)), device_(device), kv_type_(kv_type), mode_(mode),
       page_tokens_(kv_page_tokens ? kv_page_tokens : 128), max_batch_(std::max<std::size_t>(1, max_batch)) {
+    if (kv_type != mvh::kKvF32 && kv_type != mvh::kKvF16 && kv_type != mvh::kKvQ8)
+        throw std::runtime_error("unknown KV cache type id " + std::to_string(kv_type));
     const auto arch = file_->get_string("general.architecture").value_or("");
     if (arch != "llama")
         throw std::runtime_error("MemVanta real-model path currently supports GGUF architecture=llama, got: " + arch);
@@ -136,21 +138,22 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     check(hipMemcpy(rope_cos_, co.data(), co.size() * 4, hipMemcpyHostToDevice), "upload rope");
     check(hipMemcpy(rope_sin_, si.data(), si.size() * 4, hipMemcpyHostToDevice), "upload rope");
 
-    // paged F16 KV cache: the pages of every layer preallocated in HBM,
-    // addressed through per-layer page tables
+    // paged KV cache: the pages of every layer preallocated in HBM, addressed
+    // through per-layer page tables; page stride 256-byte aligned (a Q8 page
+    // ends with its float row scales)
     max_pages_ = (c_.n_ctx + page_tokens_ - 1) / page_tokens_;
-    const std::size_t page_elems = page_tokens_ * c_.kv_dim();
-    auto* kslab = static_cast<uint16_t*>(dalloc(c_.n_layer * max_pages_ * page_elems * 2));
-    auto* vslab = static_cast<uint16_t*>(dalloc(c_.n_layer * max_pages_ * page_elems * 2));
-    std::vector<uint16_t*> tk(c_.n_layer * max_pages_), tv(c_.n_layer * max_pages_);
+    const std::size_t stride = (mvh::kv_page_bytes(kv_type_, page_tokens_, c_.kv_dim()) + 255) / 256 * 256;
+    auto* kslab = static_cast<uint8_t*>(dalloc(c_.n_layer * max_pages_ * stride));
+    auto* vslab = static_cast<uint8_t*>(dalloc(c_.n_layer * max_pages_ * stride));
+    std::vector<void*> tk(c_.n_layer * max_pages_), tv(c_.n_layer * max_pages_);
     for (std::size_t i = 0; i < tk.size(); ++i) {
-        tk[i] = kslab + i * page_elems;
-        tv[i] = vslab + i * page_elems;
+        tk[i] = kslab + i * stride;
+        tv[i] = vslab + i * stride;
     }
-    pt_k_ = static_cast<uint16_t**>(dalloc(tk.size() * sizeof(uint16_t*)));
-    pt_v_ = static_cast<uint16_t**>(dalloc(tv.size() * sizeof(uint16_t*)));
-    check(hipMemcpy(pt_k_, tk.data(), tk.size() * sizeof(uint16_t*), hipMemcpyHostToDevice), "page table");
-    check(hipMemcpy(pt_v_, tv.data(), tv.size() * sizeof(uint16_t*), hipMemcpyHostToDevice), "page table");
+    pt_k_ = static_cast<void**>(dalloc(tk.size() * sizeof(void*)));
+    pt_v_ = static_cast<void**>(dalloc(tv.size() * sizeof(void*)));
+    check(hipMemcpy(pt_k_, tk.data(), tk.size() * sizeof(void*), hipMemcpyHostToDevice), "page table");
+    check(hipMemcpy(pt_v_, tv.data(), tv.size() * sizeof(void*), hipMemcpyHostToDevice), "page table");
 
     const std::size_t B = max_batch_, D = c_.n_embd, F = c_.n_ff, KV = c_.kv_dim(), W = std::max(D, F);
     x_ = static_cast<float*>(dalloc(B * D * 4));
@@ -175,7 +178,7 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     check(hipHostMalloc(reinterpret_cast<void**>(&pin_), 4 * (c_.n_ctx + B + 8), hipHostMallocDefault),
           "hipHostMalloc");
     logits_.resize(c_.vocab);
-    fused_attn_ = mvh::attn_decode_fused_ok(c_.head_dim(), c_.n_ctx, page_tokens_);
+    fused_attn_ = kv_type_ == mvh::kKvF16 && mvh::attn_decode_fused_ok(c_.head_dim(), c_.n_ctx, page_tokens_);
     reset();
 }
 
@@ -343,20 +346,22 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
             gemv(L.k, n_, L.k.type == 2 ? q8_ : nullptr, q8d_, lay.k);
             gemv(L.v, n_, L.v.type == 2 ? q8_ : nullptr, q8d_, lay.v);
         }
-        uint16_t* const* pk = pt_k_ + li * max_pages_;
-        uint16_t* const* pv = pt_v_ + li * max_pages_;
-        const bool o_q8 = fused_attn_ && L.o.type == 2 && hd % 32 == 0;
+        void* const* pk = pt_k_ + li * max_pages_;
+        void* const* pv = pt_v_ + li * max_pages_;
+        // the attention kernels write the o projection's Q8 activations (32-element head slices are Q8 blocks)
+        const bool o_q8 = L.o.type == 2 && hd % 32 == 0 && L.o.cols == c_.n_head * hd;
         if (fused_attn_) {
-            check(mvh::launch_attn_decode_fused(lay.q, lay.k, lay.v, rope_cos_, rope_sin_, d_pos_, pk, pv, page_tokens_,
-                                                att_, o_q8 ? q8_ : nullptr, q8d_, c_.n_head, c_.n_head_kv, hd,
-                                                c_.n_ctx, stream_),
+            check(mvh::launch_attn_decode_fused(lay.q, lay.k, lay.v, rope_cos_, rope_sin_, d_pos_,
+                                                reinterpret_cast<uint16_t* const*>(pk),
+                                                reinterpret_cast<uint16_t* const*>(pv), page_tokens_, att_,
+                                                o_q8 ? q8_ : nullptr, q8d_, c_.n_head, c_.n_head_kv, hd, c_.n_ctx,
+                                                stream_),
                   "attention");
         } else {
-            check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, d_pos_, 0,
-                                      1, c_.n_head, c_.n_head_kv, hd, pk, pv, page_tokens_, stream_),
-                  "rope/kv");
-            check(mvh::launch_attn(pk, pv, lay.q, lay.q_pitch, scores_, att_, d_pos_, 0, c_.n_ctx, 1, c_.n_head,
-                                   c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_),
+            store_kv(lay, pk, pv, d_pos_, 0, 1);
+            check(mvh::launch_attn(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, d_pos_, 0, c_.n_ctx, 1,
+                                   c_.n_head, c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_,
+                                   o_q8 ? q8_ : nullptr, q8d_),
                   "attention");
         }
         gemv(L.o, att_, o_q8 ? q8_ : nullptr, q8d_, proj_);
@@ -407,23 +412,23 @@ void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
             gemm(L.k, n_, q8mode ? q8_ : nullptr, q8d_, lay.k, B, op_qkv);
             gemm(L.v, n_, q8mode ? q8_ : nullptr, q8d_, lay.v, B, op_qkv);
         }
-        uint16_t* const* pk = pt_k_ + li * max_pages_;
-        uint16_t* const* pv = pt_v_ + li * max_pages_;
-        check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, nullptr, pos_,
-                                  B, c_.n_head, c_.n_head_kv, hd, pk, pv, page_tokens_, stream_),
-              "rope/kv");
+        void* const* pk = pt_k_ + li * max_pages_;
+        void* const* pv = pt_v_ + li * max_pages_;
+        store_kv(lay, pk, pv, nullptr, pos_, B);
         // the softmax-V kernel also writes the o projection's Q8 activations
         // (32-element head slices are Q8 blocks), in the MFMA GEMM's operand
         // order when the projection runs there
         const bool o_q8 = q8mode && L.o.type == 2 && hd % 32 == 0 && L.o.cols == c_.n_head * hd;
         const bool o_op = o_q8 && mfma_gemm(L.o);
         if (hd % 32 == 0) {  // scores + softmax once per (token, head), V tiles shared by the chunk's tokens
-            check(mvh::launch_attn_prefill(pk, pv, lay.q, lay.q_pitch, scores_, att_, o_q8 ? q8_ : nullptr, q8d_,
+            check(mvh::launch_attn_prefill(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, o_q8 ? q8_ : nullptr,
+                                           q8d_,
                                            o_op, nullptr, pos_, pos_ + B, B, c_.n_head, c_.n_head_kv, hd,
                                            c_.kv_dim(), page_tokens_, stream_),
                   "attention");
         } else {
-            check(mvh::launch_attn(pk, pv, lay.q, lay.q_pitch, scores_, att_, nullptr, pos_, pos_ + B, B, c_.n_head,
+            check(mvh::launch_attn(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, nullptr, pos_, pos_ + B, B,
+                                   c_.n_head,
                                    c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_, o_q8 ? q8_ : nullptr, q8d_,
                                    o_op),
                   "attention");
@@ -462,7 +467,24 @@ std::size_t LlamaModel::kv_bytes_allocated() const {
     // pages are allocated lazily in the reference (PagedKVCache::ensure):
     // every page any written position touched, in every layer
     const std::size_t pages = (kv_hi_ + page_tokens_ - 1) / page_tokens_;
-    return c_.n_layer * pages * 2 * page_tokens_ * c_.kv_dim() * sizeof(uint16_t);
+    return c_.n_layer * pages * mvh::kv_page_pair_bytes_ref(kv_type_, page_tokens_, c_.kv_dim());
+}
+
+// RoPE of q and k of B tokens at positions pos.. (*d_pos when non-null), then
+// PagedKVCache::write of k and v: fused into the RoPE kernel for F16 pages,
+// a write kernel of its own for F32 / Q8 (Q8 needs the whole row's max).
+void LlamaModel::store_kv(const QkvLayout& lay, void* const* pk, void* const* pv, const int* d_pos, std::size_t pos,
+                          std::size_t B) {
+    const bool f16 = kv_type_ == mvh::kKvF16;
+    check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, d_pos, pos, B,
+                              c_.n_head, c_.n_head_kv, c_.head_dim(),
+                              f16 ? reinterpret_cast<uint16_t* const*>(pk) : nullptr,
+                              f16 ? reinterpret_cast<uint16_t* const*>(pv) : nullptr, page_tokens_, stream_),
+          "rope/kv");
+    if (!f16)
+        check(mvh::launch_kv_write(kv_type_, pk, pv, lay.k, lay.v, lay.kv_pitch, d_pos, pos, B, c_.kv_dim(),
+                                   page_tokens_, stream_),
+              "kv write");
 }
 
 const std::vector<float>& LlamaModel::logits() {

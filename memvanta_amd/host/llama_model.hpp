@@ -1,9 +1,9 @@
 // llama_model.hpp -- device-resident Llama decode/prefill with the public
 // surface of MemVanta's LlamaModel (include/memvanta/llama_model.hpp:100-138):
 // construct from a GGUF path, reset(), forward(token), prefill(tokens, batch,
-// logits_last), position(), kv_bytes_allocated().  Numerics follow the
-// reference step for step (src/llama_model.cpp:222-262); the F16 paged KV
-// cache lives in HBM.  generate_greedy() runs the decode loop from a captured
+// logits_last), position(), kv_bytes_allocated(), kv_type().  Numerics
+// follow the reference step for step (src/llama_model.cpp:222-262); the paged
+// KV cache (F32, F16 or Q8 pages) lives in HBM.  generate_greedy() runs the decode loop from a captured
 // HIP graph, the greedy token of each step feeding the next on the device.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -31,8 +31,10 @@ enum class PrefillMode { Reference = 0, Q8 = 1 };  // Q8 = MEMVANTA_FORCE_Q8_ACT
 
 class LlamaModel {
 public:
+    // kv_type: KVCacheType order, 0 = F32, 1 = F16 (the reference's default), 2 = Q8
     LlamaModel(const std::string& gguf_path, int device = 0, std::size_t ctx_override = 0,
-               std::size_t kv_page_tokens = 128, PrefillMode mode = PrefillMode::Q8, std::size_t max_batch = 64);
+               std::size_t kv_page_tokens = 128, int kv_type = 1, PrefillMode mode = PrefillMode::Q8,
+               std::size_t max_batch = 64);
     ~LlamaModel();
     LlamaModel(const LlamaModel&) = delete;
     LlamaModel& operator=(const LlamaModel&) = delete;
@@ -46,6 +48,7 @@ public:
     std::vector<int> generate_greedy(int token, std::size_t n);
     std::size_t position() const { return pos_; }
     std::size_t kv_bytes_allocated() const;
+    int kv_type() const { return kv_type_; }
     hipStream_t stream() const { return stream_; }
     const std::vector<float>& logits();  // copies the device logits of the last step
 
@@ -81,6 +84,8 @@ private:
               bool q8_op = false);
     static bool mfma_gemm(const Tensor& w);
     void decode_step(const int* d_token, bool logits, bool argmax);
+    void store_kv(const QkvLayout& lay, void* const* pk, void* const* pv, const int* d_pos, std::size_t pos,
+                  std::size_t B);
     void batch_step(const int* tokens, std::size_t B, bool logits);
     void check(hipError_t e, const char* what) const;
 
@@ -88,15 +93,16 @@ private:
     LlamaConfig c_;
     int device_{};
     hipStream_t stream_{};
+    int kv_type_{1};
     PrefillMode mode_;
     std::size_t page_tokens_{}, max_pages_{}, max_batch_{}, pos_{}, kv_hi_{};
     Tensor embd_, out_;
     float* out_norm_{};
     std::vector<Layer> layers_;
     std::vector<void*> allocs_;
-    // paged F16 KV: one slab per layer and kind, page tables per layer
-    uint16_t** pt_k_{};
-    uint16_t** pt_v_{};
+    // paged KV: one slab per kind, page tables per layer ([layer][max_pages])
+    void** pt_k_{};
+    void** pt_v_{};
     float *rope_cos_{}, *rope_sin_{};
     // activations ([max_batch][...] for prefill; row 0 for decode)
     float *x_{}, *n_{}, *qkv_{}, *att_{}, *proj_{}, *gu_{}, *ff_{}, *logits_d_{}, *scores_{};
@@ -108,7 +114,7 @@ private:
     int* pin_{};         // pinned host staging
     std::vector<float> logits_;
     hipGraphExec_t graph_{};
-    bool fused_attn_{};  // decode attention in one launch (launch_attn_decode_fused)
+    bool fused_attn_{};  // decode attention in one launch (launch_attn_decode_fused; F16 pages)
 };
 
 }  // namespace hip

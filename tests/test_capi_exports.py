@@ -2,6 +2,9 @@
 include/memvanta_hip.h declares (no compute calls here)."""
 import ctypes
 
+import pytest
+
+from conftest import golden
 from memvanta_amd import capi
 
 
@@ -28,6 +31,17 @@ def test_version_and_error_channel():
     assert lib.mvh_kv_bytes_allocated(None, ctypes.byref(n)) == 1
 
 
+def test_kv_type_names_match_reference():
+    """parse_kv_cache_type / kv_cache_type_name (src/llama_model.cpp:16-17)
+    against the compiled reference's answers; host-only calls."""
+    g = golden("kv_types.npz")
+    assert [capi.kv_type_name(t) for t in range(3)] == g["names"].tolist()
+    assert capi.kv_type_name(7) == "?"
+    assert [capi.kv_parse_type(s) for s in ("f32", "f16", "q8", "q8_0")] == g["parsed"].tolist()
+    with pytest.raises(capi.MvhError, match="unknown KV cache type: bf16"):
+        capi.kv_parse_type("bf16")
+
+
 def test_header_compiles_as_c_and_links(tmp_path):
     """A plain C program (what a cgo / C++ shim sees) compiles against the
     header alone and links against the library; no call touches a device."""
@@ -44,6 +58,9 @@ int main(void) {
     if (mvh_version() < 1) return 1;
     if (mvh_kv_bytes_allocated(NULL, &bytes) != MVH_E_INVALID) return 2;
     if (!mvh_last_error()[0]) return 3;
+    int t = -1;
+    if (mvh_kv_parse_type("q8_0", &t) != MVH_OK || t != MVH_KV_Q8) return 4;
+    if (mvh_kv_type_name(MVH_KV_F32)[1] != '3') return 5;
     puts("ok");
     return 0;
 }

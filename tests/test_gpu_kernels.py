@@ -204,22 +204,35 @@ def test_read_row(ctx, oracle, ty, k):
 
 # ---------------------------------------------------------------- paged KV + attention
 
+KV_TYPES = {"f32": capi.MVH_KV_F32, "f16": capi.MVH_KV_F16, "q8": capi.MVH_KV_Q8}
+
+
+@pytest.mark.parametrize("tname", sorted(KV_TYPES))
 @pytest.mark.parametrize("kv_dim,page", [(288, 128), (256, 16), (4096, 128)])
-def test_kv_write_bits_and_pages(ctx, oracle, kv_dim, page):
-    rng = np.random.default_rng(kv_dim + page)
-    kv = ctx.kv_cache(2, kv_dim, page, 400)
-    okv = oracle.kv(kv_dim, page)
+def test_kv_write_bits_and_pages(ctx, oracle, kv_dim, page, tname):
+    """Stored rows (elements and the Q8 row scale) bit-identical to PagedKVCache::write."""
+    kt = KV_TYPES[tname]
+    rng = np.random.default_rng(kv_dim + page + kt)
+    kv = ctx.kv_cache(2, kv_dim, page, 400, kv_type=kt)
+    assert kv.type() == kt
+    okv = oracle.kv(kv_dim, page, kt)
     n = 300
     k = rng.standard_normal((n, kv_dim), dtype=np.float32) * np.float32(3)
     v = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    k[1] = 0.0                                  # Q8: all-zero row, scale 1
+    v[2, 5] = np.float32(-1e30)                 # Q8: one huge element, the rest round to 0
+    k[3, :4] = np.array([127.0, 0.5, -0.5, 2.5], np.float32)  # Q8: max 127 -> scale 1, ties away from zero
     kv.write(1, 0, k[:37], v[:37])          # a multi-token write
     for p in range(37, n):
         kv.write(1, p, k[p], v[p])
     for p in range(n):
         okv.write(p, k[p], v[p])
-    for p in (0, 36, 37, page - 1, page, n - 1):
-        assert np.array_equal(kv.read_row(1, p, 0), okv.row(p, 0))
-        assert np.array_equal(kv.read_row(1, p, 1), okv.row(p, 1))
+    for p in (0, 1, 2, 3, 36, 37, page - 1, page, n - 1):
+        for which in (0, 1):
+            got, gs = kv.read_row(1, p, which)
+            want, ws = okv.row(p, which)
+            assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), (p, which)
+            assert bits(gs) == bits(ws), (p, which, gs, ws)
     assert kv.bytes_allocated() == okv.bytes_allocated()
     with pytest.raises(capi.MvhError, match="page missing"):
         kv.read_row(0, 0, 0)
@@ -230,13 +243,15 @@ def test_kv_write_bits_and_pages(ctx, oracle, kv_dim, page):
     kv.close()
 
 
+@pytest.mark.parametrize("tname", sorted(KV_TYPES))
 @pytest.mark.parametrize("n_head,n_kv,hd,pos", [(6, 6, 48, 0), (6, 6, 48, 200), (32, 4, 64, 511),
                                                 (32, 32, 128, 767), (32, 32, 128, 130)])
-def test_attn_decode(ctx, oracle, n_head, n_kv, hd, pos):
+def test_attn_decode(ctx, oracle, n_head, n_kv, hd, pos, tname):
+    kt = KV_TYPES[tname]
     rng = np.random.default_rng(n_head + hd + pos)
     kv_dim = n_kv * hd
-    kv = ctx.kv_cache(1, kv_dim, 128, 1024)
-    okv = oracle.kv(kv_dim, 128)
+    kv = ctx.kv_cache(1, kv_dim, 128, 1024, kv_type=kt)
+    okv = oracle.kv(kv_dim, 128, kt)
     k = rng.standard_normal((pos + 1, kv_dim), dtype=np.float32)
     v = rng.standard_normal((pos + 1, kv_dim), dtype=np.float32)
     kv.write(0, 0, k, v)

@@ -137,3 +137,54 @@ def test_prefill_ragged_chunks_vs_oracle(tmp_path, oracle, max_batch, chunk):
     close(got, want, "decode after ragged prefill")
     assert int(np.argmax(got)) == int(np.argmax(want))
     m.close()
+
+
+KV_TYPES = {"f32": capi.MVH_KV_F32, "q8": capi.MVH_KV_Q8}
+
+
+@pytest.mark.parametrize("tname", sorted(KV_TYPES))
+@pytest.mark.parametrize("mode", [0, 1])
+def test_tiny_kv_types_vs_reference_golden(tiny, tname, mode):
+    """LlamaModel with kv_type F32 / Q8 (src/llama_model.cpp:16-56) against the
+    compiled reference run with the same cache type."""
+    g = golden("model_tiny.npz")
+    m = capi.Model(tiny, ctx=256, act_mode=mode, max_batch=32, kv_type=KV_TYPES[tname])
+    assert m.kv_type() == KV_TYPES[tname]
+    close(m.prefill(g["prompt"], 32), g[f"kv{tname}_prefill_logits_m{mode}"], f"kv {tname} prefill")
+    ids, cur = [], 17
+    for _ in range(12):
+        lg = m.forward(cur)
+        cur = int(np.argmax(lg))
+        ids.append(cur)
+    assert ids == g[f"kv{tname}_decode_ids_m{mode}"].tolist()
+    close(lg, g[f"kv{tname}_decode_last_logits_m{mode}"], f"kv {tname} decode")
+    assert m.kv_bytes() == int(g[f"kv{tname}_kv_bytes_m{mode}"])
+    # the captured-graph greedy loop runs the same cache type
+    m.reset()
+    m.prefill(g["prompt"], 32, logits=False)
+    assert m.generate_greedy(17, 12).tolist() == g[f"kv{tname}_decode_ids_m{mode}"].tolist()
+    m.close()
+
+
+@pytest.mark.parametrize("tname", sorted(KV_TYPES))
+@pytest.mark.parametrize("cfg_name", ["tinyllama-1.1b-mixed-2layer", "openllama-7b-v2-q4_0-1layer"])
+def test_kv_types_large_shapes_vs_oracle(tmp_path, oracle, cfg_name, tname):
+    """F32 / Q8 KV pages at the GQA and 7B shapes (prefill through the chunked
+    attention kernels, decode through the two-kernel path)."""
+    cfg = synth.CONFIGS[cfg_name]
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=41)
+    prompt = synth.prompt_tokens(12, 45)
+    kt = KV_TYPES[tname]
+    mo = oracle.model(path, ctx=256, force_q8=True, kv_type=kt)
+    m = capi.Model(path, ctx=256, act_mode=1, max_batch=32, kv_type=kt)
+    close(m.prefill(prompt, 32), mo.prefill(prompt, 32), f"{cfg_name} kv {tname} prefill")
+    cur = 7
+    for _ in range(3):
+        want = mo.forward(cur)
+        got = m.forward(cur)
+        close(got, want, f"{cfg_name} kv {tname} decode")
+        cur = int(np.argmax(want))
+        assert int(np.argmax(got)) == cur
+    assert m.kv_bytes() == mo.kv_bytes()
+    m.close()
