@@ -163,6 +163,41 @@ def time_prefill_gemm(reps: int):
     return out
 
 
+def time_kv_types(path: str, steps: int, warmup: int):
+    """tg and pp512 of the same model with the F32 and Q8 KV cache types
+    (LlamaModel's kv_type; decode attention then runs as RoPE + KV write +
+    scores + softmax-V launches instead of the fused F16 kernel)."""
+    import torch
+
+    from memvanta_amd import capi
+
+    out = []
+    for kt in (capi.MVH_KV_F32, capi.MVH_KV_Q8):
+        m = capi.Model(path, ctx=CTX, page_tokens=PAGE, act_mode=capi.MVH_ACT_Q8, max_batch=BATCH, kv_type=kt)
+        seed, prompt = fixed_tokens(SEED_TOKENS, m.vocab), fixed_tokens(PROMPT_TOKENS, m.vocab)
+        m.prefill(prompt, BATCH, logits=True)
+        m.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.prefill(prompt, BATCH, logits=True)
+        torch.cuda.synchronize()
+        pp = PROMPT_TOKENS / (time.perf_counter() - t0)
+        m.reset()
+        m.prefill(seed, BATCH, logits=False)
+        m.generate_greedy(FIRST_TOKEN, warmup)
+        m.reset()
+        m.prefill(seed, BATCH, logits=False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ids = m.generate_greedy(FIRST_TOKEN, steps)
+        torch.cuda.synchronize()
+        tg = steps / (time.perf_counter() - t0)
+        out.append({"kv": capi.kv_type_name(kt), "tg_tok_s": round(tg, 2), "pp512_tok_s": round(pp, 1),
+                    "kv_bytes_after_tg": m.kv_bytes(), "greedy_ids_head": [int(i) for i in ids[:4]]})
+        m.close()
+    return out
+
+
 def cpu_baseline(path: str, budget_s: float):
     """The reference CPU LlamaModel on the same GGUF: greedy decode after a short seed."""
     from oracle import pyoracle
@@ -201,6 +236,7 @@ def main():
     ap.add_argument("--copies", type=int, default=8, help="weight copies rotated in the GEMV kernel timing")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-kv-types", action="store_true", help="skip the F32 / Q8 KV cache runs")
     ap.add_argument("--model", default=None, help="existing GGUF to use instead of the synthetic 7B shape")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the isolated GEMV kernel timing plus a 256 MiB device copy (for counter runs)")
@@ -314,6 +350,8 @@ def main():
             with open(pmc) as f:
                 traffic = json.load(f).get("hbm_bytes_per_launch")
 
+        kv_types = None if args.no_kv_types else time_kv_types(path, args.steps, args.warmup)
+
         cpu = None if args.no_cpu else cpu_baseline(path, args.cpu_budget)
     finally:
         if tmpdir:
@@ -359,6 +397,7 @@ def main():
             "prefill_gemm_int8_mfma": gemm,
             "prefill_gemm_note": "tensor_matmul_batch_v06 FORCE_Q8 numerics incl. the activation quantizer; "
                                  "frac_int8_peak vs 5 POP/s dense int8",
+            "other_kv_cache_types": kv_types,
         },
         "roofline": {"bound": "hbm", "kernel": "gemv_q4_0 (persistent, pre-quantized Q8 input)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

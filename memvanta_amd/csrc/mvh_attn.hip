@@ -44,8 +44,10 @@ __global__ __launch_bounds__(256) void kv_write_kernel(void* const* __restrict__
 // row is all zero; fmaxf skips a NaN as std::max(m, NaN) keeps m), then
 // q = clamp(round_half_away(x / s), -127, 127) with an IEEE division (a NaN
 // quotient clamps to -127, as lround's x86 result does).  Workgroup = (token,
-// K or V).
-constexpr int kKW = 256;
+// K or V); each thread holds up to kKWV groups of 4 elements in registers, so
+// the row is read once (kv_dim <= 4 * kKW * kKWV).
+constexpr int kKW = 1024;
+constexpr int kKWV = 4;
 __global__ __launch_bounds__(kKW) void kv_write_q8_kernel(void* const* __restrict__ pt_k,
                                                           void* const* __restrict__ pt_v,
                                                           const float* __restrict__ k, const float* __restrict__ v,
@@ -54,8 +56,14 @@ __global__ __launch_bounds__(kKW) void kv_write_q8_kernel(void* const* __restric
     __shared__ float red[kKW / 64];
     const int t = blockIdx.x, which = blockIdx.y;
     const float* x = (which ? v : k) + static_cast<size_t>(t) * pitch;
+    float4 xv[kKWV];
     float m = 0.0f;
-    for (int d = threadIdx.x; d < kv_dim; d += kKW) m = fmaxf(m, fabsf(x[d]));
+#pragma unroll
+    for (int j = 0; j < kKWV; ++j) {
+        const int d = 4 * (j * kKW + static_cast<int>(threadIdx.x));
+        xv[j] = d < kv_dim ? *reinterpret_cast<const float4*>(x + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[j].x), fabsf(xv[j].y)), fmaxf(fabsf(xv[j].z), fabsf(xv[j].w))));
+    }
     m = group_max<32>(m);
     m = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
@@ -68,9 +76,16 @@ __global__ __launch_bounds__(kKW) void kv_write_q8_kernel(void* const* __restric
     const int p = (d_pos ? *d_pos : pos_arg) + t, slot = p % page_tokens;
     uint8_t* page = static_cast<uint8_t*>((which ? pt_v : pt_k)[p / page_tokens]);
     int8_t* row = reinterpret_cast<int8_t*>(page) + static_cast<size_t>(slot) * kv_dim;
-    for (int d = threadIdx.x; d < kv_dim; d += kKW) {
-        const float r = fminf(fmaxf(roundf(__fdiv_rn(x[d], s)), -127.0f), 127.0f);
-        row[d] = static_cast<int8_t>(r);
+    auto qz = [&](float z) {
+        const float r = fminf(fmaxf(roundf(__fdiv_rn(z, s)), -127.0f), 127.0f);
+        return static_cast<uint32_t>(static_cast<int>(r)) & 0xffu;
+    };
+#pragma unroll
+    for (int j = 0; j < kKWV; ++j) {
+        const int d = 4 * (j * kKW + static_cast<int>(threadIdx.x));
+        if (d < kv_dim)
+            *reinterpret_cast<uint32_t*>(row + d) =
+                qz(xv[j].x) | (qz(xv[j].y) << 8) | (qz(xv[j].z) << 16) | (qz(xv[j].w) << 24);
     }
     if (threadIdx.x == 0) reinterpret_cast<float*>(page + kv_scale_offset(page_tokens, kv_dim))[slot] = s;
 }
@@ -162,14 +177,21 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
                                                             int group, int hd, int kv_dim, int page_tokens,
                                                             int score_pitch, int8_t* __restrict__ q8,
                                                             float* __restrict__ q8d, bool q8_op) {
-    extern __shared__ float s_a[];
+    extern __shared__ float s_a[];  // [score_pitch] weights; Q8: then [score_pitch] V row scales
     __shared__ uint64_t s_tab[32];
     if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
-    __syncthreads();
     const int h = blockIdx.x, b = blockIdx.z;
     const int n = (d_pos ? *d_pos : pos_arg) + b + 1;
+    if constexpr (KT == kKvQ8) {  // V row scales: loads issued before the softmax, in flight meanwhile
+        float* s_vs = s_a + score_pitch;
+#pragma unroll 4
+        for (int t = threadIdx.x; t < n; t += 64)
+            s_vs[t] = kv_row_scale<KT>(pt_v[t / page_tokens], t % page_tokens, page_tokens, kv_dim);
+    }
+    __syncthreads();
     const float* sc = scores + (static_cast<size_t>(b) * n_head + h) * score_pitch;
     float mx = -INFINITY;
+#pragma unroll 4
     for (int t = threadIdx.x; t < n; t += 64) mx = fmaxf(mx, sc[t]);
     mx = wave_max(mx);
     double den = 0.0;
@@ -184,7 +206,7 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
     const int kh = h / group;
     for (int t = threadIdx.x; t < n; t += 64) {
         float a = s_a[t] * inv;
-        if constexpr (KT == kKvQ8) a = a * kv_row_scale<KT>(pt_v[t / page_tokens], t % page_tokens, page_tokens, kv_dim);
+        if constexpr (KT == kKvQ8) a = a * s_a[score_pitch + t];
         s_a[t] = a;
     }
     __syncthreads();
@@ -675,6 +697,7 @@ hipError_t launch_kv_write(int kv_type, void* const* pt_k, void* const* pt_v, co
         kv_write_kernel<kKvF16><<<blocks, 256, 0, st>>>(pt_k, pt_v, k, v, ip, d_pos, ipos, nt, kd, pt);
         break;
     case kKvQ8:
+        if (kv_dim % 4 || kv_dim > 4 * kKW * kKWV || pitch % 4) return hipErrorInvalidValue;
         kv_write_q8_kernel<<<dim3(static_cast<unsigned>(n_tokens), 2), kKW, 0, st>>>(pt_k, pt_v, k, v, ip, d_pos, ipos,
                                                                                   kd, pt);
         break;
@@ -700,7 +723,7 @@ hipError_t attn_typed(const void* const* pt_k, const void* const* pt_v, const fl
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 g2(static_cast<unsigned>(n_head), static_cast<unsigned>((hd + 63) / 64), static_cast<unsigned>(B));
-    attn_softmax_v_kernel<KT><<<g2, 64, max_pos * sizeof(float), st>>>(
+    attn_softmax_v_kernel<KT><<<g2, 64, (KT == kKvQ8 ? 2 : 1) * max_pos * sizeof(float), st>>>(
         pt_v, scores, out, d_pos, static_cast<int>(pos), static_cast<int>(n_head), group, static_cast<int>(hd),
         static_cast<int>(kv_dim), static_cast<int>(page_tokens), pitch, q8, q8d, q8_op);
     return hipGetLastError();
@@ -770,6 +793,9 @@ hipError_t launch_attn_prefill(int kv_type, const void* const* pt_k, const void*
 hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
                               float* scores, float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd,
                               size_t kv_dim, size_t page_tokens, hipStream_t st) {
+    if (hd % 32 == 0)  // V tiles staged in LDS by whole workgroups (latency-bound otherwise)
+        return launch_attn_prefill(kv_type, pt_k, pt_v, q, n_head * hd, scores, out, nullptr, nullptr, false, nullptr,
+                                   pos, pos + 1, 1, n_head, n_head_kv, hd, kv_dim, page_tokens, st);
     return launch_attn(kv_type, pt_k, pt_v, q, n_head * hd, scores, out, nullptr, pos, pos + 1, 1, n_head, n_head_kv,
                        hd, kv_dim, page_tokens, st);
 }

@@ -357,6 +357,12 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
                                                 o_q8 ? q8_ : nullptr, q8d_, c_.n_head, c_.n_head_kv, hd, c_.n_ctx,
                                                 stream_),
                   "attention");
+        } else if (hd % 32 == 0) {  // F32 / Q8 pages: the chunk kernels with one query token
+            store_kv(lay, pk, pv, d_pos_, 0, 1);
+            check(mvh::launch_attn_prefill(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, o_q8 ? q8_ : nullptr,
+                                           q8d_, false, d_pos_, 0, c_.n_ctx, 1, c_.n_head, c_.n_head_kv, hd,
+                                           c_.kv_dim(), page_tokens_, stream_),
+                  "attention");
         } else {
             store_kv(lay, pk, pv, d_pos_, 0, 1);
             check(mvh::launch_attn(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, d_pos_, 0, c_.n_ctx, 1,
