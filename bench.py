@@ -15,6 +15,8 @@ real_model_bench (benchmarks/real_model_bench.cpp:20-27):
 * pp512: reset, prefill 512 prompt ids in chunks of 32 with last-token
   logits (tensor_matmul_batch_v06 numerics, MEMVANTA_FORCE_Q8_ACT=1 mode).
 * prompt ids follow the reference bench's fixed_tokens: (i*1543+17) % vocab.
+* the same tg and pp512 are timed beside it with F32 and Q8 KV pages
+  (LlamaModel's kv_type) and reported under config.other_kv_cache_types.
 
 `roofline` times the dominant kernel, the Q4_0 x Q8 decode GEMV, alone at the
 launches of one 7B decode layer (q|k|v fused [4096->12288], o [4096->4096],
