@@ -266,15 +266,21 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
 // from L2).
 constexpr int kAT = 256;
 constexpr int kRV = 512;        // V rows per staging round
+constexpr int kRVP = kRV + 8;   // LDS pitch of a transposed V dimension: 1040 bytes, so the
+                                // lanes' 16-byte row reads fall in different banks (at 1024
+                                // bytes all 32 lanes hit one bank)
 constexpr int kMaxPages = 128;  // page-table entries staged in LDS
 
-template <int SW>
+// HD != 0 fixes head_dim at compile time (the loops over it unroll and the
+// LDS reads of q are scheduled ahead of their use); HD == 0 reads hd_arg.
+template <int SW, int HD>
 __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int* __restrict__ d_pos,
     uint16_t* const* __restrict__ pt_k, uint16_t* const* __restrict__ pt_v, int page_tokens, int max_pages,
-    float* __restrict__ out, int8_t* __restrict__ q8, float* __restrict__ q8d, int group, int hd, int kv_dim,
+    float* __restrict__ out, int8_t* __restrict__ q8, float* __restrict__ q8d, int group, int hd_arg, int kv_dim,
     int ctx_pad, int nslice) {
+    const int hd = HD ? HD : hd_arg;
     constexpr int kCh = SW / 8;                        // 16-byte chunks per V row slice
     constexpr int kVPT = (kRV * kCh + kAT - 1) / kAT;  // chunks per thread per round
     extern __shared__ __align__(16) float sm[];
@@ -282,7 +288,7 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     float* s_k = sm + hd;
     float* s_v = sm + 2 * hd;
     float* s_a = sm + 3 * hd;
-    uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_a + ctx_pad);  // [SW][kRV]
+    uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_a + ctx_pad);  // [SW][kRVP]
     __shared__ float red_f[kAT / 64];
     __shared__ double red_d[kAT / 64];
     __shared__ uint64_t s_tab[32];
@@ -300,26 +306,24 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
         s_pv[i] = pt_v[i];
     }
     if (t < 32) s_tab[t] = mvh_expf_tab(t);
-    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
-    if (t < half) {
-        const float* qh = q + static_cast<size_t>(h) * hd;
-        const float* kk = k + static_cast<size_t>(kh) * hd;
-        const float* vv = v + static_cast<size_t>(kh) * hd;
-        q0 = qh[t];
-        q1 = qh[t + half];
-        k0 = kk[t];
-        k1 = kk[t + half];
-        v0 = vv[t];
-        v1 = vv[t + half];
-    }
+    // Every global load of round trips 1 and 2 is unconditional (threads
+    // without a use read an in-bounds element and ignore it): the compiler's
+    // wait counts then let RoPE wait for cos/sin alone while the K rows and
+    // V round 0 are still in flight (a load under a branch makes it wait for
+    // all of them).
+    const int th = t < half ? t : 0;
+    const float* qh = q + static_cast<size_t>(h) * hd;
+    const float* kk = k + static_cast<size_t>(kh) * hd;
+    const float* vv = v + static_cast<size_t>(kh) * hd;
+    const float q0 = qh[th], q1 = qh[th + half], k0 = kk[th], k1 = kk[th + half], v0 = vv[th], v1 = vv[th + half];
     __syncthreads();
 
-    // round trip 2: cos/sin, this thread's first K row, V round 0
-    float cs = 0.f, sn = 0.f;
-    if (t < half) {
-        cs = cos_t[static_cast<size_t>(pos) * half + t];
-        sn = sin_t[static_cast<size_t>(pos) * half + t];
-    }
+    // round trip 2: cos/sin, this thread's first K row, V round 0 -- issued
+    // in that order (the scheduling barriers keep it), so RoPE waits for the
+    // first two loads only
+    const float cs = cos_t[static_cast<size_t>(pos) * half + th];
+    const float sn = sin_t[static_cast<size_t>(pos) * half + th];
+    __builtin_amdgcn_sched_barrier(0);
     auto krow_of = [&](int tt) {
         return s_pk[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
     };
@@ -330,7 +334,7 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
         for (int j = 0; j < 16; ++j)
             if (c0 + 8 * j < hd) kv[j] = ld_global16(kr + 8 * j);
     };
-    if (t < pos) load_k(t, 0);
+    load_k(t < pos ? t : 0, 0);  // rows past pos: row 0 (written, unused)
     uint4 vr[kVPT];
     auto load_round = [&](int r0) {
         // branch-free: chunks past the round's rows re-read row r0 (ignored)
@@ -343,15 +347,18 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
                                 dbase + (c % kCh) * 8);
         }
     };
-    if (pos > 0) load_round(0);
+    load_round(0);  // at pos 0 every chunk reads row 0 (unused)
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 1. RoPE, K/V of the current position
+    // 1. RoPE, K/V of the current position (computed by every thread, so the
+    // cos/sin loads are used outside a branch; threads t >= half drop it)
+    const float rq0 = fmaf(q0, cs, -(q1 * sn)), rq1 = fmaf(q0, sn, q1 * cs);
+    const uint16_t hk0 = f2h_ref(fmaf(k0, cs, -(k1 * sn))), hk1 = f2h_ref(fmaf(k0, sn, k1 * cs));
+    const uint16_t hv0 = f2h_ref(v0), hv1 = f2h_ref(v1);
     if (t < half) {
         const size_t off = static_cast<size_t>(pos % page_tokens) * kv_dim + kh * hd;
-        s_q[t] = fmaf(q0, cs, -(q1 * sn));
-        s_q[t + half] = fmaf(q0, sn, q1 * cs);
-        const uint16_t hk0 = f2h_ref(fmaf(k0, cs, -(k1 * sn))), hk1 = f2h_ref(fmaf(k0, sn, k1 * cs));
-        const uint16_t hv0 = f2h_ref(v0), hv1 = f2h_ref(v1);
+        s_q[t] = rq0;
+        s_q[t + half] = rq1;
         s_k[t] = h2f(hk0);
         s_k[t + half] = h2f(hk1);
         s_v[t] = h2f(hv0);
@@ -437,38 +444,57 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
                 const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    s_vt[(d0 + e) * kRV + row] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+                    s_vt[(d0 + e) * kRVP + row] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
             }
         }
         __syncthreads();  // also orders the s_a writes above before their reads
         if (r0 + kRV < pos) load_round(r0 + kRV);
         if (t < SW) {
-            const uint16_t* vl = s_vt + t * kRV;
+            const uint16_t* vl = s_vt + t * kRVP;
             const float* al = s_a + r0;
-            int j = 0;
-            if (rows >= 16) {
-                // software pipeline over 16-row steps: the next 16 rows are
-                // read from LDS while the current 16 are summed
-                uint4 v0 = *reinterpret_cast<const uint4*>(vl), v1 = *reinterpret_cast<const uint4*>(vl + 8);
-                float4 a[4];
+            // 16-row steps with two register sets used in turn (A even, B
+            // odd).  Every LDS read is unconditional -- the read for a step
+            // past the last one re-reads the last step (in bounds, unused) --
+            // so the wait counts only cover the set being summed and the
+            // next set's reads stay in flight during the fma chain.
+            const int nsteps = rows >> 4;
+            auto ld = [&](int st, uint4& v0, uint4& v1, float4 (&a)[4]) {
+                const int j0 = min(st, nsteps - 1) << 4;
+                v0 = *reinterpret_cast<const uint4*>(vl + j0);
+                v1 = *reinterpret_cast<const uint4*>(vl + j0 + 8);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(al + 4 * i);
-                for (; j + 16 <= rows; j += 16) {
-                    const half8 h0 = as_half8(v0), h1 = as_half8(v1);
-                    const float av[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
-                                          a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
-                    if (j + 32 <= rows) {
-                        v0 = *reinterpret_cast<const uint4*>(vl + j + 16);
-                        v1 = *reinterpret_cast<const uint4*>(vl + j + 24);
+                for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(al + j0 + 4 * i);
+            };
+            auto step = [&](float c, const uint4& v0, const uint4& v1, const float4 (&a)[4]) {
+                const half8 h0 = as_half8(v0), h1 = as_half8(v1);
+                const float av[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
+                                      a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(al + j + 16 + 4 * i);
-                    }
+                for (int e = 0; e < 8; ++e) c = fmaf(av[e], static_cast<float>(h0[e]), c);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc = fmaf(av[e], static_cast<float>(h0[e]), acc);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc = fmaf(av[8 + e], static_cast<float>(h1[e]), acc);
+                for (int e = 0; e < 8; ++e) c = fmaf(av[8 + e], static_cast<float>(h1[e]), c);
+                return c;
+            };
+            if (nsteps > 0) {
+                uint4 va0, va1, vb0, vb1;
+                float4 aa[4], ab[4];
+                ld(0, va0, va1, aa);
+                for (int st = 0; st < nsteps; st += 2) {
+                    // scheduling barriers keep each set's reads ahead of the
+                    // other set's fma chain
+                    ld(st + 1, vb0, vb1, ab);
+                    __builtin_amdgcn_sched_barrier(0);
+                    acc = step(acc, va0, va1, aa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    ld(st + 2, va0, va1, aa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    // the odd step always runs (no branch for its reads to sink
+                    // into) and is kept only when it exists
+                    const float nb = step(acc, vb0, vb1, ab);
+                    acc = st + 1 < nsteps ? nb : acc;
                 }
             }
+            int j = nsteps << 4;
             for (; j < rows; ++j) acc = fmaf(al[j], h2f(vl[j]), acc);
         }
         __syncthreads();
@@ -809,23 +835,25 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
     const int sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
     const int nslice = static_cast<int>(hd) / sw;
     const int ctx_pad = static_cast<int>((max_ctx + 3) / 4 * 4);
-    const size_t lds = (3 * hd + ctx_pad) * sizeof(float) + static_cast<size_t>(kRV) * sw * sizeof(uint16_t);
+    const size_t lds = (3 * hd + ctx_pad) * sizeof(float) + static_cast<size_t>(kRVP) * sw * sizeof(uint16_t);
     const dim3 grid(static_cast<unsigned>(n_head * nslice));
     const int group = static_cast<int>(n_head / n_head_kv), kvd = static_cast<int>(n_head_kv * hd);
-#define MVH_ATTN_FUSED(SW_)                                                                                          \
-    attn_decode_fused_kernel<SW_><<<grid, kAT, lds, st>>>(q, k, v, cos_t, sin_t, d_pos, pt_k, pt_v,                 \
-                                                          static_cast<int>(page_tokens), max_pages, out, q8, q8d,  \
-                                                          group, static_cast<int>(hd), kvd, ctx_pad, nslice)
-    if (sw == 32) MVH_ATTN_FUSED(32);
-    else if (sw == 16) MVH_ATTN_FUSED(16);
-    else MVH_ATTN_FUSED(8);
+#define MVH_ATTN_FUSED(SW_, HD_)                                                                                     \
+    attn_decode_fused_kernel<SW_, HD_><<<grid, kAT, lds, st>>>(q, k, v, cos_t, sin_t, d_pos, pt_k, pt_v,            \
+                                                               static_cast<int>(page_tokens), max_pages, out, q8,  \
+                                                               q8d, group, static_cast<int>(hd), kvd, ctx_pad,      \
+                                                               nslice)
+    if (sw == 32 && hd == 128) MVH_ATTN_FUSED(32, 128);
+    else if (sw == 32) MVH_ATTN_FUSED(32, 0);
+    else if (sw == 16) MVH_ATTN_FUSED(16, 0);
+    else MVH_ATTN_FUSED(8, 0);
 #undef MVH_ATTN_FUSED
     return hipGetLastError();
 }
 
 bool attn_decode_fused_ok(size_t hd, size_t max_ctx, size_t page_tokens) {
     const size_t sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
-    const size_t lds = (3 * hd + (max_ctx + 3) / 4 * 4) * sizeof(float) + kRV * sw * sizeof(uint16_t);
+    const size_t lds = (3 * hd + (max_ctx + 3) / 4 * 4) * sizeof(float) + kRVP * sw * sizeof(uint16_t);
     return hd >= 8 && hd % 8 == 0 && hd <= 2 * kAT && max_ctx >= 1 && page_tokens >= 1 &&
            (max_ctx + page_tokens - 1) / page_tokens <= kMaxPages && lds <= 56 * 1024;
 }
