@@ -103,7 +103,10 @@ def test_gemv_q8_0_bitexact(ctx, oracle, k, n):
     t.free()
 
 
-@pytest.mark.parametrize("k,n", [(4096, 32000), (2048, 32000), (5632, 2048), (256, 64)])
+# row counts that leave the last workgroup's waves partly or wholly idle, odd
+# and even super-block counts per row
+@pytest.mark.parametrize("k,n", [(4096, 32000), (2048, 32000), (5632, 2048), (256, 64), (6144, 1000), (8192, 37),
+                                 (11008, 64)])
 def test_gemv_q6_k(ctx, oracle, k, n):
     rng = np.random.default_rng(3 * k + n)
     w = _w(rng, synth.Q6_K, n, k)
