@@ -604,6 +604,26 @@ struct PvTile {
     typedef typename KvElem<KT>::T E;
     static constexpr int kPitch = 32 + 16 / static_cast<int>(sizeof(E));
 };
+// Four consecutive stored elements of one V row, as read from the LDS tile.
+template <int KT>
+struct PvRaw;
+template <>
+struct PvRaw<kKvF32> {
+    typedef float4 T;
+    static __device__ __forceinline__ float at(const T& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }
+};
+template <>
+struct PvRaw<kKvF16> {
+    typedef half4v T;  // f16 operands go straight into v_fma_mix
+    static __device__ __forceinline__ float at(const T& v, int k) { return static_cast<float>(v[k]); }
+};
+template <>
+struct PvRaw<kKvQ8> {
+    typedef uint32_t T;
+    static __device__ __forceinline__ float at(const T& v, int k) {
+        return static_cast<float>(static_cast<int8_t>(v >> (8 * k)));
+    }
+};
 template <int KT>
 __global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const void* const* __restrict__ pt_v,
                                                             const float* __restrict__ a, float* __restrict__ out,
@@ -661,27 +681,39 @@ __global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const void* const* _
         if (r0 + kPVRows < nmax) fetch(r0 + kPVRows);
         // rows past nmax in the last tile carry weight 0 (areg) over finite rows: no-ops
         const int rows4 = min(kPVRows, (nmax - r0 + 3) & ~3);
-        for (int rr = 0; rr < rows4; rr += 4) {
-            const float4 w4 = *reinterpret_cast<const float4*>(&s_at[tb][rr]);
+        // 4-row steps with two register sets used in turn; every LDS read is
+        // unconditional (a step past the last re-reads the last one, unused)
+        // and the scheduling barriers keep the next set's reads ahead of the
+        // current set's fmas, so the wait counts never cover them
+        typedef typename PvRaw<KT>::T R;
+        const int nst = rows4 >> 2;
+        auto ld = [&](int st, float4& w, R (&v)[4]) {
+            const int r = min(st, nst - 1) << 2;
+            w = *reinterpret_cast<const float4*>(&s_at[tb][r]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const R*>(&s_v[r + i][dq]);
+        };
+        auto step = [&](float (&c)[4], const float4& w4, const R (&v)[4]) {
             const float w[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float vf[4];
-                if constexpr (KT == kKvF32) {
-                    const float4 v = *reinterpret_cast<const float4*>(&s_v[rr + i][dq]);
-                    vf[0] = v.x, vf[1] = v.y, vf[2] = v.z, vf[3] = v.w;
-                } else if constexpr (KT == kKvF16) {  // f16 operands straight into v_fma_mix
-                    const half4v v = *reinterpret_cast<const half4v*>(&s_v[rr + i][dq]);
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) vf[k] = static_cast<float>(v[k]);
-                } else {
-                    const uint32_t v = *reinterpret_cast<const uint32_t*>(&s_v[rr + i][dq]);
+                for (int k = 0; k < 4; ++k) c[k] = fmaf(w[i], PvRaw<KT>::at(v[i], k), c[k]);
+        };
+        float4 wa, wb;
+        R va[4], vb[4];
+        ld(0, wa, va);
+        for (int st = 0; st < nst; st += 2) {
+            ld(st + 1, wb, vb);
+            __builtin_amdgcn_sched_barrier(0);
+            step(acc, wa, va);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(st + 2, wa, va);
+            __builtin_amdgcn_sched_barrier(0);
+            float nx[4] = {acc[0], acc[1], acc[2], acc[3]};  // the odd step, kept when it exists
+            step(nx, wb, vb);
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) vf[k] = static_cast<float>(static_cast<int8_t>(v >> (8 * k)));
-                }
-#pragma unroll
-                for (int k = 0; k < 4; ++k) acc[k] = fmaf(w[i], vf[k], acc[k]);
-            }
+            for (int k = 0; k < 4; ++k) acc[k] = st + 1 < nst ? nx[k] : acc[k];
         }
         __syncthreads();
     }
@@ -762,6 +794,10 @@ hipError_t attn_prefill_typed(const void* const* pt_k, const void* const* pt_v, 
                               size_t kv_dim, size_t page_tokens, hipStream_t st) {
     const int group = static_cast<int>(n_head / n_head_kv);
     const int pitch = static_cast<int>(max_pos);  // weight row pitch >= last position + 1
+    // one workgroup per (head, token): all of a chunk's workgroups resident
+    // at once (a 128-wide compile-time head_dim that hoists the K loads, or
+    // several tokens per workgroup sharing them, need more registers and run
+    // slower)
     attn_scores_softmax_kernel<KT><<<dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(B)), kSM,
                                      (hd + max_pos) * sizeof(float), st>>>(
         pt_k, pt_v, q, static_cast<int>(q_pitch), a_scratch, d_pos, static_cast<int>(pos), static_cast<int>(n_head),

@@ -212,26 +212,53 @@ __device__ __forceinline__ float kv_to_f(const void* row, int e) {
     else return static_cast<float>(static_cast<const int8_t*>(row)[e]);
 }
 
-// Eight consecutive elements (16/8/4-byte aligned for F32/F16/Q8) of a stored
-// row, converted exactly.
+// Eight consecutive stored elements (16/8/4-byte aligned for F32/F16/Q8) of
+// a row: kv_raw8 loads them as stored, kv_cvt8 converts them exactly.
 template <int KT>
-__device__ __forceinline__ void kv_load8(const void* row, int e, float (&f)[8]) {
+struct KvRaw8 {
+    uint4 a, b;  // F32: two 16-byte halves
+};
+template <>
+struct KvRaw8<kKvF16> {
+    uint4 a;
+};
+template <>
+struct KvRaw8<kKvQ8> {
+    uint2 a;
+};
+template <int KT>
+__device__ __forceinline__ KvRaw8<KT> kv_raw8(const void* row, int e) {
+    KvRaw8<KT> r;
     if constexpr (KT == kKvF32) {
         const float* p = static_cast<const float*>(row) + e;
-        const uint4 a = ld_global16(p), b = ld_global16(p + 4);
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        r.a = ld_global16(p);
+        r.b = ld_global16(p + 4);
+    } else if constexpr (KT == kKvF16) {
+        r.a = ld_global16(static_cast<const uint16_t*>(row) + e);
+    } else {
+        r.a = ld_global8(static_cast<const int8_t*>(row) + e);
+    }
+    return r;
+}
+template <int KT>
+__device__ __forceinline__ void kv_cvt8(const KvRaw8<KT>& r, float (&f)[8]) {
+    if constexpr (KT == kKvF32) {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) f[j] = __uint_as_float(w[j]);
     } else if constexpr (KT == kKvF16) {
-        const half8 h = as_half8(ld_global16(static_cast<const uint16_t*>(row) + e));
+        const half8 h = as_half8(r.a);
 #pragma unroll
         for (int j = 0; j < 8; ++j) f[j] = static_cast<float>(h[j]);
     } else {
-        const uint2 w = ld_global8(static_cast<const int8_t*>(row) + e);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            f[j] = static_cast<float>(static_cast<int8_t>((j < 4 ? w.x : w.y) >> (8 * (j & 3))));
+            f[j] = static_cast<float>(static_cast<int8_t>((j < 4 ? r.a.x : r.a.y) >> (8 * (j & 3))));
     }
+}
+template <int KT>
+__device__ __forceinline__ void kv_load8(const void* row, int e, float (&f)[8]) {
+    kv_cvt8<KT>(kv_raw8<KT>(row, e), f);
 }
 
 // Q8 row scale of slot `slot` of a page (1 for the other types).
