@@ -188,3 +188,27 @@ def test_kv_types_large_shapes_vs_oracle(tmp_path, oracle, cfg_name, tname):
         assert int(np.argmax(got)) == cur
     assert m.kv_bytes() == mo.kv_bytes()
     m.close()
+
+
+@pytest.mark.parametrize("tname", ["f32", "f16", "q8"])
+@pytest.mark.parametrize("cfg_name,page", [("tiny", 7), ("openllama-7b-v2-q4_0-1layer", 16)])
+def test_page_sizes_vs_oracle(tmp_path, oracle, cfg_name, page, tname):
+    """KV pages of 7 and 16 tokens (positions cross many page boundaries in
+    one prefill chunk and in the V staging rounds) with every cache type."""
+    kt = {"f32": capi.MVH_KV_F32, "f16": capi.MVH_KV_F16, "q8": capi.MVH_KV_Q8}[tname]
+    cfg = synth.TINY if cfg_name == "tiny" else synth.CONFIGS[cfg_name]
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=57)
+    prompt = synth.prompt_tokens(21, 70)
+    mo = oracle.model(path, ctx=256, page=page, force_q8=True, kv_type=kt)
+    m = capi.Model(path, ctx=256, page_tokens=page, act_mode=1, max_batch=32, kv_type=kt)
+    close(m.prefill(prompt, 32), mo.prefill(prompt, 32), f"page {page} kv {tname} prefill")
+    cur = 3
+    for _ in range(3):
+        want = mo.forward(cur)
+        got = m.forward(cur)
+        close(got, want, f"page {page} kv {tname} decode")
+        cur = int(np.argmax(want))
+        assert int(np.argmax(got)) == cur
+    assert m.kv_bytes() == mo.kv_bytes()
+    m.close()
