@@ -29,6 +29,8 @@
  *   mvh_kv_type_name      kv_cache_type_name       llama_model.hpp:30, src/llama_model.cpp:17
  *   mvh_attn_decode       the per-head dot_key/softmax/add_value loop of
  *                         LlamaModel::forward      src/llama_model.cpp:256
+ *   mvh_attn_batch        the per-(token, head) loop of
+ *                         LlamaModel::forward_batch_impl  src/llama_model.cpp:248
  *   mvh_tensor_upload     GgufFile::tensor_data    include/memvanta/gguf.hpp:57, src/gguf.cpp:139
  *                         (the bytes it returns are copied to HBM once)
  *   mvh_model_*           LlamaModel               include/memvanta/llama_model.hpp:100-138,
@@ -145,6 +147,11 @@ int mvh_kv_read_row(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, size
 /* decode attention of one layer over positions 0..pos: q[n_head*hd] -> out[n_head*hd] */
 int mvh_attn_decode(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos,
                     size_t n_head, size_t n_head_kv, size_t head_dim, float* out, int ptr_kind);
+/* the batched causal attention of LlamaModel::forward_batch_impl (the per-(token, head) loop at
+ * src/llama_model.cpp:248) for n_tokens query tokens at positions pos..pos+n_tokens-1, whose K/V rows are
+ * already written: token b attends over positions 0..pos+b; q[n_tokens][n_head*hd] -> out[n_tokens][n_head*hd] */
+int mvh_attn_batch(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos,
+                   size_t n_tokens, size_t n_head, size_t n_head_kv, size_t head_dim, float* out, int ptr_kind);
 
 /* ---- whole model: LlamaModel on one device (weights, paged KV and activations in HBM) ---- */
 /* kv_type is LlamaModel's kv_type argument (MVH_KV_F16 is its default); act_mode selects the prefill numerics

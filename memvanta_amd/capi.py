@@ -70,6 +70,7 @@ _SIGS = {
     "mvh_kv_write": (_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _int]),
     "mvh_kv_read_row": (_int, [_vp, _vp, _sz, _sz, _int, _vp, C.POINTER(C.c_float)]),
     "mvh_attn_decode": (_int, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _vp, _int]),
+    "mvh_attn_batch": (_int, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _int]),
     "mvh_model_open": (_int, [C.c_char_p, _int, _sz, _sz, _int, _int, _sz, C.POINTER(_vp)]),
     "mvh_model_kv_type": (_int, [_vp, C.POINTER(_int)]),
     "mvh_model_close": (_int, [_vp]),
@@ -321,6 +322,15 @@ class KVCache:
         t = _int()
         self.ctx._check(self.ctx.lib.mvh_kv_type(self.h, C.byref(t)))
         return t.value
+
+    def attn_batch(self, layer, q, pos, n_tokens, n_head, n_head_kv, head_dim, out=None):
+        """causal attention of n_tokens query tokens at positions pos.. (q: [n_tokens][n_head*head_dim])"""
+        if out is None:
+            q = np.ascontiguousarray(q, np.float32)
+            out = np.empty((n_tokens, n_head * head_dim), np.float32)
+        self.ctx._check(self.ctx.lib.mvh_attn_batch(self.ctx.h, self.h, layer, _ptr(q), pos, n_tokens, n_head,
+                                                    n_head_kv, head_dim, _ptr(out), _kind(q, out)))
+        return out
 
     def attn_decode(self, layer, q, pos, n_head, n_head_kv, head_dim, out=None):
         if out is None:

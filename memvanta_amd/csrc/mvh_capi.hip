@@ -713,6 +713,43 @@ int mvh_attn_decode(mvh_context* c, const mvh_kv_cache* kv, size_t layer, const 
     return finish_out(c, out, od, qn * 4, kind);
 }
 
+int mvh_attn_batch(mvh_context* c, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos, size_t n_tokens,
+                   size_t n_head, size_t n_head_kv, size_t head_dim, float* out, int kind) {
+    CHECK_CTX(c);
+    if (int rc = check_kv(kv, layer)) return rc;
+    if (!n_tokens) return MVH_OK;
+    if (!q || !out) return fail(MVH_E_INVALID, "null q/out");
+    if (!n_head || !n_head_kv || n_head % n_head_kv || !head_dim)
+        return fail(MVH_E_SHAPE, "invalid Llama head configuration");
+    if (head_dim % 8 || n_head_kv * head_dim > kv->kv_dim)
+        return fail(MVH_E_SHAPE, "head_dim must be a multiple of 8 and n_head_kv*head_dim <= kv_dim");
+    if (pos + n_tokens > kv->max_tokens) return fail(MVH_E_RANGE, "context exhausted");
+    const size_t last = pos + n_tokens - 1;
+    for (size_t p = 0; p <= last / kv->page_tokens; ++p)
+        if (!kv->hk[layer * kv->max_pages + p]) return fail(MVH_E_RANGE, "KV key page missing");
+    const size_t qn = n_tokens * n_head * head_dim;
+    const void* qd = nullptr;
+    if (int rc = stage_in(c, c->xin, q, qn * 4, kind, &qd)) return rc;
+    float* od = out;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, qn * 4)) return rc;
+        od = static_cast<float*>(c->yout.p);
+    }
+    if (int rc = grow(c, c->scratch, n_tokens * n_head * (last + 1) * 4)) return rc;
+    const size_t base = layer * kv->max_pages;
+    const float* qf = static_cast<const float*>(qd);
+    float* sc = static_cast<float*>(c->scratch.p);
+    if (head_dim % 32 == 0)  // scores once per (token, head), V tiles shared by groups of 32 tokens
+        MVH_HIP(mvh::launch_attn_prefill(kv->type, kv->dk + base, kv->dv + base, qf, n_head * head_dim, sc, od, nullptr,
+                                         nullptr, false, nullptr, pos, last + 1, n_tokens, n_head, n_head_kv, head_dim,
+                                         kv->kv_dim, kv->page_tokens, c->stream));
+    else
+        MVH_HIP(mvh::launch_attn(kv->type, kv->dk + base, kv->dv + base, qf, n_head * head_dim, sc, od, nullptr, pos,
+                                 last + 1, n_tokens, n_head, n_head_kv, head_dim, kv->kv_dim, kv->page_tokens,
+                                 c->stream));
+    return finish_out(c, out, od, qn * 4, kind);
+}
+
 }  // extern "C"
 
 namespace {

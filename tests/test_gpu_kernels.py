@@ -268,3 +268,31 @@ def test_attn_decode(ctx, oracle, n_head, n_kv, hd, pos, tname):
     assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
     print(f"attn exact fraction {(bits(got) == bits(want)).mean():.4f}")
     kv.close()
+
+
+@pytest.mark.parametrize("tname", sorted(KV_TYPES))
+@pytest.mark.parametrize("n_head,n_kv,hd,pos,B", [(32, 4, 128, 100, 45), (32, 32, 128, 0, 32), (6, 6, 48, 37, 5),
+                                                  (8, 2, 64, 300, 1)])
+def test_attn_batch(ctx, oracle, n_head, n_kv, hd, pos, B, tname):
+    """The batched causal attention of forward_batch_impl (src/llama_model.cpp:248): token b of the batch
+    equals decode attention at position pos + b over the same cache."""
+    kt = KV_TYPES[tname]
+    rng = np.random.default_rng(n_head + hd + pos + B)
+    kv_dim = n_kv * hd
+    kv = ctx.kv_cache(1, kv_dim, 128, 1024, kv_type=kt)
+    okv = oracle.kv(kv_dim, 128, kt)
+    n = pos + B
+    k = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    kv.write(0, 0, k, v)
+    for p in range(n):
+        okv.write(p, k[p], v[p])
+    q = rng.standard_normal((B, n_head * hd), dtype=np.float32) * np.float32(2)
+    got = kv.attn_batch(0, q, pos, B, n_head, n_kv, hd)
+    want = np.stack([okv.attn_decode(q[b], pos + b, n_head, n_kv, hd) for b in range(B)])
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel <= 1e-6, rel
+    assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+    with pytest.raises(capi.MvhError, match="context exhausted"):
+        kv.attn_batch(0, q, 1024 - B + 1, B, n_head, n_kv, hd)
+    kv.close()
