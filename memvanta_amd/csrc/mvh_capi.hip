@@ -176,6 +176,12 @@ int fp32_rows(mvh_context* c, const mvh_tensor* w, const float* xd, float* yd, s
             if (cols % 256) return fail(MVH_E_SHAPE, "Q6_K %s row not block aligned: %s", what, w->name.c_str());
             MVH_HIP(mvh::launch_gemv_q6_k(W, xd, yd, rows, cols, batch, c->stream));
             return MVH_OK;
+        case MVH_TYPE_F32:
+            MVH_HIP(mvh::launch_gemv_f32(reinterpret_cast<const float*>(W), xd, yd, rows, cols, batch, c->stream));
+            return MVH_OK;
+        case MVH_TYPE_F16:
+            MVH_HIP(mvh::launch_gemv_f16(reinterpret_cast<const uint16_t*>(W), xd, yd, rows, cols, batch, c->stream));
+            return MVH_OK;
     }
     return fail(MVH_E_TYPE, "unsupported %s tensor type %s: %s", what, type_name(w->type), w->name.c_str());
 }
@@ -386,6 +392,8 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
         }
         case MVH_TYPE_Q8_0:
         case MVH_TYPE_Q6_K:
+        case MVH_TYPE_F32:
+        case MVH_TYPE_F16:
             if (int rc = fp32_rows(c, w, static_cast<const float*>(xd), yd, 1, "matrix")) return rc;
             break;
         default:

@@ -386,6 +386,67 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
     }
 }
 
+// F32 weights (dot_f32_simd, src/gguf_kernels.cpp:228-234, as tensor_matvec
+// and tensor_matmul_batch call it): per (row, token) eight accumulators
+// t_j = fma(w[i+j], x[i+j], t_j) over i = 0, 8, .. (< cols & ~7), held by a
+// lane pair (t0..t3 and t4..t7); s = t0+t1+..+t7; then the scalar tail as the
+// compiled reference runs it -- 4 elements at a time with rounded products
+// and in-order adds, the last cols % 4 fused.
+constexpr int kF32T = 256;
+__global__ __launch_bounds__(kF32T) void gemv_f32_kernel(const float* __restrict__ W, const float* __restrict__ x,
+                                                         float* __restrict__ y, int N, int K) {
+    const int g = static_cast<int>((static_cast<size_t>(blockIdx.x) * kF32T + threadIdx.x) >> 1);
+    const int h = threadIdx.x & 1;
+    const bool live = g < N;
+    const int r = live ? g : N - 1;  // lanes past the last row mirror it (results dropped)
+    const float* wr = W + static_cast<size_t>(r) * K;
+    const float* xb = x + static_cast<size_t>(blockIdx.y) * K;
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
+    const int n8 = K & ~7;
+    for (int i = 4 * h; i < n8; i += 8) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = fmaf(wr[i + e], xb[i + e], t[e]);
+    }
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = __shfl_xor(t[e], 1);  // the partner's four accumulators
+    if (h == 0 && live) {
+        float s = t[0];
+        s = s + t[1];
+        s = s + t[2];
+        s = s + t[3];
+        s = s + o[0];
+        s = s + o[1];
+        s = s + o[2];
+        s = s + o[3];
+        int i = n8;
+        for (; i + 4 <= K; i += 4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s = s + wr[i + e] * xb[i + e];
+        for (; i < K; ++i) s = fmaf(wr[i], xb[i], s);
+        y[static_cast<size_t>(blockIdx.y) * N + r] = s;
+    }
+}
+
+// F16 weights (tensor_matvec / tensor_matmul_batch, src/gguf_kernels.cpp:250,
+// :257): s = sum of double(f16(w))*x in double, rounded to f32 once.  One wave
+// per (row, token); each lane keeps a double partial over elements l, l+64,
+// .. (the products are exact in double), the wave adds them as a tree -- the
+// reference adds in element order, so a result can differ from it only when
+// the exact sum lies within ~1e-13 (relative) of an f32 rounding boundary.
+constexpr int kF16T = 256;
+__global__ __launch_bounds__(kF16T) void gemv_f16_kernel(const uint16_t* __restrict__ W, const float* __restrict__ x,
+                                                         float* __restrict__ y, int N, int K) {
+    const int row = blockIdx.x * (kF16T / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= N) return;  // whole waves leave together
+    const uint16_t* wr = W + static_cast<size_t>(row) * K;
+    const float* xb = x + static_cast<size_t>(blockIdx.y) * K;
+    double acc = 0.0;
+    for (int c = lane; c < K; c += 64) acc = fma(static_cast<double>(h2f(wr[c])), static_cast<double>(xb[c]), acc);
+    const double tot = wave_sum(acc);
+    if (lane == 0) y[static_cast<size_t>(blockIdx.y) * N + row] = static_cast<float>(tot);
+}
+
 int pick_rows_per_wg(size_t rows, size_t nb, size_t pair_budget) {
     // enough rows per workgroup that every lane owns at least one 8-block
     // unit, capped by the LDS budget of the pair buffer
@@ -465,6 +526,22 @@ hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x,
         batch4_f32act_kernel<kQ4_0><<<grid, 256, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows), nb);
     else
         batch4_f32act_kernel<kQ8_0><<<grid, 256, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows), nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_f32(const float* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                           hipStream_t st) {
+    if (!rows || !batch) return hipSuccess;
+    const dim3 grid(static_cast<unsigned>((2 * rows + kF32T - 1) / kF32T), static_cast<unsigned>(batch));
+    gemv_f32_kernel<<<grid, kF32T, 0, st>>>(W, x, y, static_cast<int>(rows), static_cast<int>(cols));
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_f16(const uint16_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                           hipStream_t st) {
+    if (!rows || !batch) return hipSuccess;
+    const dim3 grid(static_cast<unsigned>((rows + kF16T / 64 - 1) / (kF16T / 64)), static_cast<unsigned>(batch));
+    gemv_f16_kernel<<<grid, kF16T, 0, st>>>(W, x, y, static_cast<int>(rows), static_cast<int>(cols));
     return hipGetLastError();
 }
 

@@ -26,6 +26,11 @@ hipError_t launch_gemv_q8_0(const uint8_t* W, const float* x, float* y, size_t r
                             hipStream_t st);
 hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                             hipStream_t st);
+// F32 / F16 weights with fp32 activations, y[b*rows + r] (dot_f32_simd / the double F16 sum)
+hipError_t launch_gemv_f32(const float* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                           hipStream_t st);
+hipError_t launch_gemv_f16(const uint16_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                           hipStream_t st);
 // Persistent Q4_0 x Q8 GEMV (cols % 256 == 0): x != nullptr quantizes the fp32
 // input inside the kernel; otherwise aq (16-byte aligned) / ad are the Q8 input.
 bool gemv_q4_0_persistent_ok(size_t cols);

@@ -198,7 +198,7 @@ void LlamaModel::upload(Tensor& t, const std::string& name) {
     t.type = g.type;
     t.cols = static_cast<std::size_t>(g.ne(0));
     t.rows = static_cast<std::size_t>(g.ne(1));
-    if (t.type != 2 && t.type != 8 && t.type != 14)
+    if (t.type != 0 && t.type != 1 && t.type != 2 && t.type != 8 && t.type != 14)
         throw std::runtime_error(std::string("unsupported device tensor type ") + type_name(t.type) + ": " + name);
     if (!g.nbytes) throw std::runtime_error("bad tensor size: " + name);
     check(hipMalloc(&t.d, g.nbytes), "hipMalloc tensor");
@@ -213,7 +213,7 @@ bool LlamaModel::upload_fused(Tensor& t, const std::vector<std::string>& names) 
     for (const auto& nm : names) {
         const auto& g = file_->tensor(nm);
         if (g.dims.size() < 2 || g.type != g0.type || g.ne(0) != g0.ne(0) || !g.nbytes) return false;
-        if (g.type != 2 && g.type != 8 && g.type != 14) return false;
+        if (g.type != 0 && g.type != 1 && g.type != 2 && g.type != 8 && g.type != 14) return false;
         bytes += g.nbytes;
         rows += static_cast<std::size_t>(g.ne(1));
     }
@@ -277,10 +277,22 @@ void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const f
                 if (e == hipSuccess) e = mvh::launch_gemv_q4_0(W, q8s_, q8sd_, y, w.rows, w.cols, stream_);
             }
             break;
-        case 8: e = mvh::launch_gemv_q8_0(W, x, y, w.rows, w.cols, 1, stream_); break;
-        default: e = mvh::launch_gemv_q6_k(W, x, y, w.rows, w.cols, 1, stream_); break;
+        default: e = fp32_gemv(w, x, y, 1); break;
     }
     check(e, w.sname.c_str());
+}
+
+// tensor_matvec / tensor_matmul_batch with fp32 activations for Q8_0, Q6_K,
+// F32 and F16 weights (src/gguf_kernels.cpp:247-250,:257): y[b*rows + r]
+hipError_t LlamaModel::fp32_gemv(const Tensor& w, const float* x, float* y, std::size_t B) {
+    const auto* W = static_cast<const uint8_t*>(w.d);
+    switch (w.type) {
+        case 8: return mvh::launch_gemv_q8_0(W, x, y, w.rows, w.cols, B, stream_);
+        case 14: return mvh::launch_gemv_q6_k(W, x, y, w.rows, w.cols, B, stream_);
+        case 0: return mvh::launch_gemv_f32(reinterpret_cast<const float*>(W), x, y, w.rows, w.cols, B, stream_);
+        case 1: return mvh::launch_gemv_f16(reinterpret_cast<const uint16_t*>(W), x, y, w.rows, w.cols, B, stream_);
+    }
+    return hipErrorInvalidValue;
 }
 
 bool LlamaModel::mfma_gemm(const Tensor& w) { return w.type == 2 && mvh::gemm_q4_0_mfma_ok(w.cols); }
@@ -293,8 +305,7 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
     hipError_t e = hipSuccess;
     if (B < 2 || (w.type != 2 && w.type != 8) || cols % 32) {  // tensor_matmul_batch: fp32 per token
         if (w.type == 2) e = mvh::launch_gemv_q4_0_f32act(W, x, y, rows, cols, B, stream_);
-        else if (w.type == 8) e = mvh::launch_gemv_q8_0(W, x, y, rows, cols, B, stream_);
-        else e = mvh::launch_gemv_q6_k(W, x, y, rows, cols, B, stream_);
+        else e = fp32_gemv(w, x, y, B);
     } else if (mode_ == PrefillMode::Q8) {
         if (w.type == 2) {
             if (!q8) {

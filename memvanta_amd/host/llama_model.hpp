@@ -83,6 +83,7 @@ private:
     void gemm(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y, std::size_t B,
               bool q8_op = false);
     static bool mfma_gemm(const Tensor& w);
+    hipError_t fp32_gemv(const Tensor& w, const float* x, float* y, std::size_t B);
     void decode_step(const int* d_token, bool logits, bool argmax);
     void store_kv(const QkvLayout& lay, void* const* pk, void* const* pv, const int* d_pos, std::size_t pos,
                   std::size_t B);

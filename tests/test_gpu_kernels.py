@@ -296,3 +296,37 @@ def test_attn_batch(ctx, oracle, n_head, n_kv, hd, pos, B, tname):
     with pytest.raises(capi.MvhError, match="context exhausted"):
         kv.attn_batch(0, q, 1024 - B + 1, B, n_head, n_kv, hd)
     kv.close()
+
+
+@pytest.mark.parametrize("k", [8, 9, 12, 13, 15, 301, 4096])
+def test_gemv_f32_bitexact(ctx, oracle, k):
+    """F32 weights: dot_f32_simd per (row, token) -- 8 fma lanes, t0+..+t7, the tail 4-wide unfused then fused --
+    bit-exact for every tail length, through matvec and matmul_batch."""
+    rng = np.random.default_rng(k)
+    n = 70
+    w = synth.quantize(synth.F32, rng.standard_normal((n, k), dtype=np.float32))
+    t = ctx.upload("blk.0.attn_q.weight", synth.F32, k, n, w)
+    x = rng.standard_normal(k, dtype=np.float32)
+    assert_bitexact(ctx.matvec(t, x), oracle.matvec(w, synth.F32, n, k, x), f"F32 matvec {k}")
+    xb = rng.standard_normal((3, k), dtype=np.float32)
+    assert_bitexact(ctx.matmul_batch(t, xb), oracle.matmul_batch(w, synth.F32, n, k, xb), f"F32 batch {k}")
+    t.free()
+
+
+@pytest.mark.parametrize("k,n", [(301, 33), (4096, 4096), (2048, 32000)])
+def test_gemv_f16(ctx, oracle, k, n):
+    """F16 weights: the double sum of the reference added as per-lane partials and a wave tree."""
+    rng = np.random.default_rng(k + n)
+    w = synth.quantize(synth.F16, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    t = ctx.upload("output.weight", synth.F16, k, n, w)
+    x = synth.activations(rng, 1, k)[0]
+    got = ctx.matvec(t, x)
+    want = oracle.matvec(w, synth.F16, n, k, x)
+    u = ulp_diff(got, want)
+    assert u.max() <= 2, u.max()
+    assert (u == 0).mean() >= 0.999, (u == 0).mean()
+    xb = synth.activations(rng, 2, k)
+    gb = ctx.matmul_batch(t, xb)
+    wb = oracle.matmul_batch(w, synth.F16, n, k, xb)
+    assert ulp_diff(gb, wb).max() <= 2
+    t.free()

@@ -212,3 +212,25 @@ def test_page_sizes_vs_oracle(tmp_path, oracle, cfg_name, page, tname):
         assert int(np.argmax(got)) == cur
     assert m.kv_bytes() == mo.kv_bytes()
     m.close()
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_f16_f32_weights_vs_oracle(tmp_path, oracle, mode):
+    """A model with F16 attention/FFN matrices, an F16 embedding and an F32 output head (tensor_matvec's and
+    tensor_matmul_batch's F16 / F32 branches; v06 falls back to tensor_matmul_batch for them)."""
+    cfg = synth.dataclasses.replace(synth.TINY, name="tiny-f16-f32", wtype=synth.F16, embd_type=synth.F16,
+                                    out_type=synth.F32, layers=2)
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=61)
+    prompt = synth.prompt_tokens(4, 41)
+    mo = oracle.model(path, ctx=256, force_q8=bool(mode))
+    m = capi.Model(path, ctx=256, act_mode=mode, max_batch=32)
+    close(m.prefill(prompt, 32), mo.prefill(prompt, 32), "f16/f32 prefill")
+    cur = 19
+    for _ in range(4):
+        want = mo.forward(cur)
+        got = m.forward(cur)
+        close(got, want, "f16/f32 decode")
+        cur = int(np.argmax(want))
+        assert int(np.argmax(got)) == cur
+    m.close()
