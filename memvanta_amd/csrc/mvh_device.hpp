@@ -169,6 +169,82 @@ __host__ __device__ constexpr size_t q8_op_offset(size_t t, size_t k, size_t K) 
 // bytes of that layout for B tokens (the last slab is whole)
 __host__ __device__ constexpr size_t q8_op_bytes(size_t B, size_t K) { return (B + 15) / 16 * 16 * K; }
 
+// One row of LlamaModel::rmsnorm (src/llama_model.cpp:237) by a workgroup of
+// kT threads, D <= 4 * kT * kV, D % 32 == 0 (D % 256 == 0 with q_op):
+// x += add (when add != null), ss = sum of x*x in double,
+// inv = 1/sqrtf(float(ss/D) + eps), n = (x*inv)*w, and (q != null) the Q8
+// activation of n (quantize_q8, bit-exact; row-major, or in the prefill
+// GEMM's operand order when q_op).  Thread t owns float4s t, t + kT, ...; the
+// double sum is added as a tree (per thread, per wave, then the waves in
+// order), not in the reference's element order: the two can differ only when
+// the exact sum of squares lies within ~1e-15 (relative) of an f32 rounding
+// boundary of ss/D.  red: kT/64 doubles of LDS.  Every thread must call it.
+template <int kT, int kV>
+__device__ __forceinline__ void rmsnorm_row(float* __restrict__ xr_, const float* __restrict__ add,
+                                            const float* __restrict__ w, float* __restrict__ n_row,
+                                            int8_t* __restrict__ q, float* __restrict__ qd, size_t row, int D,
+                                            float eps, bool q_op, double* red) {
+    const int t = threadIdx.x;
+    float4* xr = reinterpret_cast<float4*>(xr_);
+    const float4* ar = reinterpret_cast<const float4*>(add);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    const int D4 = D / 4;
+    // one memory round trip: x, the residual and the norm weights together
+    float4 v[kV], g[kV], a[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        const int i = t + k * kT;
+        v[k] = g[k] = a[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < D4) {
+            v[k] = xr[i];
+            g[k] = w4[i];
+            if (ar) a[k] = ar[i];
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        const int i = t + k * kT;
+        if (i >= D4) continue;
+        if (ar) {
+            v[k] = make_float4(v[k].x + a[k].x, v[k].y + a[k].y, v[k].z + a[k].z, v[k].w + a[k].w);
+            xr[i] = v[k];
+        }
+        ss = fma(static_cast<double>(v[k].x), static_cast<double>(v[k].x), ss);
+        ss = fma(static_cast<double>(v[k].y), static_cast<double>(v[k].y), ss);
+        ss = fma(static_cast<double>(v[k].z), static_cast<double>(v[k].z), ss);
+        ss = fma(static_cast<double>(v[k].w), static_cast<double>(v[k].w), ss);
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    ss = red[0];
+#pragma unroll
+    for (int k = 1; k < kT / 64; ++k) ss += red[k];
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(static_cast<float>(ss / static_cast<double>(D)) + eps));
+    float4* nr = reinterpret_cast<float4*>(n_row);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        const int i = t + k * kT;
+        if (k * kT >= D4) break;  // uniform; D4 % 8 == 0: 8-lane groups are whole blocks
+        const float4 o = make_float4((v[k].x * inv) * g[k].x, (v[k].y * inv) * g[k].y, (v[k].z * inv) * g[k].z,
+                                     (v[k].w * inv) * g[k].w);
+        if (i < D4) nr[i] = o;
+        if (q) {
+            float d;
+            int s;
+            const uint32_t packed = quantize_q8_x4(o, d, s);
+            if (i < D4) {
+                if (q_op)
+                    *reinterpret_cast<uint32_t*>(q + q8_op_offset(row, 4 * static_cast<size_t>(i), D)) = packed;
+                else
+                    reinterpret_cast<uint32_t*>(q + row * D)[i] = packed;
+                if ((i & 7) == 0) qd[row * (D / 32) + (i >> 3)] = d;
+            }
+        }
+    }
+}
+
 // ---- paged KV cache element types ------------------------------------------
 //
 // PagedKVCache's KVCacheType (F32, F16, Q8 in that order).  One page of K (or

@@ -43,13 +43,9 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t
     out[static_cast<size_t>(blockIdx.y) * cols + i] = dequant_elem(type, W, cols, static_cast<size_t>(tokens[blockIdx.y]), i);
 }
 
-// x += add (when add != null), then LlamaModel::rmsnorm (src/llama_model.cpp:237):
-// ss = sum of x*x in double, inv = 1/sqrtf(float(ss/D) + eps), n = (x*inv)*w;
-// optionally also the Q8 activation of n (quantize_q8, bit-exact; row-major,
-// or in the prefill GEMM's operand order when q_op).  One workgroup per row;
-// D % 32 == 0 (D % 256 == 0 with q_op).  The double sum is added as a tree, not in
-// the reference's element order; the two can differ only when the exact sum
-// of squares lies within ~1e-15 (relative) of an f32 rounding boundary of ss/D.
+// x += add (when add != null), then LlamaModel::rmsnorm (src/llama_model.cpp:237)
+// of each row and optionally its Q8 activation: rmsnorm_row, one workgroup
+// per row.
 constexpr int kNormT = 1024;
 constexpr int kNormV = 4;  // float4s per thread: D <= 16384, all held in registers
 __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ add,
@@ -58,65 +54,8 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
                                                          float eps, bool q_op) {
     __shared__ double red[kNormT / 64];
     const size_t row = blockIdx.x;
-    const int t = threadIdx.x;
-    float4* xr = reinterpret_cast<float4*>(x + row * D);
-    const float4* ar = add ? reinterpret_cast<const float4*>(add + row * D) : nullptr;
-    const float4* w4 = reinterpret_cast<const float4*>(w);
-    const int D4 = D / 4;
-    // one memory round trip: x, the residual and the norm weights together
-    float4 v[kNormV], g[kNormV], a[kNormV];
-#pragma unroll
-    for (int k = 0; k < kNormV; ++k) {
-        const int i = t + k * kNormT;
-        v[k] = g[k] = a[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i < D4) {
-            v[k] = xr[i];
-            g[k] = w4[i];
-            if (ar) a[k] = ar[i];
-        }
-    }
-    double ss = 0.0;
-#pragma unroll
-    for (int k = 0; k < kNormV; ++k) {
-        const int i = t + k * kNormT;
-        if (i >= D4) continue;
-        if (ar) {
-            v[k] = make_float4(v[k].x + a[k].x, v[k].y + a[k].y, v[k].z + a[k].z, v[k].w + a[k].w);
-            xr[i] = v[k];
-        }
-        ss = fma(static_cast<double>(v[k].x), static_cast<double>(v[k].x), ss);
-        ss = fma(static_cast<double>(v[k].y), static_cast<double>(v[k].y), ss);
-        ss = fma(static_cast<double>(v[k].z), static_cast<double>(v[k].z), ss);
-        ss = fma(static_cast<double>(v[k].w), static_cast<double>(v[k].w), ss);
-    }
-    ss = wave_sum(ss);
-    if ((t & 63) == 0) red[t >> 6] = ss;
-    __syncthreads();
-    ss = red[0];
-#pragma unroll
-    for (int k = 1; k < kNormT / 64; ++k) ss += red[k];
-    const float inv = __fdiv_rn(1.0f, sqrt_rn(static_cast<float>(ss / static_cast<double>(D)) + eps));
-    float4* nr = reinterpret_cast<float4*>(n + row * D);
-#pragma unroll
-    for (int k = 0; k < kNormV; ++k) {
-        const int i = t + k * kNormT;
-        if (k * kNormT >= D4) break;  // uniform; D4 % 8 == 0: 8-lane groups are whole blocks
-        const float4 o = make_float4((v[k].x * inv) * g[k].x, (v[k].y * inv) * g[k].y, (v[k].z * inv) * g[k].z,
-                                     (v[k].w * inv) * g[k].w);
-        if (i < D4) nr[i] = o;
-        if (q) {
-            float d;
-            int s;
-            const uint32_t packed = quantize_q8_x4(o, d, s);
-            if (i < D4) {
-                if (q_op)
-                    *reinterpret_cast<uint32_t*>(q + q8_op_offset(row, 4 * static_cast<size_t>(i), D)) = packed;
-                else
-                    reinterpret_cast<uint32_t*>(q + row * D)[i] = packed;
-                if ((i & 7) == 0) qd[row * (D / 32) + (i >> 3)] = d;
-            }
-        }
-    }
+    rmsnorm_row<kNormT, kNormV>(x + row * D, add ? add + row * D : nullptr, w, n + row * D, q, qd, row, D, eps, q_op,
+                                red);
 }
 
 // RoPE (LlamaModel::rope_ptr, src/llama_model.cpp:238; half-split pairs,
