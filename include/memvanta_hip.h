@@ -153,6 +153,38 @@ int mvh_attn_decode(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, cons
 int mvh_attn_batch(mvh_context* ctx, const mvh_kv_cache* kv, size_t layer, const float* q, size_t pos,
                    size_t n_tokens, size_t n_head, size_t n_head_kv, size_t head_dim, float* out, int ptr_kind);
 
+/* ---- kernel profiler: enable_kernel_profiling, reset_kernel_profile, kernel_profile_snapshot,
+ * kernel_profile_kind_name (include/memvanta/gguf_kernels.hpp:11-23, src/gguf_kernels.cpp:34-73,:219-222) ----
+ * While enabled, every mvh_matvec / mvh_matvec_q8 / mvh_matmul_batch / mvh_matmul_batch_v06 call, and
+ * every GEMV / GEMM of a model step, is timed on the device with a HIP event pair on its stream (host
+ * staging copies excluded; a profiled call waits for its end event) and added to the entry of its
+ * (layer, kind, tensor, batch), with layer and kind taken from the tensor name as tensor_layer and
+ * classify_tensor take them.  A model step runs without its HIP graph while profiling; a launch over
+ * fused weights is one entry named by its members joined with '+'.  Process-wide, like the reference. */
+#define MVH_PROF_Q_PROJ 0
+#define MVH_PROF_K_PROJ 1
+#define MVH_PROF_V_PROJ 2
+#define MVH_PROF_O_PROJ 3
+#define MVH_PROF_FFN_GATE 4
+#define MVH_PROF_FFN_UP 5
+#define MVH_PROF_FFN_DOWN 6
+#define MVH_PROF_OUTPUT 7
+#define MVH_PROF_OTHER 8
+typedef struct mvh_profile_entry {
+    int layer;         /* -1 when the name has no "blk.N." prefix */
+    int kind;          /* MVH_PROF_* */
+    char tensor[192];  /* NUL-terminated, truncated to 191 bytes */
+    size_t calls;
+    size_t batch;
+    double ms;
+} mvh_profile_entry;
+void mvh_profile_enable(int enabled);
+void mvh_profile_reset(void);
+/* *n_total = the number of entries; the first min(cap, *n_total) are copied to out (may be NULL when cap is 0) */
+int mvh_profile_snapshot(mvh_profile_entry* out, size_t cap, size_t* n_total);
+/* "q_proj", "k_proj", "v_proj", "o_proj", "ffn_gate", "ffn_up", "ffn_down", "output", "other" */
+const char* mvh_profile_kind_name(int kind);
+
 /* ---- whole model: LlamaModel on one device (weights, paged KV and activations in HBM) ---- */
 /* kv_type is LlamaModel's kv_type argument (MVH_KV_F16 is its default); act_mode selects the prefill numerics
  * (MVH_ACT_REF / MVH_ACT_Q8); max_batch bounds the prefill chunk */

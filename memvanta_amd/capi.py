@@ -82,7 +82,18 @@ _SIGS = {
     "mvh_model_position": (_int, [_vp, C.POINTER(_sz)]),
     "mvh_model_kv_bytes": (_int, [_vp, C.POINTER(_sz)]),
     "mvh_model_stream": (_int, [_vp, C.POINTER(_vp)]),
+    "mvh_profile_enable": (None, [_int]),
+    "mvh_profile_reset": (None, []),
+    "mvh_profile_snapshot": (_int, [_vp, _sz, C.POINTER(_sz)]),
+    "mvh_profile_kind_name": (C.c_char_p, [_int]),
 }
+
+
+class ProfileEntry(C.Structure):
+    """mvh_profile_entry (KernelProfileEntry of include/memvanta/gguf_kernels.hpp:12-19)."""
+
+    _fields_ = [("layer", C.c_int), ("kind", C.c_int), ("tensor", C.c_char * 192), ("calls", C.c_size_t),
+                ("batch", C.c_size_t), ("ms", C.c_double)]
 
 _lib = None
 
@@ -264,6 +275,37 @@ class Tensor:
         self.ctx._check(self.ctx.lib.mvh_tensor_info(self.h, C.byref(ty), C.byref(n0), C.byref(n1), C.byref(nb),
                                                      C.byref(dp)))
         return ty.value, n0.value, n1.value, nb.value, dp.value
+
+
+PROFILE_KINDS = ("q_proj", "k_proj", "v_proj", "o_proj", "ffn_gate", "ffn_up", "ffn_down", "output", "other")
+
+
+def profile_enable(on: bool = True) -> None:
+    """enable_kernel_profiling: time every tensor call and model GEMV/GEMM on the device."""
+    load_library().mvh_profile_enable(1 if on else 0)
+
+
+def profile_reset() -> None:
+    """reset_kernel_profile."""
+    load_library().mvh_profile_reset()
+
+
+def profile_snapshot() -> list[dict]:
+    """kernel_profile_snapshot: one dict per (layer, kind, tensor, batch) entry, in first-call order."""
+    lib = load_library()
+    n = _sz()
+    if lib.mvh_profile_snapshot(None, 0, C.byref(n)) != 0:
+        raise MvhError(1, lib.mvh_last_error().decode())
+    arr = (ProfileEntry * max(1, n.value))()
+    if lib.mvh_profile_snapshot(C.cast(arr, _vp), n.value, C.byref(n)) != 0:
+        raise MvhError(1, lib.mvh_last_error().decode())
+    return [{"layer": e.layer, "kind": e.kind, "kind_name": profile_kind_name(e.kind), "tensor": e.tensor.decode(),
+             "calls": e.calls, "batch": e.batch, "ms": e.ms} for e in arr[: n.value]]
+
+
+def profile_kind_name(kind: int) -> str:
+    """kernel_profile_kind_name."""
+    return load_library().mvh_profile_kind_name(kind).decode()
 
 
 def kv_parse_type(s: str) -> int:

@@ -5,12 +5,14 @@
 #include "memvanta_hip.h"
 #include "mvh_kernels.hpp"
 #include "llama_model.hpp"
+#include "profile.hpp"
 
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <optional>
 #include <string>
 #include <vector>
 
@@ -159,6 +161,39 @@ int act_buffers(mvh_context* c, size_t rows, size_t cols, ActView* v) {
         MVH_HIP(hipSetDevice((c)->device));                            \
     } while (0)
 
+namespace prof = memvanta::hip::prof;
+
+// Times the device work of one tensor call for the kernel profiler (nothing
+// when it is off): the start event goes in after the input staging, end()
+// records the stop event before the output copy and waits for it.
+class ProfSpan {
+public:
+    ProfSpan(mvh_context* c, const mvh_tensor* w, size_t batch) : name_(w->name), batch_(batch) {
+        if (!prof::enabled()) return;
+        rec_.emplace(c->stream);
+        if (rec_->start() != hipSuccess) rec_.reset();
+    }
+    int end() {
+        if (!rec_) return MVH_OK;
+        hipError_t e = rec_->stop(name_, batch_);
+        if (e == hipSuccess) e = rec_->flush();
+        rec_.reset();
+        return e == hipSuccess ? MVH_OK : fail(MVH_E_DEVICE, "profiler events: %s", hipGetErrorString(e));
+    }
+
+private:
+    std::string name_;
+    size_t batch_;
+    std::optional<prof::Recorder> rec_;
+};
+
+// A call with nothing to launch still counts, as profile_add runs after the
+// reference's empty loops.
+int prof_empty(const mvh_tensor* w, size_t batch) {
+    if (prof::enabled()) prof::add(w->name, batch, 0.0);
+    return MVH_OK;
+}
+
 // Per-(token, row) fp32-activation dots with tensor_matmul_batch's dispatch.
 int fp32_rows(mvh_context* c, const mvh_tensor* w, const float* xd, float* yd, size_t batch, const char* what) {
     const size_t cols = w->ne0, rows = w->ne1;
@@ -217,6 +252,31 @@ extern "C" {
 
 const char* mvh_last_error(void) { return g_err.c_str(); }
 int mvh_version(void) { return 1; }
+
+void mvh_profile_enable(int enabled) { prof::enable(enabled != 0); }
+void mvh_profile_reset(void) { prof::reset(); }
+
+int mvh_profile_snapshot(mvh_profile_entry* out, size_t cap, size_t* n_total) {
+    if (!n_total) return fail(MVH_E_INVALID, "null n_total");
+    if (cap && !out) return fail(MVH_E_INVALID, "null out with cap > 0");
+    const auto entries = prof::snapshot();
+    *n_total = entries.size();
+    for (size_t i = 0; i < entries.size() && i < cap; ++i) {
+        const auto& e = entries[i];
+        mvh_profile_entry& o = out[i];
+        o.layer = e.layer;
+        o.kind = e.kind;
+        const size_t n = std::min(e.tensor.size(), sizeof o.tensor - 1);
+        std::memcpy(o.tensor, e.tensor.data(), n);
+        o.tensor[n] = '\0';
+        o.calls = e.calls;
+        o.batch = e.batch;
+        o.ms = e.ms;
+    }
+    return MVH_OK;
+}
+
+const char* mvh_profile_kind_name(int kind) { return prof::kind_name(kind); }
 
 int mvh_device_count(int* count) {
     if (!count) return fail(MVH_E_INVALID, "null count");
@@ -367,7 +427,7 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
     if (!w) return fail(MVH_E_INVALID, "null tensor");
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
     const size_t cols = w->ne0, rows = w->ne1;
-    if (!rows) return MVH_OK;
+    if (!rows) return prof_empty(w, 1);
     const void* xd = nullptr;
     if (int rc = stage_in(c, c->xin, x, cols * 4, kind, &xd)) return rc;
     float* yd = y;
@@ -375,6 +435,7 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
         if (int rc = grow(c, c->yout, rows * 4)) return rc;
         yd = static_cast<float*>(c->yout.p);
     }
+    ProfSpan span(c, w, 1);
     const auto* W = static_cast<const uint8_t*>(w->d);
     switch (w->type) {
         case MVH_TYPE_Q4_0: {
@@ -399,6 +460,7 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
         default:
             return fail(MVH_E_TYPE, "unsupported matvec tensor type %s: %s", type_name(w->type), w->name.c_str());
     }
+    if (int rc = span.end()) return rc;
     return finish_out(c, y, yd, rows * 4, kind);
 }
 
@@ -411,7 +473,7 @@ int mvh_matvec_q8(mvh_context* c, const mvh_tensor* w, const int8_t* q, const fl
                     w->name.c_str());
     const size_t cols = w->ne0, rows = w->ne1, nb = cols / 32;
     if (cols % 32) return fail(MVH_E_SHAPE, "Q4_0 matrix row not block aligned: %s", w->name.c_str());
-    if (!rows) return MVH_OK;
+    if (!rows) return prof_empty(w, 1);
     const int8_t* qd = q;
     const float* dd = d;
     float* yd = y;
@@ -429,7 +491,9 @@ int mvh_matvec_q8(mvh_context* c, const mvh_tensor* w, const int8_t* q, const fl
     } else if (reinterpret_cast<uintptr_t>(q) & 15) {
         return fail(MVH_E_INVALID, "device q must be 16-byte aligned");
     }
+    ProfSpan span(c, w, 1);
     MVH_HIP(mvh::launch_gemv_q4_0(static_cast<const uint8_t*>(w->d), qd, dd, yd, rows, cols, c->stream));
+    if (int rc = span.end()) return rc;
     return finish_out(c, y, yd, rows * 4, kind);
 }
 
@@ -437,7 +501,7 @@ int mvh_matmul_batch(mvh_context* c, const mvh_tensor* w, const float* x, float*
     CHECK_CTX(c);
     if (!w) return fail(MVH_E_INVALID, "null tensor");
     const size_t cols = w->ne0, rows = w->ne1;
-    if (!batch || !rows) return MVH_OK;
+    if (!batch || !rows) return prof_empty(w, batch);
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
     const void* xd = nullptr;
     if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
@@ -446,7 +510,9 @@ int mvh_matmul_batch(mvh_context* c, const mvh_tensor* w, const float* x, float*
         if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
         yd = static_cast<float*>(c->yout.p);
     }
+    ProfSpan span(c, w, batch);
     if (int rc = fp32_rows(c, w, static_cast<const float*>(xd), yd, batch, "batch matrix")) return rc;
+    if (int rc = span.end()) return rc;
     return finish_out(c, y, yd, batch * rows * 4, kind);
 }
 
@@ -459,7 +525,7 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
     // fallback conditions of src/gguf_kernels.cpp:263
     if (batch < 2 || (w->type != MVH_TYPE_Q4_0 && w->type != MVH_TYPE_Q8_0) || cols % 32)
         return mvh_matmul_batch(c, w, x, y, batch, kind);
-    if (!rows) return MVH_OK;
+    if (!rows) return prof_empty(w, batch);
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
     const void* xv = nullptr;
     if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xv)) return rc;
@@ -469,6 +535,7 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
         if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
         yd = static_cast<float*>(c->yout.p);
     }
+    ProfSpan span(c, w, batch);
     const auto* W = static_cast<const uint8_t*>(w->d);
     const size_t nb = cols / 32;
     if (act_mode == MVH_ACT_Q8) {
@@ -499,6 +566,7 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
                 return rc;
         }
     }
+    if (int rc = span.end()) return rc;
     return finish_out(c, y, yd, batch * rows * 4, kind);
 }
 

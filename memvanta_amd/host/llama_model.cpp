@@ -171,6 +171,7 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     d_hist_ = static_cast<int*>(dalloc(4 * (c_.n_ctx + 1)));
     d_pos_ = static_cast<int*>(dalloc(16));
     d_toks_ = static_cast<int*>(dalloc(B * 4));
+    rec_ = std::make_unique<prof::Recorder>(stream_);
     ffo_ = static_cast<float*>(dalloc(B * D * 4));
     q8s_ = static_cast<int8_t*>(dalloc(mvh::q8_op_bytes(B, W)));
     q8sd_ = static_cast<float*>(dalloc(B * (W / 32) * 4));
@@ -194,7 +195,7 @@ LlamaModel::~LlamaModel() {
 void LlamaModel::upload(Tensor& t, const std::string& name) {
     const auto& g = file_->tensor(name);
     if (g.dims.size() < 2) throw std::runtime_error("matvec requires rank-2 tensor: " + name);
-    t.sname = name;
+    t.sname = t.pname = name;
     t.type = g.type;
     t.cols = static_cast<std::size_t>(g.ne(0));
     t.rows = static_cast<std::size_t>(g.ne(1));
@@ -217,7 +218,8 @@ bool LlamaModel::upload_fused(Tensor& t, const std::vector<std::string>& names) 
         bytes += g.nbytes;
         rows += static_cast<std::size_t>(g.ne(1));
     }
-    t.sname = names[0];
+    t.sname = t.pname = names[0];
+    for (std::size_t i = 1; i < names.size(); ++i) t.pname += "+" + names[i];
     t.type = g0.type;
     t.cols = static_cast<std::size_t>(g0.ne(0));
     t.rows = rows;
@@ -263,9 +265,22 @@ float* LlamaModel::upload_vector(const std::string& name) {
 }
 
 // tensor_matvec numerics (src/gguf_kernels.cpp:244-253)
+void LlamaModel::prof_start() {
+    if (profiling_) check(rec_->start(), "profiler event");
+}
+
+void LlamaModel::prof_stop(const Tensor& w, std::size_t batch) {
+    if (profiling_) check(rec_->stop(w.pname, batch), "profiler event");
+}
+
+void LlamaModel::prof_flush() {
+    if (profiling_) check(rec_->flush(), "profiler events");
+}
+
 void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const float* q8d, float* y) {
     const auto* W = static_cast<const uint8_t*>(w.d);
     hipError_t e;
+    prof_start();
     switch (w.type) {
         case 2:
             if (q8) {
@@ -280,6 +295,7 @@ void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const f
         default: e = fp32_gemv(w, x, y, 1); break;
     }
     check(e, w.sname.c_str());
+    prof_stop(w, 1);
 }
 
 // tensor_matvec / tensor_matmul_batch with fp32 activations for Q8_0, Q6_K,
@@ -303,6 +319,7 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
     const auto* W = static_cast<const uint8_t*>(w.d);
     const std::size_t rows = w.rows, cols = w.cols, nb = cols / 32;
     hipError_t e = hipSuccess;
+    prof_start();
     if (B < 2 || (w.type != 2 && w.type != 8) || cols % 32) {  // tensor_matmul_batch: fp32 per token
         if (w.type == 2) e = mvh::launch_gemv_q4_0_f32act(W, x, y, rows, cols, B, stream_);
         else e = fp32_gemv(w, x, y, B);
@@ -336,6 +353,7 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
         }
     }
     check(e, w.sname.c_str());
+    prof_stop(w, B);
 }
 
 // One decode step (LlamaModel::forward, src/llama_model.cpp:253-259) for the
@@ -518,7 +536,9 @@ const std::vector<float>& LlamaModel::forward(int token, bool compute_logits) {
     pin_[1] = static_cast<int>(pos_);
     check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, stream_), "token upload");
     check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, stream_), "pos upload");
+    profiling_ = prof::enabled();
     decode_step(d_tok_, compute_logits, false);
+    prof_flush();
     ++pos_;
     kv_hi_ = std::max(kv_hi_, pos_);
     if (compute_logits) return logits();
@@ -541,7 +561,9 @@ const std::vector<float>& LlamaModel::prefill(const std::vector<int>& tokens, st
         const bool last = compute_logits_last && i + B == tokens.size();
         std::memcpy(pin_, tokens.data() + i, B * 4);
         check(hipMemcpyAsync(d_toks_, pin_, B * 4, hipMemcpyHostToDevice, stream_), "token upload");
+        profiling_ = prof::enabled();
         batch_step(d_toks_, B, last);
+        prof_flush();
         check(hipStreamSynchronize(stream_), "sync");  // pin_ is reused by the next chunk
         pos_ += B;
         kv_hi_ = std::max(kv_hi_, pos_);
@@ -560,7 +582,14 @@ std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
     pin_[1] = static_cast<int>(pos_);
     check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, stream_), "token upload");
     check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, stream_), "pos upload");
-    if (!graph_) {
+    profiling_ = prof::enabled();
+    if (profiling_) {
+        // the same steps without the graph, so every GEMV can be timed
+        for (std::size_t i = 0; i < n; ++i) {
+            decode_step(d_tok_, true, true);
+            prof_flush();
+        }
+    } else if (!graph_) {
         // the step reads token and position from device memory and its argmax
         // writes the next token and advances the position: one graph serves
         // every step
@@ -571,7 +600,8 @@ std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
         check(hipGraphInstantiate(&graph_, g, nullptr, nullptr, 0), "graph instantiate");
         (void)hipGraphDestroy(g);
     }
-    for (std::size_t i = 0; i < n; ++i) check(hipGraphLaunch(graph_, stream_), "graph launch");
+    if (!profiling_)
+        for (std::size_t i = 0; i < n; ++i) check(hipGraphLaunch(graph_, stream_), "graph launch");
     check(hipMemcpyAsync(pin_, d_hist_ + pos_, n * 4, hipMemcpyDeviceToHost, stream_), "token copy");
     check(hipStreamSynchronize(stream_), "sync");
     std::memcpy(out.data(), pin_, n * 4);

@@ -14,6 +14,8 @@
 #include <string>
 #include <vector>
 
+#include "profile.hpp"
+
 namespace memvanta {
 namespace hip {
 
@@ -55,6 +57,7 @@ public:
 private:
     struct Tensor {
         std::string sname;
+        std::string pname;  // profiler name: sname, or the fused members joined with '+'
         std::uint32_t type{};
         std::size_t rows{}, cols{};
         void* d{};
@@ -116,6 +119,12 @@ private:
     std::vector<float> logits_;
     hipGraphExec_t graph_{};
     bool fused_attn_{};  // decode attention in one launch (launch_attn_decode_fused; F16 pages)
+    // kernel profiler: GEMV / GEMM launches of a step are timed while it is on
+    std::unique_ptr<prof::Recorder> rec_;
+    bool profiling_{};
+    void prof_start();
+    void prof_stop(const Tensor& w, std::size_t batch);
+    void prof_flush();
 };
 
 }  // namespace hip

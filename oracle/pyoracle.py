@@ -305,6 +305,11 @@ class Ref:
         L.mvr_model_position.argtypes = [C.c_void_p]
         L.mvr_model_kv_bytes.restype = _sz
         L.mvr_model_kv_bytes.argtypes = [C.c_void_p]
+        L.mvr_profile_enable.argtypes = [C.c_int]
+        L.mvr_profile_kind_name.restype = C.c_char_p
+        L.mvr_profile_kind_name.argtypes = [C.c_int]
+        L.mvr_profile_snapshot.restype = _sz
+        L.mvr_profile_snapshot.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _sz, _sz]
 
     def _check(self, rc):
         if rc != 0:
@@ -328,6 +333,27 @@ class Ref:
 
     def kv(self, kv_dim, page_tokens=128, kv_type=KV_F16):
         return RefKV(self, kv_dim, page_tokens, kv_type)
+
+    def profile_enable(self, on=True):
+        self.lib.mvr_profile_enable(int(on))
+
+    def profile_reset(self):
+        self.lib.mvr_profile_reset()
+
+    def profile_kind_name(self, kind):
+        return self.lib.mvr_profile_kind_name(kind).decode()
+
+    def profile_snapshot(self):
+        """[(layer, kind, tensor, calls, batch)] in the reference's snapshot order."""
+        L = self.lib
+        n = L.mvr_profile_snapshot(None, None, None, None, None, 0, 0)
+        layer, kind = np.zeros(max(1, n), np.int32), np.zeros(max(1, n), np.int32)
+        calls, batch = np.zeros(max(1, n), np.uint64), np.zeros(max(1, n), np.uint64)
+        names = C.create_string_buffer(256 * max(1, n))
+        L.mvr_profile_snapshot(layer.ctypes.data, kind.ctypes.data, calls.ctypes.data, batch.ctypes.data,
+                               C.addressof(names), len(names), n)
+        tensors = names.raw.split(b"\0")[:n]
+        return [(int(layer[i]), int(kind[i]), tensors[i].decode(), int(calls[i]), int(batch[i])) for i in range(n)]
 
     def model(self, path, ctx=0, page=128, threads=8, force_q8=False, kv_type=KV_F16):
         return RefModel(self, path, ctx, page, threads, force_q8, kv_type)

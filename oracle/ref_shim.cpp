@@ -149,4 +149,28 @@ int mvr_model_prefill(void* h, const int* tokens, size_t n, size_t batch, float*
 size_t mvr_model_position(void* h) { return static_cast<RefModel*>(h)->m->position(); }
 size_t mvr_model_kv_bytes(void* h) { return static_cast<RefModel*>(h)->m->kv_bytes_allocated(); }
 
+// kernel profiler (include/memvanta/gguf_kernels.hpp:11-23)
+void mvr_profile_enable(int on) { memvanta::enable_kernel_profiling(on != 0); }
+void mvr_profile_reset(void) { memvanta::reset_kernel_profile(); }
+const char* mvr_profile_kind_name(int kind) {
+    return memvanta::kernel_profile_kind_name(static_cast<memvanta::KernelProfileKind>(kind));
+}
+// entries in snapshot order: the first `cap` go to the arrays, their tensor
+// names (NUL-separated) to names[names_cap]; returns the entry count
+size_t mvr_profile_snapshot(int* layer, int* kind, size_t* calls, size_t* batch, char* names, size_t names_cap,
+                            size_t cap) {
+    const auto es = memvanta::kernel_profile_snapshot();
+    size_t off = 0;
+    for (size_t i = 0; i < es.size() && i < cap; ++i) {
+        layer[i] = es[i].layer;
+        kind[i] = static_cast<int>(es[i].kind);
+        calls[i] = es[i].calls;
+        batch[i] = es[i].batch;
+        const size_t n = es[i].tensor.size() + 1;
+        if (off + n <= names_cap) std::memcpy(names + off, es[i].tensor.c_str(), n);
+        off += n;
+    }
+    return es.size();
+}
+
 }  // extern "C"

@@ -42,6 +42,18 @@ def test_kv_type_names_match_reference():
         capi.kv_parse_type("bf16")
 
 
+def test_profile_kind_names_match_reference():
+    """kernel_profile_kind_name (src/gguf_kernels.cpp:222) for every kind and
+    out-of-range values, against the compiled reference's strings; the
+    registry's enable / reset / snapshot run without a device."""
+    g = golden("profile.npz")
+    assert [capi.profile_kind_name(int(k)) for k in g["kind_codes"]] == g["kind_names"].tolist()
+    assert capi.PROFILE_KINDS == tuple(g["kind_names"][1:10].tolist())
+    capi.profile_enable(False)
+    capi.profile_reset()
+    assert capi.profile_snapshot() == []
+
+
 def test_header_compiles_as_c_and_links(tmp_path):
     """A plain C program (what a cgo / C++ shim sees) compiles against the
     header alone and links against the library; no call touches a device."""
@@ -61,6 +73,10 @@ int main(void) {
     int t = -1;
     if (mvh_kv_parse_type("q8_0", &t) != MVH_OK || t != MVH_KV_Q8) return 4;
     if (mvh_kv_type_name(MVH_KV_F32)[1] != '3') return 5;
+    size_t n = 7;
+    mvh_profile_reset();
+    if (mvh_profile_snapshot(NULL, 0, &n) != MVH_OK || n != 0) return 6;
+    if (mvh_profile_kind_name(MVH_PROF_FFN_DOWN)[4] != 'd') return 7;
     puts("ok");
     return 0;
 }
