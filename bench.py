@@ -23,7 +23,9 @@ launches of one 7B decode layer (q|k|v fused [4096->12288], o [4096->4096],
 gate|up fused [4096->22016], down [11008->4096]; the isolated-GEMV shapes
 [4096->4096], [4096->11008], [11008->4096], [4096->32000] are timed beside),
 with HIP events on the backend's stream over graph replays that rotate weight
-copies so every launch streams its weights from HBM.  `cpu_baseline` runs the
+copies (at least 640 MB between two uses of one copy, more than the 256 MB
+Infinity Cache) so every launch streams its weights from HBM; the prefill GEMM
+timing rotates copies the same way.  `cpu_baseline` runs the
 compiled reference's LlamaModel (oracle/_ref; else the C restatement) on the
 same GGUF on the host cores, over a bounded decode sample.
 """
@@ -75,7 +77,13 @@ def kv_read_bytes(cfg, first_pos: int, n: int) -> int:
     return cfg.layers * 2 * kv * 2 * positions
 
 
-def time_gemv_kernels(launches: int, copies: int):
+def rotation_copies(nbytes: int, rotate_mb: float) -> int:
+    """Weight copies whose rotation streams at least rotate_mb MB between two
+    uses of one copy (more than the 256 MB Infinity Cache: cold-HBM timing)."""
+    return max(2, -(-int(rotate_mb * 1e6) // nbytes))
+
+
+def time_gemv_kernels(launches: int, rotate_mb: float):
     """Average duration of the Q4_0 x Q8 GEMV kernel per shape (HIP events, graph replays)."""
     import numpy as np
     import torch
@@ -89,10 +97,9 @@ def time_gemv_kernels(launches: int, copies: int):
     rng = np.random.default_rng(99)
     out = {}
     for k, n in ISOLATED_GEMVS:
-        ts = []
-        for _ in range(copies):
-            w = synth.quantize_torch(synth.Q4_0, torch.randn((n, k), generator=gen, device="cuda") * 0.02)
-            ts.append(ctx.upload("blk.0.attn_q.weight", synth.Q4_0, k, n, w.cpu().numpy()))
+        w = synth.quantize_torch(synth.Q4_0, torch.randn((n, k), generator=gen, device="cuda") * 0.02).cpu().numpy()
+        copies = rotation_copies(w.nbytes, rotate_mb)
+        ts = [ctx.upload("blk.0.attn_q.weight", synth.Q4_0, k, n, w) for _ in range(copies)]
         x = torch.from_numpy(synth.activations(rng, 1, k)[0]).cuda()
         q = torch.empty(k, dtype=torch.int8, device="cuda")
         d = torch.empty(k // 32, dtype=torch.float32, device="cuda")
@@ -126,7 +133,7 @@ PREFILL_M = [32, 128, 512]
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
 
 
-def time_prefill_gemm(reps: int):
+def time_prefill_gemm(reps: int, rotate_mb: float):
     """Q4_0 x Q8 prefill GEMM (int8 MFMA) at the GEMM config shapes: us, TOP/s, GB/s."""
     import numpy as np
     import torch
@@ -140,18 +147,18 @@ def time_prefill_gemm(reps: int):
     rng = np.random.default_rng(5)
     out = []
     for k, n in PREFILL_GEMMS:
-        w = synth.quantize_torch(synth.Q4_0, torch.randn((n, k), generator=gen, device="cuda") * 0.02)
-        t = ctx.upload("blk.0.ffn_up.weight", synth.Q4_0, k, n, w.cpu().numpy())
+        w = synth.quantize_torch(synth.Q4_0, torch.randn((n, k), generator=gen, device="cuda") * 0.02).cpu().numpy()
+        ts = [ctx.upload("blk.0.ffn_up.weight", synth.Q4_0, k, n, w) for _ in range(rotation_copies(w.nbytes, rotate_mb))]
         for m in PREFILL_M:
             x = torch.from_numpy(synth.activations(rng, m, k)).cuda()
             y = torch.empty((m, n), dtype=torch.float32, device="cuda")
-            ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8, y=y)  # warm-up (includes the activation quantizer)
+            ctx.matmul_batch_v06(ts[0], x, capi.MVH_ACT_Q8, y=y)  # warm-up (includes the activation quantizer)
             ctx.synchronize()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             with torch.cuda.stream(stream):
                 a.record(stream)
-                for _ in range(reps):
-                    ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8, y=y)
+                for r in range(reps):
+                    ctx.matmul_batch_v06(ts[r % len(ts)], x, capi.MVH_ACT_Q8, y=y)
                 b.record(stream)
             b.synchronize()
             us = a.elapsed_time(b) * 1e3 / reps
@@ -160,7 +167,8 @@ def time_prefill_gemm(reps: int):
             out.append({"K": k, "N": n, "M": m, "us": round(us, 2), "TOP/s": round(ops / us / 1e6, 2),
                         "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
                         "GB/s": round(byts / us / 1e3, 1)})
-        t.free()
+        for t in ts:
+            t.free()
     ctx.close()
     return out
 
@@ -235,7 +243,8 @@ def main():
     ap.add_argument("--pp-reps", type=int, default=3)
     ap.add_argument("--api-tokens", type=int, default=32, help="decode tokens timed through forward()")
     ap.add_argument("--kernel-launches", type=int, default=96)
-    ap.add_argument("--copies", type=int, default=8, help="weight copies rotated in the GEMV kernel timing")
+    ap.add_argument("--rotate-mb", type=float, default=640.0,
+                    help="weight bytes streamed between two uses of one copy in the kernel timings (> 256 MB MALL)")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kv-types", action="store_true", help="skip the F32 / Q8 KV cache runs")
@@ -257,9 +266,9 @@ def main():
     from memvanta_amd import capi, synth
 
     if args.kernels_only:
-        gemm = time_prefill_gemm(10)
+        gemm = time_prefill_gemm(10, args.rotate_mb)
         print(json.dumps({"prefill_gemm": gemm}))
-        us = time_gemv_kernels(args.kernel_launches, args.copies)
+        us = time_gemv_kernels(args.kernel_launches, args.rotate_mb)
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -335,7 +344,7 @@ def main():
         m.close()
 
         # dominant kernel alone: Q4_0 x Q8 GEMV
-        us = time_gemv_kernels(args.kernel_launches, args.copies)
+        us = time_gemv_kernels(args.kernel_launches, args.rotate_mb)
         mix_bytes = sum(gemv_bytes(k, n) * c for k, n, c in DECODE_GEMVS)
         mix_us = sum(us[(k, n)] * c for k, n, c in DECODE_GEMVS)
         launches = sum(c for _, _, c in DECODE_GEMVS)
@@ -344,7 +353,7 @@ def main():
                       "GB/s": round(gemv_bytes(k, n) / us[(k, n)] / 1e3, 1)} for k, n in ISOLATED_GEMVS]
 
         # batched prefill GEMM (int8 MFMA) at the GEMM config shapes
-        gemm = time_prefill_gemm(10)
+        gemm = time_prefill_gemm(10, args.rotate_mb)
 
         traffic = None
         pmc = os.path.join(ROOT, "profiles", "gemv_q4_0_7b_decode_traffic.json")
