@@ -324,6 +324,168 @@ __global__ __launch_bounds__(256) void batch4_f32act_kernel(const uint8_t* __res
     y[static_cast<size_t>(blockIdx.y) * N + r] = s;
 }
 
+// The same numerics for K % 256 == 0 with the work spread over lanes: lane
+// (row, j) owns accumulator j of its row for kBT tokens, i.e. elements j,
+// j+8, j+16, j+24 of every block in that order (the reference's 8-wide
+// vector lane j); eight lanes per row, eight rows per wave, 32 rows per
+// workgroup.  Each dequantized float(q)*d feeds the kBT tokens' fmas.  The
+// weights come in 8-block units (16-byte loads; the eight lanes of a row load
+// the same bytes); the activations of the kBT tokens come through LDS one
+// 8-block chunk at a time, stored as [token][block][j][m] so lane j reads its
+// four elements x[32b + j + 8m] with one 16-byte read.  The final
+// t0 + t1 + ... + t7 runs in order through LDS.
+constexpr int kBT = 8;         // tokens per workgroup
+constexpr int kBRows = 32;     // rows per workgroup
+constexpr int kBChunk = 256;   // activation elements per LDS chunk (one 8-block unit)
+
+template <uint32_t TYPE>
+struct Unit;
+template <>
+struct Unit<kQ4_0> {
+    static constexpr int kU4 = 9;  // 16-byte loads per 8 blocks (144 bytes)
+    // block jb of the unit: f16 scale bits and the 16 quant bytes as 4 dwords
+    static __device__ __forceinline__ void block(const uint32_t (&w)[4 * kU4], int jb, uint32_t& dbits,
+                                                 uint32_t (&qs)[4]) {
+        const int o = 18 * jb;
+        if ((jb & 1) == 0) {
+            dbits = w[o / 4] & 0xffffu;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qs[k] = align16(w[o / 4 + k + 1], w[o / 4 + k]);
+        } else {
+            dbits = w[o / 4] >> 16;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qs[k] = w[(o + 2) / 4 + k];
+        }
+    }
+    // elements j, j+8, j+16, j+24: low nibbles of bytes j, 8+j, high nibbles of the same
+    static __device__ __forceinline__ void lane_values(const uint32_t (&qs)[4], int j, int (&v)[4]) {
+        const uint32_t sh = 8u * static_cast<uint32_t>(j & 3);
+        const uint32_t b0 = ((j & 4) ? qs[1] : qs[0]) >> sh, b1 = ((j & 4) ? qs[3] : qs[2]) >> sh;
+        v[0] = static_cast<int>(b0 & 15u) - 8;
+        v[1] = static_cast<int>(b1 & 15u) - 8;
+        v[2] = static_cast<int>((b0 >> 4) & 15u) - 8;
+        v[3] = static_cast<int>((b1 >> 4) & 15u) - 8;
+    }
+};
+template <>
+struct Unit<kQ8_0> {
+    static constexpr int kU4 = 17;  // 272 bytes
+    static __device__ __forceinline__ void block(const uint32_t (&w)[4 * kU4], int jb, uint32_t& dbits,
+                                                 uint32_t (&qs)[8]) {
+        const int o = 34 * jb;
+        if ((jb & 1) == 0) {
+            dbits = w[o / 4] & 0xffffu;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) qs[k] = align16(w[o / 4 + k + 1], w[o / 4 + k]);
+        } else {
+            dbits = w[o / 4] >> 16;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) qs[k] = w[(o + 2) / 4 + k];
+        }
+    }
+    // elements j + 8m: byte j + 8m of the 32 int8 values
+    static __device__ __forceinline__ void lane_values(const uint32_t (&qs)[8], int j, int (&v)[4]) {
+        const uint32_t sh = 8u * static_cast<uint32_t>(j & 3);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            v[m] = static_cast<int>(static_cast<int8_t>(((j & 4) ? qs[2 * m + 1] : qs[2 * m]) >> sh));
+    }
+};
+
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* __restrict__ W,
+                                                                 const float* __restrict__ x, float* __restrict__ y,
+                                                                 int N, int nb) {
+    using U = Unit<TYPE>;
+    constexpr int kQdw = Blk<TYPE>::kQdw;
+    __shared__ __align__(16) float s_x[2][kBT * kBChunk];  // [token][block][j][m], double-buffered
+    const int t = threadIdx.x, j = t & 7;
+    const int rl = t >> 3;  // row within the workgroup
+    const int r = blockIdx.x * kBRows + rl;
+    const int tok0 = blockIdx.y * kBT;
+    const int K = nb * 32, units = nb / 8;
+    const size_t row_bytes = static_cast<size_t>(nb) * Blk<TYPE>::kBytes;
+    const uint4* wrow = reinterpret_cast<const uint4*>(W + static_cast<size_t>(min(r, N - 1)) * row_bytes);
+
+    // chunk c of the kBT activation rows into s_x[buf]: 4 float4 per thread (kBT * 256 floats)
+    auto stage = [&](int c, int buf) {
+#pragma unroll
+        for (int k = 0; k < kBT * kBChunk / 4 / 256; ++k) {
+            const int f = t + 256 * k;           // float4 index within the chunk: token f / 64, element 4 (f % 64)
+            const int tk = f >> 6, e = 4 * (f & 63);
+            const float4 v = *reinterpret_cast<const float4*>(x + static_cast<size_t>(tok0 + tk) * K + c * kBChunk + e);
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // element e+i: block (e+i)/32, lane (e+i)%8, m = ((e+i)%32)/8
+                const int ei = e + i;
+                s_x[buf][((tk * 8 + (ei >> 5)) * 8 + (ei & 7)) * 4 + ((ei & 31) >> 3)] = vv[i];
+            }
+        }
+    };
+
+    float acc[kBT];
+#pragma unroll
+    for (int k = 0; k < kBT; ++k) acc[k] = 0.0f;
+    uint32_t w[4 * U::kU4];
+    auto load = [&](int u) {
+#pragma unroll
+        for (int k = 0; k < U::kU4; ++k) {
+            const uint4 v = wrow[u * U::kU4 + k];
+            w[4 * k] = v.x;
+            w[4 * k + 1] = v.y;
+            w[4 * k + 2] = v.z;
+            w[4 * k + 3] = v.w;
+        }
+    };
+    load(0);
+    stage(0, 0);
+    __syncthreads();
+    for (int u = 0; u < units; ++u) {
+        const int buf = u & 1;
+        uint32_t cur[4 * U::kU4];
+#pragma unroll
+        for (int k = 0; k < 4 * U::kU4; ++k) cur[k] = w[k];
+        if (u + 1 < units) {
+            load(u + 1);
+            stage(u + 1, buf ^ 1);
+        }
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+            uint32_t dbits, qs[kQdw];
+            U::block(cur, jb, dbits, qs);
+            const float d = h2f(dbits);
+            int v[4];
+            U::lane_values(qs, j, v);
+            float q[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) q[m] = static_cast<float>(v[m]) * d;
+#pragma unroll
+            for (int k = 0; k < kBT; ++k) {
+                const float4 xv = *reinterpret_cast<const float4*>(&s_x[buf][((k * 8 + jb) * 8 + j) * 4]);
+                acc[k] = fmaf(q[0], xv.x, acc[k]);
+                acc[k] = fmaf(q[1], xv.y, acc[k]);
+                acc[k] = fmaf(q[2], xv.z, acc[k]);
+                acc[k] = fmaf(q[3], xv.w, acc[k]);
+            }
+        }
+        __syncthreads();  // s_x[buf] is restaged at u + 2; s_x[buf ^ 1] is complete
+    }
+    // t0 + t1 + ... + t7 per (row, token), in order, through LDS
+    float* s_red = &s_x[0][0];  // [row][token][j]
+#pragma unroll
+    for (int k = 0; k < kBT; ++k) s_red[(rl * kBT + k) * 8 + j] = acc[k];
+    __syncthreads();
+    {
+        const int tk = t / kBRows, row = t % kBRows;  // one output per thread, rows fastest
+        const float* p = s_red + (row * kBT + tk) * 8;
+        float sum = p[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) sum = sum + p[i];
+        const int orow = blockIdx.x * kBRows + row;
+        if (orow < N) y[static_cast<size_t>(tok0 + tk) * N + orow] = sum;
+    }
+}
+
 // Q6_K with fp32 activations (dot_q6_k_fp32, src/gguf_kernels.cpp:138-146):
 // w = (d*sc[i/16])*q in f32, exact products summed in double.  One wave per
 // row; each lane owns 64 elements of one half super-block and keeps its own
@@ -521,6 +683,21 @@ hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x,
                                 size_t batch, hipStream_t st) {
     if (!rows || !batch) return hipSuccess;
     const int nb = static_cast<int>(cols / 32);
+    static_assert(kBT * kBRows == 256, "one output per thread in the final sum");
+    if (cols % 256 == 0 && batch >= kBT) {
+        // whole groups of kBT tokens on the lane-spread kernel, the rest per token below
+        const size_t groups = batch / kBT;
+        const dim3 grid(static_cast<unsigned>((rows + kBRows - 1) / kBRows), static_cast<unsigned>(groups));
+        if (type == kQ4_0)
+            batch_f32act_lanes_kernel<kQ4_0><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
+        else
+            batch_f32act_lanes_kernel<kQ8_0><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
+        const size_t done = groups * kBT;
+        if (done == batch) return hipGetLastError();
+        x += done * cols;
+        y += done * rows;
+        batch -= done;
+    }
     const dim3 grid(static_cast<unsigned>((rows + 255) / 256), static_cast<unsigned>(batch));
     if (type == kQ4_0)
         batch4_f32act_kernel<kQ4_0><<<grid, 256, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows), nb);

@@ -147,6 +147,25 @@ def test_matmul_v06_ref_mode_bitexact(ctx, oracle, ty, name, batch):
 
 
 @pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0])
+@pytest.mark.parametrize("name,batch,k,n", [("blk.0.attn_q.weight", 32, 4096, 300), ("blk.0.attn_q.weight", 12, 4096, 33),
+                                            ("blk.0.ffn_up.weight", 24, 11008, 40), ("blk.0.attn_q.weight", 27, 768, 64),
+                                            ("blk.0.ffn_up.weight", 8, 2048, 1)])
+def test_matmul_v06_ref_mode_lanes_bitexact(ctx, oracle, ty, name, batch, k, n):
+    """Default prefill numerics (batch4 / batch8 accumulators) at 7B-scale K:
+    whole 8-token groups run on the lane-spread kernel, the rest of the blocked
+    tokens per token, the unblocked tail with dot_*_fp32; row counts off the
+    32-row tile."""
+    rng = np.random.default_rng(batch * 13 + k + n + ty)
+    w = _w(rng, ty, n, k)
+    t = ctx.upload(name, ty, k, n, w)
+    x = synth.activations(rng, batch, k)
+    got = ctx.matmul_batch_v06(t, x, capi.MVH_ACT_REF)
+    want = oracle.matmul_batch_v06(w, ty, n, k, x, is_ffn="ffn" in name, force_q8=False)
+    assert_bitexact(got, want, f"v06 ref {name} B={batch} K={k} N={n}")
+    t.free()
+
+
+@pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0])
 @pytest.mark.parametrize("batch,k,n", [(2, 1024, 96), (32, 4096, 512), (7, 288, 768)])
 def test_matmul_v06_q8_mode_bitexact(ctx, oracle, ty, batch, k, n):
     rng = np.random.default_rng(batch + k + n + ty)
