@@ -407,14 +407,25 @@ __global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* 
     const size_t row_bytes = static_cast<size_t>(nb) * Blk<TYPE>::kBytes;
     const uint4* wrow = reinterpret_cast<const uint4*>(W + static_cast<size_t>(min(r, N - 1)) * row_bytes);
 
-    // chunk c of the kBT activation rows into s_x[buf]: 4 float4 per thread (kBT * 256 floats)
-    auto stage = [&](int c, int buf) {
+    // chunk c of the kBT activation rows: 2 float4 per thread (kBT * 256
+    // floats) into registers, written to LDS after the current unit's fmas,
+    // so the wait for them neither delays those fmas nor covers the weight
+    // loads issued after them
+    constexpr int kSt = kBT * kBChunk / 4 / 256;
+    auto stage_load = [&](int c, float4 (&v)[kSt]) {
 #pragma unroll
-        for (int k = 0; k < kBT * kBChunk / 4 / 256; ++k) {
-            const int f = t + 256 * k;           // float4 index within the chunk: token f / 64, element 4 (f % 64)
+        for (int k = 0; k < kSt; ++k) {
+            const int f = t + 256 * k;  // float4 index within the chunk: token f / 64, element 4 (f % 64)
+            v[k] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(tok0 + (f >> 6)) * K + c * kBChunk +
+                                                    4 * (f & 63));
+        }
+    };
+    auto stage_store = [&](const float4 (&v)[kSt], int buf) {
+#pragma unroll
+        for (int k = 0; k < kSt; ++k) {
+            const int f = t + 256 * k;
             const int tk = f >> 6, e = 4 * (f & 63);
-            const float4 v = *reinterpret_cast<const float4*>(x + static_cast<size_t>(tok0 + tk) * K + c * kBChunk + e);
-            const float vv[4] = {v.x, v.y, v.z, v.w};
+            const float vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {  // element e+i: block (e+i)/32, lane (e+i)%8, m = ((e+i)%32)/8
                 const int ei = e + i;
@@ -437,18 +448,22 @@ __global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* 
             w[4 * k + 3] = v.w;
         }
     };
+    float4 xs[kSt];
+    stage_load(0, xs);
     load(0);
-    stage(0, 0);
+    stage_store(xs, 0);
     __syncthreads();
     for (int u = 0; u < units; ++u) {
         const int buf = u & 1;
+        // the next unit's loads and staging run unconditionally (the last
+        // unit reloads itself and restages into the idle buffer), so no
+        // branch lets the compiler move the staging stores ahead of the fmas
+        const int nu = min(u + 1, units - 1);
         uint32_t cur[4 * U::kU4];
 #pragma unroll
         for (int k = 0; k < 4 * U::kU4; ++k) cur[k] = w[k];
-        if (u + 1 < units) {
-            load(u + 1);
-            stage(u + 1, buf ^ 1);
-        }
+        stage_load(nu, xs);
+        load(nu);
 #pragma unroll
         for (int jb = 0; jb < 8; ++jb) {
             uint32_t dbits, qs[kQdw];
@@ -467,8 +482,14 @@ __global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* 
                 acc[k] = fmaf(q[2], xv.z, acc[k]);
                 acc[k] = fmaf(q[3], xv.w, acc[k]);
             }
+            // each block's LDS reads stay with its fmas, and the staging
+            // stores stay after the last block: hoisted, the reads take a
+            // register set per block and the stores wait for the activation
+            // loads in the middle of the fmas
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();  // s_x[buf] is restaged at u + 2; s_x[buf ^ 1] is complete
+        stage_store(xs, buf ^ 1);  // s_x[buf ^ 1] was last read by unit u - 1
+        __syncthreads();  // s_x[buf ^ 1] is complete; s_x[buf] is free for unit u + 2
     }
     // t0 + t1 + ... + t7 per (row, token), in order, through LDS
     float* s_red = &s_x[0][0];  // [row][token][j]
