@@ -15,6 +15,8 @@ real_model_bench (benchmarks/real_model_bench.cpp:20-27):
 * pp512: reset, prefill 512 prompt ids in chunks of 32 with last-token
   logits (tensor_matmul_batch_v06 numerics, MEMVANTA_FORCE_Q8_ACT=1 mode).
 * prompt ids follow the reference bench's fixed_tokens: (i*1543+17) % vocab.
+* pp512 is also timed with the default prefill numerics (no
+  MEMVANTA_FORCE_Q8_ACT): config.pp512_default_numerics_tok_s.
 * the same tg and pp512 are timed beside it with F32 and Q8 KV pages
   (LlamaModel's kv_type) and reported under config.other_kv_cache_types.
 
@@ -208,6 +210,27 @@ def time_kv_types(path: str, steps: int, warmup: int):
     return out
 
 
+def time_pp_default_numerics(path: str) -> float:
+    """pp512 with tensor_matmul_batch_v06's default numerics (no
+    MEMVANTA_FORCE_Q8_ACT: fp32 activations, batch8 / batch4 accumulators),
+    after one untimed run."""
+    import torch
+
+    from memvanta_amd import capi
+
+    m = capi.Model(path, ctx=CTX, page_tokens=PAGE, act_mode=capi.MVH_ACT_REF, max_batch=BATCH)
+    prompt = fixed_tokens(PROMPT_TOKENS, m.vocab)
+    m.prefill(prompt, BATCH, logits=True)
+    m.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.prefill(prompt, BATCH, logits=True)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    m.close()
+    return PROMPT_TOKENS / dt
+
+
 def cpu_baseline(path: str, budget_s: float):
     """The reference CPU LlamaModel on the same GGUF: greedy decode after a short seed."""
     from oracle import pyoracle
@@ -343,6 +366,8 @@ def main():
         api_tg = args.api_tokens / (time.perf_counter() - t0)
         m.close()
 
+        pp_default = time_pp_default_numerics(path)
+
         # dominant kernel alone: Q4_0 x Q8 GEMV
         us = time_gemv_kernels(args.kernel_launches, args.rotate_mb)
         mix_bytes = sum(gemv_bytes(k, n) * c for k, n, c in DECODE_GEMVS)
@@ -398,6 +423,9 @@ def main():
             "pp512_tok_s": round(float(np.mean(pp)), 1),
             "pp512_tok_s_reps": [round(v, 1) for v in pp],
             "pp_numerics": "tensor_matmul_batch_v06, MEMVANTA_FORCE_Q8_ACT=1",
+            "pp512_default_numerics_tok_s": round(pp_default, 1),
+            "pp_default_numerics": "tensor_matmul_batch_v06 without MEMVANTA_FORCE_Q8_ACT (fp32 activations, "
+                                   "batch8 / batch4 accumulators)",
             "greedy_ids_head": [int(v) for v in ids[:8]],
             "model_write_s": round(t_write, 1),
             "model_load_s": round(t_load, 2),
