@@ -324,6 +324,92 @@ __global__ __launch_bounds__(256) void batch4_f32act_kernel(const uint8_t* __res
     y[static_cast<size_t>(blockIdx.y) * N + r] = s;
 }
 
+// dot_q8_0_fp32 / dot_q4_0_fp32 per row (tensor_matvec's Q8_0 branch and the
+// fp32-activation Q4_0 dot, src/gguf_kernels.cpp:93-120) for one token, K %
+// 256 == 0, K / 256 <= 64, in the structure of the persistent Q4_0 x Q8 GEMV:
+// lane (r, u) of a wave owns unit u (8 blocks) of row r of the wave's tile of
+// TR = 64 / (K/256) rows, turns its 8 blocks into (d_b, s_b) pairs (s_b the
+// block's exact 8-lane sum, f32act_block_sum) against the activation staged
+// in LDS, and the row's chain sum = fma(d_b, s_b, sum) then walks the lanes
+// in unit order (DPP shift by one lane per stage).  Persistent waves stride
+// over the tiles; every weight load is unconditional (clamped rows).
+template <uint32_t TYPE>
+__device__ __forceinline__ void gemv_f32act_persistent(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                       float* __restrict__ y, int N, int nb, int ntiles) {
+    constexpr int kU4 = 8 * Blk<TYPE>::kBytes / 16;  // 16-byte loads per unit
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* s_x = reinterpret_cast<float*>(smem);
+    const int upr = nb >> 3;
+    const size_t row_bytes = static_cast<size_t>(nb) * Blk<TYPE>::kBytes;
+    const int t = threadIdx.x, lane = t & 63;
+    const int TR = 64 / upr;
+    const int r = lane / upr, u = lane - r * upr;
+    const bool worker = r < TR;
+    const int uu = worker ? u : 0;
+    const int gw = blockIdx.x * 4 + (t >> 6), GW = gridDim.x * 4;
+    auto load = [&](uint32_t (&w)[4 * kU4], int tl) {
+        const int grow = min(tl * TR + (worker ? r : 0), N - 1);
+        const uint4* src = reinterpret_cast<const uint4*>(W + static_cast<size_t>(grow) * row_bytes +
+                                                          static_cast<size_t>(uu) * 8 * Blk<TYPE>::kBytes);
+#pragma unroll
+        for (int k = 0; k < kU4; ++k) {
+            const uint4 v = src[k];
+            w[4 * k] = v.x;
+            w[4 * k + 1] = v.y;
+            w[4 * k + 2] = v.z;
+            w[4 * k + 3] = v.w;
+        }
+    };
+    // the wave's first two tiles go out before the activation staging
+    uint32_t wa[4 * kU4], wb[4 * kU4];
+    int tile = gw;
+    load(wa, min(tile, ntiles - 1));
+    load(wb, min(tile + GW, ntiles - 1));
+    for (int c = t; c < nb * 8; c += 256)
+        *reinterpret_cast<float4*>(s_x + (c >> 6) * kXPitchF + (c & 63) * 4) = reinterpret_cast<const float4*>(x)[c];
+    __syncthreads();
+    const float* xg = s_x + uu * kXPitchF;
+    auto tile_step = [&](int tl, const uint32_t (&w)[4 * kU4]) {
+        const int grow = tl * TR + r;
+        float2 pr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t dbits, qs[Blk<TYPE>::kQdw];
+            unit_block<TYPE>(w, j, dbits, qs);
+            pr[j] = make_float2(h2f(dbits), f32act_block_sum<TYPE>(qs, xg + j * 32));
+        }
+        // lane u's value is final from stage u on; after upr stages the last
+        // lane of each row holds the in-order chain
+        float sum = 0.0f;
+        for (int st = 0; st < upr; ++st) {
+            const float in = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x138, 0xf, 0xf, false));
+            float acc = u == 0 ? 0.0f : in;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = fmaf(pr[j].x, pr[j].y, acc);
+            sum = acc;
+        }
+        if (worker && grow < N && u == upr - 1) y[grow] = sum;
+    };
+    while (tile < ntiles) {
+        tile_step(tile, wa);
+        if (tile + 2 * GW < ntiles) load(wa, tile + 2 * GW);
+        tile += GW;
+        if (tile >= ntiles) break;
+        tile_step(tile, wb);
+        if (tile + 2 * GW < ntiles) load(wb, tile + 2 * GW);
+        tile += GW;
+    }
+}
+
+__global__ __launch_bounds__(256) void gemv_f32act_persistent_q4_0(
+    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
+    gemv_f32act_persistent<kQ4_0>(W, x, y, N, nb, ntiles);
+}
+__global__ __launch_bounds__(256) void gemv_f32act_persistent_q8_0(
+    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
+    gemv_f32act_persistent<kQ8_0>(W, x, y, N, nb, ntiles);
+}
+
 // The same numerics for K % 256 == 0 with the work spread over lanes: lane
 // (row, j) owns accumulator j of its row for kBT tokens, i.e. elements j,
 // j+8, j+16, j+24 of every block in that order (the reference's 8-wide
@@ -690,14 +776,43 @@ static hipError_t launch_f32act(const uint8_t* W, const float* x, float* y, size
     return hipGetLastError();
 }
 
+// One token, K % 256 == 0, K <= 16384: the persistent kernel; otherwise the
+// two-phase kernel per token.
+template <uint32_t TYPE>
+static hipError_t launch_f32act_any(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,
+                                    size_t batch, hipStream_t st) {
+    if (!rows || !batch) return hipSuccess;
+    if (batch == 1 && cols % 256 == 0 && cols / 256 <= 64) {
+        static const int cus = [] {
+            int dev = 0;
+            hipDeviceProp_t prop;
+            if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+                prop.multiProcessorCount > 0)
+                return prop.multiProcessorCount;
+            return 256;
+        }();
+        const int nb = static_cast<int>(cols / 32);
+        const int tr = 64 / (nb / 8);
+        const int ntiles = static_cast<int>((rows + tr - 1) / tr);
+        const int waves = std::min(ntiles, cus * 16);
+        const size_t lds = static_cast<size_t>(nb / 8) * kXPitchF * 4;
+        if constexpr (TYPE == kQ4_0)
+            gemv_f32act_persistent_q4_0<<<(waves + 3) / 4, 256, lds, st>>>(W, x, y, static_cast<int>(rows), nb, ntiles);
+        else
+            gemv_f32act_persistent_q8_0<<<(waves + 3) / 4, 256, lds, st>>>(W, x, y, static_cast<int>(rows), nb, ntiles);
+        return hipGetLastError();
+    }
+    return launch_f32act<TYPE>(W, x, y, rows, cols, batch, st);
+}
+
 hipError_t launch_gemv_q8_0(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                             hipStream_t st) {
-    return launch_f32act<kQ8_0>(W, x, y, rows, cols, batch, st);
+    return launch_f32act_any<kQ8_0>(W, x, y, rows, cols, batch, st);
 }
 
 hipError_t launch_gemv_q4_0_f32act(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                                    hipStream_t st) {
-    return launch_f32act<kQ4_0>(W, x, y, rows, cols, batch, st);
+    return launch_f32act_any<kQ4_0>(W, x, y, rows, cols, batch, st);
 }
 
 hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,
