@@ -210,6 +210,29 @@ def time_kv_types(path: str, steps: int, warmup: int):
     return out
 
 
+def measure_hbm(nbytes: int = 1 << 30, reps: int = 5):
+    """Device read and copy bandwidth in GB/s measured here (torch's sum over a
+    1 GiB tensor, and a 1 GiB device-to-device copy), as a measured ceiling
+    beside the 8 TB/s specification."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    out = {}
+    for name, fn, moved in (("read", lambda: src.sum(), nbytes), ("copy", lambda: dst.copy_(src), 2 * nbytes)):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        b.synchronize()
+        out[name] = moved * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+    return out
+
+
 def time_pp_default_numerics(path: str) -> float:
     """pp512 with tensor_matmul_batch_v06's default numerics (no
     MEMVANTA_FORCE_Q8_ACT: fp32 activations, batch8 / batch4 accumulators),
@@ -391,6 +414,7 @@ def main():
 
         # batched prefill GEMM (int8 MFMA) at the GEMM config shapes
         gemm = time_prefill_gemm(10, args.rotate_mb)
+        hbm = measure_hbm()
 
         traffic = None
         pmc = os.path.join(ROOT, "profiles", "gemv_q4_0_7b_decode_traffic.json")
@@ -456,7 +480,9 @@ def main():
                      "avg_launch_us": round(mix_us / launches, 3),
                      "algorithmic_bytes_per_launch": mix_bytes // launches,
                      "launch_mix": "7B decode layer: 4096->12288 (q|k|v), 4096->4096 (o), 4096->22016 "
-                                       "(gate|up), 11008->4096 (down)"},
+                                       "(gate|up), 11008->4096 (down)",
+                     "measured_read_gbs": round(hbm["read"], 1), "measured_copy_gbs": round(hbm["copy"], 1),
+                     "frac_of_measured_read": round(achieved / hbm["read"], 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
