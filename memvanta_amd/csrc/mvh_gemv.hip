@@ -601,7 +601,7 @@ __global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* 
 // can differ from it only when the exact sum lies within ~1e-13 (relative) of
 // an f32 rounding boundary.
 constexpr int kQ6Threads = 256;
-constexpr int kQ6RowsPerWg = 8;
+constexpr int kQ6RowsPerWg = 4;  // one row per wave
 
 __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __restrict__ W,
                                                                const float* __restrict__ x, float* __restrict__ y,
