@@ -95,11 +95,11 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
                           size_t D, float eps, hipStream_t st, bool q_op = false);
 // q/k/v of token b at q + b*q_pitch, k + b*kv_pitch, v + b*kv_pitch; the
-// rotated k and v go to the F16 pages when pt_k != null (k is rotated in place
-// either way)
+// rotated k and v go to the pages when pt_k != null, F16 or F32 (kv_type;
+// Q8 pages are written by launch_kv_write), k is rotated in place either way
 hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, size_t kv_pitch, const float* cos_t,
                           const float* sin_t, const int* d_pos, size_t pos0, size_t B, size_t n_head, size_t n_kv,
-                          size_t hd, uint16_t* const* pt_k, uint16_t* const* pt_v, size_t page_tokens,
+                          size_t hd, int kv_type, void* const* pt_k, void* const* pt_v, size_t page_tokens,
                           hipStream_t st);
 // B rows: g/u row b at g + b*pitch, u + b*pitch; ff/q rows of F
 hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff, int8_t* q, float* qd, size_t B,

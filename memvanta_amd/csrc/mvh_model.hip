@@ -60,16 +60,18 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
 
 // RoPE (LlamaModel::rope_ptr, src/llama_model.cpp:238; half-split pairs,
 // GCC's contraction fma(x0,c,-(x1*s)) / fma(x0,s,x1*c)) on q and k of B
-// tokens at positions pos..pos+B-1, in place, then (pt_k != null) the F16
-// PagedKVCache::write of k and v through the reference's fp32_to_fp16 (:22).
+// tokens at positions pos..pos+B-1, in place, then (pt_k != null)
+// PagedKVCache::write of k and v: F16 pages through the reference's
+// fp32_to_fp16 (:22), F32 pages as they are (kv_f32).
 // One thread per (token, head, i).
 __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int q_pitch, float* __restrict__ k,
                                                       const float* __restrict__ v, int kv_pitch,
                                                       const float* __restrict__ cos_t,
                                                       const float* __restrict__ sin_t, const int* __restrict__ d_pos,
                                                       int pos0, int B, int n_head, int n_kv, int hd,
-                                                      uint16_t* const* __restrict__ pt_k,
-                                                      uint16_t* const* __restrict__ pt_v, int page_tokens) {
+                                                      void* const* __restrict__ pt_k,
+                                                      void* const* __restrict__ pt_v, int page_tokens,
+                                                      int kv_f32) {
     const int half = hd / 2, heads = n_head + n_kv;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= B * heads * half) return;
@@ -86,13 +88,22 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int
     if (h >= n_head && pt_k) {
         const int kh = h - n_head;
         const size_t off = static_cast<size_t>(pos % page_tokens) * KV + kh * hd;
-        uint16_t* kp = pt_k[pos / page_tokens] + off;
-        uint16_t* vp = pt_v[pos / page_tokens] + off;
         const float* vv = v + static_cast<size_t>(b) * kv_pitch + kh * hd;
-        kp[i] = f2h_ref(r0);
-        kp[i + half] = f2h_ref(r1);
-        vp[i] = f2h_ref(vv[i]);
-        vp[i + half] = f2h_ref(vv[i + half]);
+        if (kv_f32) {  // F32 pages: the row as it is (PagedKVCache::write's memcpy)
+            float* kp = static_cast<float*>(pt_k[pos / page_tokens]) + off;
+            float* vp = static_cast<float*>(pt_v[pos / page_tokens]) + off;
+            kp[i] = r0;
+            kp[i + half] = r1;
+            vp[i] = vv[i];
+            vp[i + half] = vv[i + half];
+        } else {
+            uint16_t* kp = static_cast<uint16_t*>(pt_k[pos / page_tokens]) + off;
+            uint16_t* vp = static_cast<uint16_t*>(pt_v[pos / page_tokens]) + off;
+            kp[i] = f2h_ref(r0);
+            kp[i + half] = f2h_ref(r1);
+            vp[i] = f2h_ref(vv[i]);
+            vp[i + half] = f2h_ref(vv[i + half]);
+        }
     }
 }
 
@@ -211,14 +222,14 @@ hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, 
 
 hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, size_t kv_pitch, const float* cos_t,
                           const float* sin_t, const int* d_pos, size_t pos0, size_t B, size_t n_head, size_t n_kv,
-                          size_t hd, uint16_t* const* pt_k, uint16_t* const* pt_v, size_t page_tokens,
+                          size_t hd, int kv_type, void* const* pt_k, void* const* pt_v, size_t page_tokens,
                           hipStream_t st) {
     const size_t n = B * (n_head + n_kv) * (hd / 2);
     if (!n) return hipSuccess;
     rope_kv_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(
         q, static_cast<int>(q_pitch), k, v, static_cast<int>(kv_pitch), cos_t, sin_t, d_pos, static_cast<int>(pos0),
         static_cast<int>(B), static_cast<int>(n_head), static_cast<int>(n_kv), static_cast<int>(hd), pt_k, pt_v,
-        static_cast<int>(page_tokens));
+        static_cast<int>(page_tokens), kv_type == kKvF32 ? 1 : 0);
     return hipGetLastError();
 }
 

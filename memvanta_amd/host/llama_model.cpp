@@ -510,13 +510,14 @@ std::size_t LlamaModel::kv_bytes_allocated() const {
 // a write kernel of its own for F32 / Q8 (Q8 needs the whole row's max).
 void LlamaModel::store_kv(const QkvLayout& lay, void* const* pk, void* const* pv, const int* d_pos, std::size_t pos,
                           std::size_t B) {
-    const bool f16 = kv_type_ == mvh::kKvF16;
+    // F16 and F32 rows are written by the RoPE launch; a Q8 row's scale
+    // spans every head, so Q8 pages get their own write launch
+    const bool fused = kv_type_ != mvh::kKvQ8;
     check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, d_pos, pos, B,
-                              c_.n_head, c_.n_head_kv, c_.head_dim(),
-                              f16 ? reinterpret_cast<uint16_t* const*>(pk) : nullptr,
-                              f16 ? reinterpret_cast<uint16_t* const*>(pv) : nullptr, page_tokens_, stream_),
+                              c_.n_head, c_.n_head_kv, c_.head_dim(), kv_type_, fused ? pk : nullptr,
+                              fused ? pv : nullptr, page_tokens_, stream_),
           "rope/kv");
-    if (!f16)
+    if (!fused)
         check(mvh::launch_kv_write(kv_type_, pk, pv, lay.k, lay.v, lay.kv_pitch, d_pos, pos, B, c_.kv_dim(),
                                    page_tokens_, stream_),
               "kv write");
