@@ -24,6 +24,8 @@
 //      applies the reference's fma to its 4 outputs.
 #include "mvh_kernels.hpp"
 
+#include <cstdlib>
+
 namespace mvh {
 namespace {
 
@@ -202,7 +204,15 @@ hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const fl
     // 16-token tiles while the grid is small (more waves, shorter chains);
     // 32-token tiles share each weight operand when there are waves to spare.
     // The deeper ring pays where few waves each stream a long K.
-    if (batch <= 32 || gx * g32 <= 1024) {
+    // From 512 row tiles (N >= 8192: the fused q|k|v and gate|up) 32-token
+    // tiles pay even at M <= 32: the raw-weight staging and unpack is shared
+    // by two token groups (pp512 +1.5%); below it the 16-token tiles keep
+    // the wave count up.  Tuning override: MVH_GEMM_TG2_ROWTILES.
+    static const size_t tg2_min = [] {
+        const char* e = getenv("MVH_GEMM_TG2_ROWTILES");
+        return e ? static_cast<size_t>(atoll(e)) : static_cast<size_t>(512);
+    }();
+    if ((batch <= 32 && gx < tg2_min) || gx * g32 <= 1024) {
         if (gx * g16 <= 1024)
             gemm_q4_0_q8_mfma_kernel<1, 4><<<dim3(gx, static_cast<unsigned>(g16)), 64, 0, st>>>(W, aq, ad, y, N, nb, Bn);
         else
