@@ -50,6 +50,7 @@ CTX, BATCH, PAGE, SEED_TOKENS, PROMPT_TOKENS, FIRST_TOKEN = 768, 32, 128, 128, 5
 DECODE_GEMVS = [(4096, 12288, 1), (4096, 4096, 1), (4096, 22016, 1), (11008, 4096, 1)]
 ISOLATED_GEMVS = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000), (4096, 12288), (4096, 22016)]
 REF_TG128_TOKS = 1.52  # published reference tg128, OpenLLaMA-7B-v2 Q4_0, 4-thread Xeon 8573C, ctx 768
+REF_PP512_TOKS = 3.15  # published reference pp512, same run
 
 
 def fixed_tokens(n: int, vocab: int):
@@ -468,6 +469,8 @@ def main():
             "timing": "tg: device-resident greedy loop (one HIP graph per token), wall clock between "
                       "device synchronizations; pp: host-driven chunks, wall clock",
             "vs_baseline_basis": "published reference tg128 1.52 tok/s (real OpenLLaMA-7B-v2 Q4_0, CPU, 4 threads)",
+            "pp512_vs_published": round(float(np.mean(pp)) / REF_PP512_TOKS, 1),
+            "pp512_vs_published_basis": "published reference pp512 3.15 tok/s (same run)",
             "gemv_kernel_per_shape": per_shape,
             "prefill_gemm_int8_mfma": gemm,
             "prefill_gemm_note": "tensor_matmul_batch_v06 FORCE_Q8 numerics incl. the activation quantizer; "
