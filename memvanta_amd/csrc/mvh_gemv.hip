@@ -282,6 +282,71 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_f32act_kernel(const uint8_t
     fold_pairs(s_pair, pitch, rows, nb, y + static_cast<size_t>(blockIdx.y) * N + r0);
 }
 
+// The same two phases for TT tokens per workgroup (nb % 8 == 0): each 8-block
+// unit is loaded once and turned into pairs for every token of the group (the
+// per-token kernel reloads the weights for every token); the folds then run
+// one thread per (row, token).  Token t of the group is t0 + t, t < B - t0.
+template <uint32_t TYPE, int TT>
+__global__ __launch_bounds__(kGemvThreads) void gemv_f32act_tokens_kernel(const uint8_t* __restrict__ W,
+                                                                           const float* __restrict__ x,
+                                                                           float* __restrict__ y, int N, int nb,
+                                                                           int rows_per_wg, int B) {
+    constexpr int BB = Blk<TYPE>::kBytes;
+    constexpr int UNIT16 = 8 * BB / 16;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int ngrp = nb >> 3;
+    const int xstride = ngrp * kXPitchF;  // floats per token
+    float* s_x = reinterpret_cast<float*>(smem);
+    float2* s_pair = reinterpret_cast<float2*>(smem + static_cast<size_t>(TT) * xstride * 4);
+    const int pitch = nb + 1;
+    const int K = nb * 32;
+    const int t0 = blockIdx.y * TT, nt = min(TT, B - t0);
+    for (int tk = 0; tk < nt; ++tk) {
+        const float* xt = x + static_cast<size_t>(t0 + tk) * K;
+        for (int c = threadIdx.x; c < K / 4; c += blockDim.x)
+            *reinterpret_cast<float4*>(s_x + tk * xstride + (c >> 6) * kXPitchF + (c & 63) * 4) =
+                reinterpret_cast<const float4*>(xt)[c];
+    }
+    __syncthreads();
+
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int rows = min(rows_per_wg, N - r0);
+    const int upr = nb / 8;
+    const int nunits = rows * upr;
+    const uint8_t* tile = W + static_cast<size_t>(r0) * nb * BB;
+    for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
+        const int row = u / upr;
+        const int b0 = (u - row * upr) * 8;
+        uint32_t w[4 * UNIT16];
+        const uint4* src = reinterpret_cast<const uint4*>(tile + static_cast<size_t>(u) * 8 * BB);
+#pragma unroll
+        for (int k = 0; k < UNIT16; ++k) {
+            const uint4 v = ld_stream16(src + k);
+            w[4 * k] = v.x;
+            w[4 * k + 1] = v.y;
+            w[4 * k + 2] = v.z;
+            w[4 * k + 3] = v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t dbits, qs[Blk<TYPE>::kQdw];
+            unit_block<TYPE>(w, j, dbits, qs);
+            const float d = h2f(dbits);
+            for (int tk = 0; tk < nt; ++tk)
+                s_pair[(tk * rows_per_wg + row) * pitch + b0 + j] =
+                    make_float2(d, f32act_block_sum<TYPE>(qs, s_x + tk * xstride + (b0 >> 3) * kXPitchF + j * 32));
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows * nt; i += blockDim.x) {
+        const int tk = i / rows, r = i - tk * rows;
+        const float2* pr = s_pair + (tk * rows_per_wg + r) * pitch;
+        float sum = 0.0f;
+        for (int b = 0; b < nb; ++b) sum = fmaf(pr[b].x, pr[b].y, sum);
+        y[static_cast<size_t>(t0 + tk) * N + r0 + r] = sum;
+    }
+}
+
 // Default batched prefill numerics (q4_row_batch4_fp32 / q8_row_batch4_fp32,
 // src/gguf_kernels.cpp:191-209; batch8 = two batch4, :211-216): per
 // (row, token) eight lane accumulators run over ALL blocks without reset,
@@ -766,6 +831,24 @@ static hipError_t launch_f32act(const uint8_t* W, const float* x, float* y, size
     const int nb = static_cast<int>(cols / 32);
     const int ngrp = (nb + 7) / 8;
     const size_t fixed = static_cast<size_t>(ngrp) * kXPitchF * 4;
+    if (batch >= 2 && nb % 8 == 0) {
+        // token groups of 4 (or 2) when their activations leave room for a few rows of pairs
+        const int tt = 4 * fixed <= 36 * 1024 ? 4 : 2 * fixed <= 36 * 1024 ? 2 : 1;
+        if (tt > 1) {
+            const size_t budget = 60 * 1024 - tt * fixed;
+            const int rpw = std::max(1, std::min(pick_rows_per_wg(rows, nb, budget / tt),
+                                                 static_cast<int>(budget / (tt * (nb + 1) * sizeof(float2)))));
+            const size_t lds = tt * fixed + static_cast<size_t>(tt) * rpw * (nb + 1) * sizeof(float2);
+            const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw), static_cast<unsigned>((batch + tt - 1) / tt));
+            if (tt == 4)
+                gemv_f32act_tokens_kernel<TYPE, 4><<<grid, kGemvThreads, lds, st>>>(
+                    W, x, y, static_cast<int>(rows), nb, rpw, static_cast<int>(batch));
+            else
+                gemv_f32act_tokens_kernel<TYPE, 2><<<grid, kGemvThreads, lds, st>>>(
+                    W, x, y, static_cast<int>(rows), nb, rpw, static_cast<int>(batch));
+            return hipGetLastError();
+        }
+    }
     const int rpw = pick_rows_per_wg(rows, nb, 60 * 1024 - fixed);
     const size_t lds = fixed + static_cast<size_t>(rpw) * (nb + 1) * sizeof(float2);
     const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw), static_cast<unsigned>(batch));
