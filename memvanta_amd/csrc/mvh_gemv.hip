@@ -398,13 +398,15 @@ __global__ __launch_bounds__(256) void batch4_f32act_kernel(const uint8_t* __res
 // in LDS, and the row's chain sum = fma(d_b, s_b, sum) then walks the lanes
 // in unit order (DPP shift by one lane per stage).  Persistent waves stride
 // over the tiles; every weight load is unconditional (clamped rows).
-template <uint32_t TYPE>
+template <uint32_t TYPE, int UB>
 __device__ __forceinline__ void gemv_f32act_persistent(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                        float* __restrict__ y, int N, int nb, int ntiles) {
-    constexpr int kU4 = 8 * Blk<TYPE>::kBytes / 16;  // 16-byte loads per unit
+    // a unit is UB blocks (8, or 4 to halve the weights each lane holds),
+    // loaded with 8-byte loads (a 4-block unit is only 8-byte aligned)
+    constexpr int kU2 = UB * Blk<TYPE>::kBytes / 8;
     extern __shared__ __align__(16) uint8_t smem[];
     float* s_x = reinterpret_cast<float*>(smem);
-    const int upr = nb >> 3;
+    const int upr = nb / UB;
     const size_t row_bytes = static_cast<size_t>(nb) * Blk<TYPE>::kBytes;
     const int t = threadIdx.x, lane = t & 63;
     const int TR = 64 / upr;
@@ -412,33 +414,31 @@ __device__ __forceinline__ void gemv_f32act_persistent(const uint8_t* __restrict
     const bool worker = r < TR;
     const int uu = worker ? u : 0;
     const int gw = blockIdx.x * 4 + (t >> 6), GW = gridDim.x * 4;
-    auto load = [&](uint32_t (&w)[4 * kU4], int tl) {
+    auto load = [&](uint32_t (&w)[2 * kU2], int tl) {
         const int grow = min(tl * TR + (worker ? r : 0), N - 1);
-        const uint4* src = reinterpret_cast<const uint4*>(W + static_cast<size_t>(grow) * row_bytes +
-                                                          static_cast<size_t>(uu) * 8 * Blk<TYPE>::kBytes);
+        const uint2* src = reinterpret_cast<const uint2*>(W + static_cast<size_t>(grow) * row_bytes +
+                                                          static_cast<size_t>(uu) * UB * Blk<TYPE>::kBytes);
 #pragma unroll
-        for (int k = 0; k < kU4; ++k) {
-            const uint4 v = src[k];
-            w[4 * k] = v.x;
-            w[4 * k + 1] = v.y;
-            w[4 * k + 2] = v.z;
-            w[4 * k + 3] = v.w;
+        for (int k = 0; k < kU2; ++k) {
+            const uint2 v = src[k];
+            w[2 * k] = v.x;
+            w[2 * k + 1] = v.y;
         }
     };
     // the wave's first two tiles go out before the activation staging
-    uint32_t wa[4 * kU4], wb[4 * kU4];
+    uint32_t wa[2 * kU2], wb[2 * kU2];
     int tile = gw;
     load(wa, min(tile, ntiles - 1));
     load(wb, min(tile + GW, ntiles - 1));
     for (int c = t; c < nb * 8; c += 256)
         *reinterpret_cast<float4*>(s_x + (c >> 6) * kXPitchF + (c & 63) * 4) = reinterpret_cast<const float4*>(x)[c];
     __syncthreads();
-    const float* xg = s_x + uu * kXPitchF;
-    auto tile_step = [&](int tl, const uint32_t (&w)[4 * kU4]) {
+    const float* xg = s_x + (uu * UB >> 3) * kXPitchF + (uu * UB & 7) * 32;
+    auto tile_step = [&](int tl, const uint32_t (&w)[2 * kU2]) {
         const int grow = tl * TR + r;
-        float2 pr[8];
+        float2 pr[UB];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < UB; ++j) {
             uint32_t dbits, qs[Blk<TYPE>::kQdw];
             unit_block<TYPE>(w, j, dbits, qs);
             pr[j] = make_float2(h2f(dbits), f32act_block_sum<TYPE>(qs, xg + j * 32));
@@ -450,7 +450,7 @@ __device__ __forceinline__ void gemv_f32act_persistent(const uint8_t* __restrict
             const float in = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x138, 0xf, 0xf, false));
             float acc = u == 0 ? 0.0f : in;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc = fmaf(pr[j].x, pr[j].y, acc);
+            for (int j = 0; j < UB; ++j) acc = fmaf(pr[j].x, pr[j].y, acc);
             sum = acc;
         }
         if (worker && grow < N && u == upr - 1) y[grow] = sum;
@@ -468,11 +468,11 @@ __device__ __forceinline__ void gemv_f32act_persistent(const uint8_t* __restrict
 
 __global__ __launch_bounds__(256) void gemv_f32act_persistent_q4_0(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
-    gemv_f32act_persistent<kQ4_0>(W, x, y, N, nb, ntiles);
+    gemv_f32act_persistent<kQ4_0, 4>(W, x, y, N, nb, ntiles);
 }
 __global__ __launch_bounds__(256) void gemv_f32act_persistent_q8_0(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
-    gemv_f32act_persistent<kQ8_0>(W, x, y, N, nb, ntiles);
+    gemv_f32act_persistent<kQ8_0, 4>(W, x, y, N, nb, ntiles);
 }
 
 // The same numerics for K % 256 == 0 with the work spread over lanes: lane
@@ -865,7 +865,7 @@ template <uint32_t TYPE>
 static hipError_t launch_f32act_any(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,
                                     size_t batch, hipStream_t st) {
     if (!rows || !batch) return hipSuccess;
-    if (batch == 1 && cols % 256 == 0 && cols / 256 <= 64) {
+    if (batch == 1 && cols % 256 == 0 && cols / 128 <= 64) {
         static const int cus = [] {
             int dev = 0;
             hipDeviceProp_t prop;
@@ -875,7 +875,7 @@ static hipError_t launch_f32act_any(const uint8_t* W, const float* x, float* y, 
             return 256;
         }();
         const int nb = static_cast<int>(cols / 32);
-        const int tr = 64 / (nb / 8);
+        const int tr = 64 / (nb / 4);
         const int ntiles = static_cast<int>((rows + tr - 1) / tr);
         const int waves = std::min(ntiles, cus * 16);
         const size_t lds = static_cast<size_t>(nb / 8) * kXPitchF * 4;
