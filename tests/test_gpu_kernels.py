@@ -94,7 +94,7 @@ def test_gemv_q4_0_bitexact(ctx, oracle, k, n):
 
 
 @pytest.mark.parametrize("k,n", [(288, 32000), (2048, 2048), (2048, 256), (5632, 2048), (4096, 4096), (288, 768),
-                                 (4096, 37), (256, 130), (11008, 64), (16384, 5)])
+                                 (4096, 37), (256, 130), (8192, 33), (11008, 64), (16384, 5)])
 def test_gemv_q8_0_bitexact(ctx, oracle, k, n):
     rng = np.random.default_rng(7 * k + n)
     w = _w(rng, synth.Q8_0, n, k)
@@ -104,12 +104,13 @@ def test_gemv_q8_0_bitexact(ctx, oracle, k, n):
     t.free()
 
 
-@pytest.mark.parametrize("k,n", [(4096, 37), (256, 130), (11008, 64), (16384, 5), (2048, 2048), (1024, 96)])
+@pytest.mark.parametrize("k,n", [(4096, 37), (256, 130), (8192, 33), (11008, 64), (16384, 5), (2048, 2048),
+                                 (1024, 96)])
 def test_q4_0_f32act_one_token_bitexact(ctx, oracle, k, n):
-    """dot_q4_0_fp32 for one token (tensor_matmul_batch with batch 1, K % 256
-    == 0: the persistent fp32-activation GEMV): row counts that leave the last
-    tile partial, one unit per row (K = 256) up to 64 (K = 16384), and K = 11008
-    (43 of 64 lanes of each wave working)."""
+    """dot_q4_0_fp32 for one token (tensor_matmul_batch with batch 1): the
+    persistent fp32-activation GEMV for K % 256 == 0 up to K = 8192 (4-block
+    units: 2 per row at K = 256, 64 at K = 8192; row counts that leave the
+    last tile partial), the two-phase kernel beyond (K = 11008, 16384)."""
     rng = np.random.default_rng(11 * k + n)
     w = _w(rng, synth.Q4_0, n, k)
     t = ctx.upload("blk.0.attn_q.weight", synth.Q4_0, k, n, w)
