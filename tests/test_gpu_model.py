@@ -142,6 +142,41 @@ def test_prefill_ragged_chunks_vs_oracle(tmp_path, oracle, max_batch, chunk):
 KV_TYPES = {"f32": capi.MVH_KV_F32, "q8": capi.MVH_KV_Q8}
 
 
+@pytest.fixture(scope="module")
+def gqa(tmp_path_factory):
+    """The 2-layer TinyLlama-shape mixed model of the GQA golden (32 heads, 4 KV heads)."""
+    g = golden("model_gqa.npz")
+    path = str(tmp_path_factory.mktemp("gqa") / "gqa.gguf")
+    assert synth.write_model(synth.TINYLLAMA_MIXED_2L, path, seed=int(g["seed"])) == str(g["model_sha"])
+    return path
+
+
+@pytest.mark.parametrize("tname", ["f16", "q8"])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_gqa_vs_reference_golden(gqa, tname, mode):
+    """Grouped-query attention (query head h reads KV head h / 8,
+    src/llama_model.cpp:248,256) against the compiled reference's own run:
+    prefill logits of 40 tokens (32 + 8 chunks), six greedy ids, the last
+    step's logits and KV bytes; then the captured-graph greedy loop."""
+    g = golden("model_gqa.npz")
+    key = f"{tname}_m{mode}"
+    kt = capi.MVH_KV_F16 if tname == "f16" else capi.MVH_KV_Q8
+    m = capi.Model(gqa, ctx=256, act_mode=mode, max_batch=32, kv_type=kt)
+    close(m.prefill(g["prompt"], 32), g[f"prefill_logits_{key}"], f"GQA {key} prefill")
+    ids, cur = [], 29
+    for _ in range(6):
+        lg = m.forward(cur)
+        cur = int(np.argmax(lg))
+        ids.append(cur)
+    assert ids == g[f"decode_ids_{key}"].tolist()
+    close(lg, g[f"decode_last_logits_{key}"], f"GQA {key} decode")
+    assert m.kv_bytes() == int(g[f"kv_bytes_{key}"])
+    m.reset()
+    m.prefill(g["prompt"], 32, logits=False)
+    assert m.generate_greedy(29, 6).tolist() == g[f"decode_ids_{key}"].tolist()
+    m.close()
+
+
 @pytest.mark.parametrize("tname", sorted(KV_TYPES))
 @pytest.mark.parametrize("mode", [0, 1])
 def test_tiny_kv_types_vs_reference_golden(tiny, tname, mode):

@@ -50,6 +50,36 @@ def tiny_model(tmp_path_factory):
     return path
 
 
+@pytest.fixture(scope="module")
+def gqa_model(tmp_path_factory):
+    """The 2-layer TinyLlama-shape mixed model (32 heads over 4 KV heads)."""
+    g = golden("model_gqa.npz")
+    path = str(tmp_path_factory.mktemp("gqa") / "gqa.gguf")
+    sha = synth.write_model(synth.TINYLLAMA_MIXED_2L, path, seed=int(g["seed"]))
+    assert sha == str(g["model_sha"]), "model generator drifted"
+    return path
+
+
+def _gqa_check(o, path, tname, mode):
+    """Oracle vs the compiled reference's GQA golden run: prefill logits of 40
+    tokens (32 + 8 chunks), six greedy steps, the last step's logits, KV bytes."""
+    g = golden("model_gqa.npz")
+    key = f"{tname}_m{mode}"
+    m = o.model(path, ctx=256, force_q8=bool(mode), kv_type=KV_TYPES[tname])
+    try:
+        assert_bitexact(m.prefill(g["prompt"], 32), g[f"prefill_logits_{key}"], f"GQA prefill logits {key}")
+        ids, cur = [], 29
+        for _ in range(6):
+            lg = m.forward(cur)
+            cur = int(np.argmax(lg))
+            ids.append(cur)
+        assert ids == g[f"decode_ids_{key}"].tolist(), f"GQA greedy ids {key}"
+        assert_bitexact(lg, g[f"decode_last_logits_{key}"], f"GQA decode logits {key}")
+        assert m.kv_bytes() == int(g[f"kv_bytes_{key}"])
+    finally:
+        m.close()
+
+
 # ----------------------------------------------------------------- fp16
 
 def test_fp16_to_fp32_exhaustive(oracle):
@@ -316,6 +346,14 @@ def test_tiny_model_kv_types_golden(oracle, tiny_model, tname, mode):
     assert m.kv_bytes() == int(g[f"kv{tname}_kv_bytes_m{mode}"])
 
 
+@pytest.mark.parametrize("tname", ["f16", "q8"])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_gqa_model_golden(oracle, gqa_model, tname, mode):
+    """32 query heads over 4 KV heads: head h reads KV head h / 8, which only a
+    grouped-query model tells apart from h % 4 (the tiny model has group 1)."""
+    _gqa_check(oracle, gqa_model, tname, mode)
+
+
 def test_tiny_model_vs_reference_live(oracle, ref, tiny_model):
     mo = oracle.model(tiny_model, ctx=256)
     mr = ref.model(tiny_model, ctx=256)
@@ -350,6 +388,12 @@ MUTATIONS = {
                                 "float w = alpha;\n    if (kv->type == MVO_KV_Q8) alpha = sc;"),
     "f32_tail_all_fused": ("for (int j = 0; j < 4; ++j) s = s + a[i + j] * b[i + j];",
                            "for (int j = 0; j < 4; ++j) s = fmaf(a[i + j], b[i + j], s);"),
+    # the KV head of query head h: h / group, not h % n_head_kv (equal when
+    # group = 1), once in the decode attention and once in the prefill loop
+    "gqa_head_map_decode": ("size_t kb = (h / group) * hd, qb = h * hd;",
+                            "size_t kb = (h % n_head_kv) * hd, qb = h * hd;"),
+    "gqa_head_map_prefill": ("kb = (h / group) * hd, qb = h * hd, upto = start + b;",
+                             "kb = (h % m->n_head_kv) * hd, qb = h * hd, upto = start + b;"),
     "batch4_unrounded_scale": ("float q = (float)qi * d;\n                    size_t off = b * 32 + h * 16 + k + j;",
                                "float q = (float)qi;\n                    size_t off = b * 32 + h * 16 + k + j;"),
 }
@@ -372,7 +416,7 @@ def _mutant(tmp, name):
     return Oracle(so)
 
 
-def _golden_ok(o, mats, tiny_model):
+def _golden_ok(o, mats, tiny_model, gqa_model):
     g = golden("kernels.npz")
     try:
         for name, (w, rows, cols, ty, key) in mats.items():
@@ -392,12 +436,18 @@ def _golden_ok(o, mats, tiny_model):
         m.close()
         for tname in KV_TYPES:
             _kv_types_check(o, tname)
+        _gqa_check(o, gqa_model, "f16", 0)
     except AssertionError:
         return False
     return True
 
 
+def test_unmutated_oracle_passes_golden_checks(oracle, mats, tiny_model, gqa_model):
+    """The control of the planted-mistake tests: the checks accept the oracle as built."""
+    assert _golden_ok(oracle, mats, tiny_model, gqa_model)
+
+
 @pytest.mark.parametrize("name", sorted(MUTATIONS))
-def test_planted_mistake_is_caught(name, mats, tiny_model):
+def test_planted_mistake_is_caught(name, mats, tiny_model, gqa_model):
     with tempfile.TemporaryDirectory() as tmp:
-        assert not _golden_ok(_mutant(tmp, name), mats, tiny_model), f"golden checks miss mutation {name}"
+        assert not _golden_ok(_mutant(tmp, name), mats, tiny_model, gqa_model), f"golden checks miss mutation {name}"
