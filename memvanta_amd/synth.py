@@ -171,6 +171,55 @@ def quantize_torch(ty: int, x):
     raise ValueError(f"unsupported type {ty}")
 
 
+# ---- native MemVanta blocks (src/quant.cpp:44-85), not GGUF: BlockQ4_0 =
+# {float d; uint8 qs[16]} (20 bytes, element 2i in the low nibble of qs[i],
+# 2i+1 in the high nibble), BlockQ8_0 = {float d; int8 qs[32]} (36 bytes).
+# Same arithmetic as quantize_q4_0 / quantize_q8_0 there: f32 amax/7 (amax/127),
+# f32 reciprocal, f32 product, round half to even, clamp; a zero block stores
+# d = 0 and zero bytes (not the nibble of zero).
+
+def _native_scales(xb: np.ndarray, div: float):
+    amax = np.max(np.abs(xb), axis=-1)
+    d = (amax / np.float32(div)).astype(np.float32)
+    with np.errstate(divide="ignore", over="ignore"):
+        inv = np.where(d == 0, np.float32(0), np.float32(1) / np.where(d == 0, np.float32(1), d)).astype(np.float32)
+    return d, inv
+
+
+def _x86_round_int(v: np.ndarray) -> np.ndarray:
+    """int(nearbyint(v)) as the reference's x86 build converts: round half to
+    even, and INT_MIN for NaN / infinities (a block so small that 1/d overflows)."""
+    with np.errstate(invalid="ignore"):
+        r = np.rint(v)
+        return np.where(np.abs(r) < 2.0 ** 31, r, -(2.0 ** 31))
+
+
+def quantize_q8_0_native(x: np.ndarray) -> np.ndarray:
+    """[..., K] fp32 -> uint8 [..., K/32, 36] (quantize_q8_0, src/quant.cpp:44-62)."""
+    x = np.ascontiguousarray(x, np.float32)
+    xb = x.reshape(x.shape[:-1] + (x.shape[-1] // 32, 32))
+    d, inv = _native_scales(xb, 127.0)
+    with np.errstate(invalid="ignore", over="ignore"):
+        q = np.clip(_x86_round_int(xb * inv[..., None]), -127, 127).astype(np.int8)
+    out = np.empty(xb.shape[:-1] + (36,), np.uint8)
+    out[..., :4] = d[..., None].view(np.uint8).reshape(d.shape + (4,))
+    out[..., 4:] = q.view(np.uint8)
+    return out
+
+
+def quantize_q4_0_native(x: np.ndarray) -> np.ndarray:
+    """[..., K] fp32 -> uint8 [..., K/32, 20] (quantize_q4_0, src/quant.cpp:64-85)."""
+    x = np.ascontiguousarray(x, np.float32)
+    xb = x.reshape(x.shape[:-1] + (x.shape[-1] // 32, 32))
+    d, inv = _native_scales(xb, 7.0)
+    with np.errstate(invalid="ignore", over="ignore"):
+        q = (np.clip(_x86_round_int(xb * inv[..., None]), -8, 7) + 8).astype(np.uint8)
+    out = np.empty(xb.shape[:-1] + (20,), np.uint8)
+    out[..., :4] = d[..., None].view(np.uint8).reshape(d.shape + (4,))
+    out[..., 4:] = np.where((d == 0)[..., None], np.uint8(0), q[..., 0::2] | (q[..., 1::2] << 4))
+    return out
+
+
 def quantize(ty: int, x: np.ndarray) -> np.ndarray:
     if ty == Q4_0:
         return quantize_q4_0(x)

@@ -1215,3 +1215,161 @@ int mvo_model_prefill(mvo_model* m, const int* tokens, size_t n, size_t batch, f
     }
     return 0;
 }
+
+/* ======================================================================
+ * Native (non-GGUF) block formats of src/quant.cpp / quant_kernels.cpp.
+ * BlockQ4_0 = {float d; uint8 qs[16]} (20 bytes), element 2i = low nibble of
+ * qs[i], element 2i+1 = high nibble (src/quant.cpp:79-81); BlockQ8_0 =
+ * {float d; int8 qs[32]} (36 bytes) (include/memvanta/quant.hpp:9-13).
+ * ====================================================================== */
+
+static float nq_d(const uint8_t* blk) {
+    float d;
+    memcpy(&d, blk, 4);
+    return d;
+}
+
+/* quantize_q8_0 (src/quant.cpp:44-62): amax = max|p| (fabs, NaN-skipping
+ * std::max), d = amax/127 or 0, q = clamp(nearbyint(p*(1/d)), -127, 127) in
+ * the default round-half-even mode; a zero block stores d = 0 and q = 0. */
+int mvo_nq_quantize_q8_0(const float* src, size_t n, uint8_t* out) {
+    if (n % 32) { set_err("q8_0 length must be multiple of 32"); return -1; }
+    for (size_t b = 0; b < n / 32; ++b) {
+        const float* p = src + 32 * b;
+        uint8_t* o = out + 36 * b;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) { float a = fabsf(p[i]); if (amax < a) amax = a; }
+        float d = amax == 0.0f ? 0.0f : amax / 127.0f;
+        memcpy(o, &d, 4);
+        if (d == 0.0f) { memset(o + 4, 0, 32); continue; }
+        float id = 1.0f / d;
+        for (int i = 0; i < 32; ++i) {
+            int q = (int)nearbyintf(p[i] * id);
+            q = q < -127 ? -127 : q > 127 ? 127 : q;
+            o[4 + i] = (uint8_t)(int8_t)q;
+        }
+    }
+    return 0;
+}
+
+/* quantize_q4_0 (src/quant.cpp:64-85): d = amax/7 or 0, q = clamp(nearbyint(
+ * p*(1/d)), -8, 7), nibble q+8, even elements in the low nibble. */
+int mvo_nq_quantize_q4_0(const float* src, size_t n, uint8_t* out) {
+    if (n % 32) { set_err("q4_0 length must be multiple of 32"); return -1; }
+    for (size_t b = 0; b < n / 32; ++b) {
+        const float* p = src + 32 * b;
+        uint8_t* o = out + 20 * b;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) { float a = fabsf(p[i]); if (amax < a) amax = a; }
+        float d = amax == 0.0f ? 0.0f : amax / 7.0f;
+        memcpy(o, &d, 4);
+        memset(o + 4, 0, 16);
+        if (d == 0.0f) continue;
+        float id = 1.0f / d;
+        for (int i = 0; i < 32; ++i) {
+            int q = (int)nearbyintf(p[i] * id);
+            q = q < -8 ? -8 : q > 7 ? 7 : q;
+            uint8_t nib = (uint8_t)(q + 8);
+            if ((i & 1) == 0) o[4 + i / 2] = nib;
+            else o[4 + i / 2] |= (uint8_t)(nib << 4);
+        }
+    }
+    return 0;
+}
+
+/* dot_q4_q8 (src/quant_kernels.cpp:52-66): isum exact per block, then
+ * sum += float(isum) * a.d * x.d, which GCC contracts into
+ * fma(float(isum) * a.d, x.d, sum) (the left product rounded first). */
+float mvo_nq_dot_q4_q8(const uint8_t* a, const uint8_t* x, size_t nb) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < nb; ++b) {
+        const uint8_t* wa = a + 20 * b;
+        const uint8_t* xb = x + 36 * b;
+        int isum = 0;
+        for (int k = 0; k < 32; ++k) {
+            uint8_t packed = wa[4 + k / 2];
+            int q4 = ((k & 1) ? (packed >> 4) : (packed & 0x0f)) - 8;
+            isum += q4 * (int)(int8_t)xb[4 + k];
+        }
+        float p = (float)isum * nq_d(wa);
+        sum = fmaf(p, nq_d(xb), sum);
+    }
+    return sum;
+}
+
+/* The AVX2 block dot shared by dot_q4_0 / dot_q8_0 (src/quant.cpp:87-156):
+ * lane j of eight accumulates elements j, 8+j, 16+j, 24+j by fma from zero,
+ * s = 0 + t0 + ... + t7 in order, then sum = fma(s, d, sum). */
+static float nq_block_sum(const int* q, const float* x) {
+    float t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < 32; k += 8)
+        for (int j = 0; j < 8; ++j) t[j] = fmaf((float)q[k + j], x[k + j], t[j]);
+    float s = 0.0f;
+    for (int j = 0; j < 8; ++j) s = s + t[j];
+    return s;
+}
+
+/* dot_q4_0 (src/quant.cpp:110-156): the nibbles unpacked back to natural
+ * element order (0..31), minus 8. */
+float mvo_nq_dot_q4_0(const uint8_t* a, const float* x, size_t n) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t* wa = a + 20 * b;
+        int q[32];
+        for (int k = 0; k < 32; ++k) {
+            uint8_t packed = wa[4 + k / 2];
+            q[k] = ((k & 1) ? (packed >> 4) : (packed & 0x0f)) - 8;
+        }
+        sum = fmaf(nq_block_sum(q, x + 32 * b), nq_d(wa), sum);
+    }
+    return sum;
+}
+
+/* dot_q8_0 (src/quant.cpp:87-108). */
+float mvo_nq_dot_q8_0(const uint8_t* a, const float* x, size_t n) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t* wa = a + 36 * b;
+        int q[32];
+        for (int k = 0; k < 32; ++k) q[k] = (int)(int8_t)wa[4 + k];
+        sum = fmaf(nq_block_sum(q, x + 32 * b), nq_d(wa), sum);
+    }
+    return sum;
+}
+
+/* matvec_q4_q8 (src/quant_kernels.cpp:68-76): y[r] = dot_q4_q8(row r, x). */
+int mvo_nq_matvec_q4_q8(const uint8_t* A, const uint8_t* x, float* y, size_t rows, size_t cols, int threads) {
+    if (cols % 32) { set_err("q4_q8 cols must be multiple of 32"); return -1; }
+    size_t nb = cols / 32;
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (size_t r = 0; r < rows; ++r) y[r] = mvo_nq_dot_q4_q8(A + r * nb * 20, x, nb);
+    return 0;
+}
+
+/* matmul_q4_0_batch (src/quant_kernels.cpp:78-91): y[b*rows + r] = dot_q4_0(row r, x + b*cols). */
+int mvo_nq_matmul_q4_0_batch(const uint8_t* A, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                             int threads) {
+    if (cols % 32) { set_err("q4_0 cols must be multiple of 32"); return -1; }
+    size_t nb = cols / 32;
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t b = 0; b < batch; ++b) y[b * rows + r] = mvo_nq_dot_q4_0(A + r * nb * 20, x + b * cols, cols);
+    return 0;
+}
+
+/* matvec_q4_0 / matvec_q8_0 (src/quant.cpp:158-174). */
+int mvo_nq_matvec_q4_0(const uint8_t* A, const float* x, float* y, size_t rows, size_t cols, int threads) {
+    if (cols % 32) { set_err("q4_0 cols must be multiple of 32"); return -1; }
+    size_t nb = cols / 32;
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (size_t r = 0; r < rows; ++r) y[r] = mvo_nq_dot_q4_0(A + r * nb * 20, x, cols);
+    return 0;
+}
+
+int mvo_nq_matvec_q8_0(const uint8_t* A, const float* x, float* y, size_t rows, size_t cols, int threads) {
+    if (cols % 32) { set_err("q8_0 cols must be multiple of 32"); return -1; }
+    size_t nb = cols / 32;
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (size_t r = 0; r < rows; ++r) y[r] = mvo_nq_dot_q8_0(A + r * nb * 36, x, cols);
+    return 0;
+}

@@ -24,6 +24,11 @@
  *                         probes of the stored values, bytes), model runs with
  *                         each cache type, plus an fp64 softmax bound
  *   model ............... bit-exact logits + greedy ids vs the compiled reference
+ *                         (the tiny MHA model and a 2-layer GQA model, 32/4 heads)
+ *   native blocks ....... quantize_q8_0 / quantize_q4_0 / matvec_q4_q8 /
+ *                         matmul_q4_0_batch / matvec_q4_0 / matvec_q8_0
+ *                         bit-exact vs golden vectors of the compiled
+ *                         reference (ties, zero blocks, saturation, K 32..11008)
  */
 #ifndef MV_ORACLE_H
 #define MV_ORACLE_H
@@ -111,6 +116,19 @@ int    mvo_model_forward(mvo_model* m, int token, float* logits);
 int    mvo_model_prefill(mvo_model* m, const int* tokens, size_t n, size_t batch, float* logits);
 size_t mvo_model_position(const mvo_model* m);
 size_t mvo_model_kv_bytes(const mvo_model* m);
+
+/* ---- native block formats (src/quant.cpp, src/quant_kernels.cpp): BlockQ4_0 20 bytes,
+ * BlockQ8_0 36 bytes; 0 / -1 with the reference's message in mvo_last_error() ---- */
+int   mvo_nq_quantize_q8_0(const float* src, size_t n, uint8_t* out);
+int   mvo_nq_quantize_q4_0(const float* src, size_t n, uint8_t* out);
+float mvo_nq_dot_q4_q8(const uint8_t* a, const uint8_t* x, size_t nb);
+float mvo_nq_dot_q4_0(const uint8_t* a, const float* x, size_t n);
+float mvo_nq_dot_q8_0(const uint8_t* a, const float* x, size_t n);
+int   mvo_nq_matvec_q4_q8(const uint8_t* A, const uint8_t* x, float* y, size_t rows, size_t cols, int threads);
+int   mvo_nq_matmul_q4_0_batch(const uint8_t* A, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                               int threads);
+int   mvo_nq_matvec_q4_0(const uint8_t* A, const float* x, float* y, size_t rows, size_t cols, int threads);
+int   mvo_nq_matvec_q8_0(const uint8_t* A, const float* x, float* y, size_t rows, size_t cols, int threads);
 
 #ifdef __cplusplus
 }

@@ -37,7 +37,55 @@ def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
-class Oracle:
+class _Native:
+    """Native block formats of src/quant.cpp / src/quant_kernels.cpp (BlockQ4_0 =
+    20 bytes, BlockQ8_0 = 36 bytes, as uint8 arrays [..., nblocks, 20 or 36])."""
+
+    _nq = ""  # symbol prefix: "mvo_nq_" (oracle) or "mvr_nq_" (reference)
+
+    def _bind_native(self):
+        L, p = self.lib, self._nq
+        getattr(L, p + "quantize_q8_0").argtypes = [_f32p, _sz, _u8p]
+        getattr(L, p + "quantize_q4_0").argtypes = [_f32p, _sz, _u8p]
+        getattr(L, p + "matvec_q4_q8").argtypes = [_u8p, _u8p, _f32p, _sz, _sz, C.c_uint]
+        getattr(L, p + "matmul_q4_0_batch").argtypes = [_u8p, _f32p, _f32p, _sz, _sz, _sz, C.c_uint]
+        getattr(L, p + "matvec_q4_0").argtypes = [_u8p, _f32p, _f32p, _sz, _sz, C.c_uint]
+        getattr(L, p + "matvec_q8_0").argtypes = [_u8p, _f32p, _f32p, _sz, _sz, C.c_uint]
+
+    def nq_quantize(self, x, bsize):
+        """quantize_q8_0 (bsize 36) / quantize_q4_0 (bsize 20) of the flattened x."""
+        x = _f32(x).ravel()
+        out = np.zeros((max(x.size // 32, 1), bsize), np.uint8)
+        fn = getattr(self.lib, self._nq + ("quantize_q8_0" if bsize == 36 else "quantize_q4_0"))
+        self._check(fn(x, x.size, out))
+        return out[: x.size // 32]
+
+    def nq_matvec_q4_q8(self, A, xq, rows, cols, threads=8):
+        y = np.empty(rows, np.float32)
+        self._check(getattr(self.lib, self._nq + "matvec_q4_q8")(np.ascontiguousarray(A, np.uint8).ravel(),
+                                                                   np.ascontiguousarray(xq, np.uint8).ravel(), y, rows,
+                                                                   cols, threads))
+        return y
+
+    def nq_matmul_q4_0_batch(self, A, X, rows, cols, threads=8):
+        X = _f32(X)
+        batch = 1 if X.ndim == 1 else X.shape[0]
+        y = np.empty((batch, rows), np.float32)
+        self._check(getattr(self.lib, self._nq + "matmul_q4_0_batch")(np.ascontiguousarray(A, np.uint8).ravel(),
+                                                                        X.ravel(), y, rows, cols, batch, threads))
+        return y
+
+    def nq_matvec(self, A, x, rows, cols, bsize, threads=8):
+        """matvec_q4_0 (bsize 20) / matvec_q8_0 (bsize 36), fp32 activations."""
+        y = np.empty(rows, np.float32)
+        fn = getattr(self.lib, self._nq + ("matvec_q8_0" if bsize == 36 else "matvec_q4_0"))
+        self._check(fn(np.ascontiguousarray(A, np.uint8).ravel(), _f32(x).ravel(), y, rows, cols, threads))
+        return y
+
+
+class Oracle(_Native):
+    _nq = "mvo_nq_"
+
     def __init__(self, path: str = ORACLE_SO):
         if not os.path.exists(path):
             raise FileNotFoundError(f"{path} missing: run `make -C oracle oracle`")
@@ -89,6 +137,7 @@ class Oracle:
         L.mvo_model_position.argtypes = [C.c_void_p]
         L.mvo_model_kv_bytes.restype = _sz
         L.mvo_model_kv_bytes.argtypes = [C.c_void_p]
+        self._bind_native()
 
     def _check(self, rc):
         if rc != 0:
@@ -265,8 +314,10 @@ class OracleModel:
         return self.o.lib.mvo_model_kv_bytes(self.h)
 
 
-class Ref:
+class Ref(_Native):
     """The compiled reference (public C++ API via ref_shim.cpp)."""
+
+    _nq = "mvr_nq_"
 
     def __init__(self, path: str = REF_SO):
         if not os.path.exists(path):
@@ -310,6 +361,7 @@ class Ref:
         L.mvr_profile_kind_name.argtypes = [C.c_int]
         L.mvr_profile_snapshot.restype = _sz
         L.mvr_profile_snapshot.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _sz, _sz]
+        self._bind_native()
 
     def _check(self, rc):
         if rc != 0:

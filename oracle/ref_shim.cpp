@@ -8,6 +8,7 @@
 #include "memvanta/gguf.hpp"
 #include "memvanta/gguf_kernels.hpp"
 #include "memvanta/llama_model.hpp"
+#include "memvanta/quant.hpp"
 
 #include <cstdint>
 #include <cstdlib>
@@ -53,6 +54,44 @@ void mvr_fp32_to_fp16_bits(uint32_t first, uint64_t count, uint16_t* out) {
 }
 
 float mvr_fp16_to_fp32(uint16_t h) { return memvanta::fp16_to_fp32(h); }
+
+// ---- native block formats (memvanta/quant.hpp): blocks are copied in and out
+// as raw bytes (BlockQ4_0 20 B, BlockQ8_0 36 B) ----
+int mvr_nq_quantize_q8_0(const float* src, size_t n, void* out) {
+    return guard([&] {
+        auto v = memvanta::quantize_q8_0(src, n);
+        std::memcpy(out, v.data(), v.size() * sizeof(memvanta::BlockQ8_0));
+    });
+}
+int mvr_nq_quantize_q4_0(const float* src, size_t n, void* out) {
+    return guard([&] {
+        auto v = memvanta::quantize_q4_0(src, n);
+        std::memcpy(out, v.data(), v.size() * sizeof(memvanta::BlockQ4_0));
+    });
+}
+int mvr_nq_dot_q4_q8(const void* a, const void* x, size_t n, float* out) {
+    return guard([&] {
+        *out = memvanta::dot_q4_q8(static_cast<const memvanta::BlockQ4_0*>(a), static_cast<const memvanta::BlockQ8_0*>(x), n);
+    });
+}
+int mvr_nq_matvec_q4_q8(const void* A, const void* x, float* y, size_t rows, size_t cols, unsigned threads) {
+    return guard([&] {
+        memvanta::matvec_q4_q8(static_cast<const memvanta::BlockQ4_0*>(A), static_cast<const memvanta::BlockQ8_0*>(x),
+                               y, rows, cols, threads);
+    });
+}
+int mvr_nq_matmul_q4_0_batch(const void* A, const float* x, float* y, size_t rows, size_t cols, size_t batch,
+                             unsigned threads) {
+    return guard([&] {
+        memvanta::matmul_q4_0_batch(static_cast<const memvanta::BlockQ4_0*>(A), x, y, rows, cols, batch, threads);
+    });
+}
+int mvr_nq_matvec_q4_0(const void* A, const float* x, float* y, size_t rows, size_t cols, unsigned threads) {
+    return guard([&] { memvanta::matvec_q4_0(static_cast<const memvanta::BlockQ4_0*>(A), x, y, rows, cols, threads); });
+}
+int mvr_nq_matvec_q8_0(const void* A, const float* x, float* y, size_t rows, size_t cols, unsigned threads) {
+    return guard([&] { memvanta::matvec_q8_0(static_cast<const memvanta::BlockQ8_0*>(A), x, y, rows, cols, threads); });
+}
 
 void* mvr_gguf_open(const char* path) {
     memvanta::GgufFile* f = nullptr;

@@ -372,6 +372,105 @@ def test_model_errors(oracle, tiny_model):
         m.forward(1)
 
 
+# ----------------------------------------------------------------- native block formats
+
+def _native_check(o):
+    """Oracle vs the compiled reference's native-format golden vectors
+    (quantize_q8_0 / quantize_q4_0 probes, matvec_q4_q8, matmul_q4_0_batch,
+    matvec_q4_0, matvec_q8_0 at K = 32, 288, 4096, 11008)."""
+    g = golden("native.npz")
+    assert np.array_equal(o.nq_quantize(g["probe_x"], 36), g["probe_q8"]), "quantize_q8_0 probes"
+    assert np.array_equal(o.nq_quantize(g["probe_x"], 20), g["probe_q4"]), "quantize_q4_0 probes"
+    for i, (rows, cols, B) in enumerate(mg.NATIVE_MATS):
+        key = f"r{rows}_c{cols}"
+        W = mg.native_weights(i, rows, cols)
+        assert hashlib.sha256(W.tobytes()).hexdigest() == str(g[f"{key}__w_sha"]), "weight generator drifted"
+        A4, A8 = o.nq_quantize(W, 20), o.nq_quantize(W, 36)
+        assert hashlib.sha256(A4.tobytes()).hexdigest() == str(g[f"{key}__a4_sha"]), f"{key} quantize_q4_0"
+        assert hashlib.sha256(A8.tobytes()).hexdigest() == str(g[f"{key}__a8_sha"]), f"{key} quantize_q8_0"
+        assert np.array_equal(o.nq_quantize(g[f"{key}__x"], 36), g[f"{key}__xq"]), f"{key} activation quantize_q8_0"
+        assert_bitexact(o.nq_matvec_q4_q8(A4, g[f"{key}__xq"], rows, cols), g[f"{key}__q4q8"], f"{key} matvec_q4_q8")
+        assert_bitexact(o.nq_matmul_q4_0_batch(A4, g[f"{key}__X"], rows, cols), g[f"{key}__batch"],
+                        f"{key} matmul_q4_0_batch")
+        assert_bitexact(o.nq_matvec(A4, g[f"{key}__x"], rows, cols, 20), g[f"{key}__mv_q4_0"], f"{key} matvec_q4_0")
+        assert_bitexact(o.nq_matvec(A8, g[f"{key}__x"], rows, cols, 36), g[f"{key}__mv_q8_0"], f"{key} matvec_q8_0")
+
+
+def test_native_golden(oracle):
+    _native_check(oracle)
+
+
+def test_native_numpy_quantizers_golden():
+    """memvanta_amd.synth's numpy quantizers (the GPU tests' input generator)
+    write the reference's bytes."""
+    g = golden("native.npz")
+    assert np.array_equal(synth.quantize_q8_0_native(g["probe_x"]).reshape(-1, 36), g["probe_q8"])
+    assert np.array_equal(synth.quantize_q4_0_native(g["probe_x"]).reshape(-1, 20), g["probe_q4"])
+    for i, (rows, cols, B) in enumerate(mg.NATIVE_MATS):
+        key = f"r{rows}_c{cols}"
+        W = mg.native_weights(i, rows, cols)
+        assert hashlib.sha256(synth.quantize_q4_0_native(W).tobytes()).hexdigest() == str(g[f"{key}__a4_sha"])
+        assert hashlib.sha256(synth.quantize_q8_0_native(W).tobytes()).hexdigest() == str(g[f"{key}__a8_sha"])
+
+
+def test_native_closed_forms(oracle):
+    """Block decode against its definition: a Q4_0 block of nibbles (q+8) with
+    d = 1 against a one-hot Q8 activation returns q (element 2i low nibble,
+    2i+1 high); the fp64 brute-force dot bounds every matvec; the ties of the
+    quantizers go to even."""
+    qs = np.arange(32) % 16 - 8
+    blk = np.zeros(20, np.uint8)
+    blk[:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
+    blk[4:] = (qs[0::2] + 8) | ((qs[1::2] + 8) << 4)
+    for e in range(32):
+        xb = np.zeros(36, np.uint8)
+        xb[:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
+        xb[4 + e] = 1
+        assert oracle.nq_matvec_q4_q8(blk, xb, 1, 32)[0] == qs[e]
+    t = np.zeros(32, np.float32)
+    t[0] = 127.0
+    t[1:5] = [0.5, 1.5, 2.5, -2.5]
+    q = oracle.nq_quantize(t, 36)[0, 4:9].view(np.int8)
+    assert q.tolist() == [127, 0, 2, 2, -2]
+    rng = np.random.default_rng(3)
+    rows, cols = 16, 1024
+    W = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+    A4 = oracle.nq_quantize(W, 20)
+    x = rng.standard_normal(cols, dtype=np.float32)
+    xq = oracle.nq_quantize(x, 36)
+    wd = A4.reshape(rows, -1, 20)
+    dw = wd[..., :4].copy().view(np.float32)[..., 0].astype(np.float64)
+    nib = np.stack([wd[..., 4:] & 15, wd[..., 4:] >> 4], -1).reshape(rows, -1, 32).astype(np.float64) - 8
+    xd = xq[:, :4].copy().view(np.float32)[:, 0].astype(np.float64)
+    xv = xq[:, 4:].view(np.int8).astype(np.float64)
+    exact = np.einsum("rbk,bk,rb,b->r", nib, xv, dw, xd)
+    got = oracle.nq_matvec_q4_q8(A4, xq, rows, cols)
+    assert np.all(np.abs(got - exact) <= 1e-4 * np.abs(exact).max())
+
+
+def test_native_errors(oracle):
+    with pytest.raises(RuntimeError, match="q4_q8 cols must be multiple of 32"):
+        oracle.nq_matvec_q4_q8(np.zeros(40, np.uint8), np.zeros(72, np.uint8), 1, 48)
+    with pytest.raises(RuntimeError, match="q4_0 cols must be multiple of 32"):
+        oracle.nq_matmul_q4_0_batch(np.zeros(40, np.uint8), np.zeros(48, np.float32), 1, 48)
+    with pytest.raises(RuntimeError, match="q8_0 length must be multiple of 32"):
+        oracle.nq_quantize(np.zeros(48, np.float32), 36)
+
+
+def test_native_vs_reference_live(oracle, ref):
+    rng = np.random.default_rng(8)
+    for rows, cols in ((5, 64), (33, 2048)):
+        W = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+        x = synth.activations(rng, 1, cols)[0]
+        A4 = ref.nq_quantize(W, 20)
+        xq = ref.nq_quantize(x, 36)
+        assert np.array_equal(oracle.nq_quantize(W, 20), A4)
+        assert np.array_equal(oracle.nq_quantize(x, 36), xq)
+        assert_bitexact(oracle.nq_matvec_q4_q8(A4, xq, rows, cols), ref.nq_matvec_q4_q8(A4, xq, rows, cols))
+        X = synth.activations(rng, 4, cols)
+        assert_bitexact(oracle.nq_matmul_q4_0_batch(A4, X, rows, cols), ref.nq_matmul_q4_0_batch(A4, X, rows, cols))
+
+
 # ----------------------------------------------------------------- planted mistakes
 
 MUTATIONS = {
@@ -394,6 +493,16 @@ MUTATIONS = {
                             "size_t kb = (h % n_head_kv) * hd, qb = h * hd;"),
     "gqa_head_map_prefill": ("kb = (h / group) * hd, qb = h * hd, upto = start + b;",
                              "kb = (h % m->n_head_kv) * hd, qb = h * hd, upto = start + b;"),
+    # native blocks: the weight scale must multiply isum before the fused add of x.d
+    "nq_q4q8_unfused": ("        sum = fmaf(p, nq_d(xb), sum);", "        sum = sum + p * nq_d(xb);"),
+    "nq_q4q8_scale_order": ("float p = (float)isum * nq_d(wa);\n        sum = fmaf(p, nq_d(xb), sum);",
+                            "float p = nq_d(wa) * nq_d(xb);\n        sum = fmaf(p, (float)isum, sum);"),
+    "nq_quant_round_away": ("int q = (int)nearbyintf(p[i] * id);\n            q = q < -127",
+                            "int q = (int)lroundf(p[i] * id);\n            q = q < -127"),
+    "nq_nibble_gguf_order": ("q[k] = ((k & 1) ? (packed >> 4) : (packed & 0x0f)) - 8;",
+                             "q[k] = (k < 16 ? (wa[4 + k] & 15) : (wa[4 + k - 16] >> 4)) - 8; (void)packed;"),
+    "nq_zero_block_unit_scale": ("float d = amax == 0.0f ? 0.0f : amax / 7.0f;",
+                                 "float d = amax == 0.0f ? 1.0f : amax / 7.0f;"),
     "batch4_unrounded_scale": ("float q = (float)qi * d;\n                    size_t off = b * 32 + h * 16 + k + j;",
                                "float q = (float)qi;\n                    size_t off = b * 32 + h * 16 + k + j;"),
 }
@@ -437,6 +546,7 @@ def _golden_ok(o, mats, tiny_model, gqa_model):
         for tname in KV_TYPES:
             _kv_types_check(o, tname)
         _gqa_check(o, gqa_model, "f16", 0)
+        _native_check(o)
     except AssertionError:
         return False
     return True
