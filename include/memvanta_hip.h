@@ -35,6 +35,12 @@
  *                         (the bytes it returns are copied to HBM once)
  *   mvh_model_*           LlamaModel               include/memvanta/llama_model.hpp:100-138,
  *                                                  src/llama_model.cpp:222-262 (device resident)
+ *   mvh_quantize_q8_0     quantize_q8_0            include/memvanta/quant.hpp:15, src/quant.cpp:44-62
+ *   mvh_quantize_q4_0     quantize_q4_0            quant.hpp:16, src/quant.cpp:64-85
+ *   mvh_matvec_q4_q8      matvec_q4_q8             quant.hpp:27, src/quant_kernels.cpp:68-76 (dot_q4_q8 :52-66)
+ *   mvh_matmul_q4_0_batch matmul_q4_0_batch        quant.hpp:29, src/quant_kernels.cpp:78-91
+ *   mvh_matvec_q4_0       matvec_q4_0              quant.hpp:25, src/quant.cpp:167-174 (dot_q4_0 :110-156)
+ *   mvh_matvec_q8_0       matvec_q8_0              quant.hpp:23, src/quant.cpp:158-165 (dot_q8_0 :87-108)
  */
 #ifndef MEMVANTA_HIP_H
 #define MEMVANTA_HIP_H
@@ -74,6 +80,13 @@ extern "C" {
 #define MVH_TYPE_Q4_0 2
 #define MVH_TYPE_Q8_0 8
 #define MVH_TYPE_Q6_K 14
+/* MemVanta's native (non-GGUF) blocks, include/memvanta/quant.hpp:9-13: BlockQ4_0 {float d; uint8 qs[16]}
+ * (20 bytes; element 2i = low nibble of qs[i], 2i+1 = high nibble) and BlockQ8_0 {float d; int8 qs[32]}
+ * (36 bytes).  A native matrix is rows (ne1) of cols/32 blocks (ne0 = cols), uploaded with
+ * mvh_tensor_upload like the GGUF types; only the mvh_matvec_q4_q8 / mvh_matmul_q4_0_batch /
+ * mvh_matvec_q4_0 / mvh_matvec_q8_0 entry points accept them. */
+#define MVH_TYPE_NATIVE_Q4_0 0x1002
+#define MVH_TYPE_NATIVE_Q8_0 0x1008
 
 typedef struct mvh_context mvh_context;
 typedef struct mvh_tensor mvh_tensor;
@@ -122,6 +135,22 @@ int mvh_read_row_f32(mvh_context* ctx, const mvh_tensor* w, size_t row, float* o
 /* fp32_to_fp16 (the reference's rounding, bit for bit) and the exact fp16_to_fp32 */
 int mvh_fp32_to_fp16(mvh_context* ctx, const float* x, uint16_t* out, size_t n, int ptr_kind);
 int mvh_fp16_to_fp32(mvh_context* ctx, const uint16_t* h, float* out, size_t n, int ptr_kind);
+
+/* ---- native block formats (src/quant.cpp, src/quant_kernels.cpp) ----
+ * Errors carry the reference's text ("q4_q8 cols must be multiple of 32", "q8_0 length must be multiple of
+ * 32", ...).  Device block pointers must be 4-byte aligned. */
+/* quantize_q8_0 / quantize_q4_0: x[n] (n % 32 == 0) -> n/32 blocks of 36 / 20 bytes (round half to even,
+ * d = amax/127 or amax/7, an all-zero block stores d = 0 and zero bytes) */
+int mvh_quantize_q8_0(mvh_context* ctx, const float* x, size_t n, void* blocks, int ptr_kind);
+int mvh_quantize_q4_0(mvh_context* ctx, const float* x, size_t n, void* blocks, int ptr_kind);
+/* matvec_q4_q8: y[r] = dot_q4_q8(row r of a MVH_TYPE_NATIVE_Q4_0 matrix, xq); xq = cols/32 BlockQ8_0 */
+int mvh_matvec_q4_q8(mvh_context* ctx, const mvh_tensor* a, const void* xq, float* y, int ptr_kind);
+/* matmul_q4_0_batch: y[b*rows + r] = dot_q4_0(row r, x + b*cols), fp32 activations */
+int mvh_matmul_q4_0_batch(mvh_context* ctx, const mvh_tensor* a, const float* x, float* y, size_t batch,
+                          int ptr_kind);
+/* matvec_q4_0 / matvec_q8_0: y[r] = dot_q4_0 / dot_q8_0(row r, x), fp32 activations */
+int mvh_matvec_q4_0(mvh_context* ctx, const mvh_tensor* a, const float* x, float* y, int ptr_kind);
+int mvh_matvec_q8_0(mvh_context* ctx, const mvh_tensor* a, const float* x, float* y, int ptr_kind);
 
 /* ---- paged KV cache (F32 / F16 / Q8 pages): all layers of one model on one device ---- */
 /* parse_kv_cache_type: "f32", "f16", "q8" or "q8_0"; anything else fails with

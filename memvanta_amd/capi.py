@@ -19,6 +19,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "memvanta_hip.h")
 MVH_HOST, MVH_DEVICE = 0, 1
 MVH_ACT_REF, MVH_ACT_Q8 = 0, 1
 MVH_KV_F32, MVH_KV_F16, MVH_KV_Q8 = 0, 1, 2  # KVCacheType order
+MVH_TYPE_NATIVE_Q4_0, MVH_TYPE_NATIVE_Q8_0 = 0x1002, 0x1008  # BlockQ4_0 (20 B) / BlockQ8_0 (36 B) of quant.hpp
 KV_DTYPE = {MVH_KV_F32: np.float32, MVH_KV_F16: np.uint16, MVH_KV_Q8: np.int8}
 STATUS = {0: "MVH_OK", 1: "MVH_E_INVALID", 2: "MVH_E_SHAPE", 3: "MVH_E_TYPE", 4: "MVH_E_DEVICE",
           5: "MVH_E_RANGE", 6: "MVH_E_NOMEM"}
@@ -82,6 +83,12 @@ _SIGS = {
     "mvh_model_position": (_int, [_vp, C.POINTER(_sz)]),
     "mvh_model_kv_bytes": (_int, [_vp, C.POINTER(_sz)]),
     "mvh_model_stream": (_int, [_vp, C.POINTER(_vp)]),
+    "mvh_quantize_q8_0": (_int, [_vp, _vp, _sz, _vp, _int]),
+    "mvh_quantize_q4_0": (_int, [_vp, _vp, _sz, _vp, _int]),
+    "mvh_matvec_q4_q8": (_int, [_vp, _vp, _vp, _vp, _int]),
+    "mvh_matmul_q4_0_batch": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
+    "mvh_matvec_q4_0": (_int, [_vp, _vp, _vp, _vp, _int]),
+    "mvh_matvec_q8_0": (_int, [_vp, _vp, _vp, _vp, _int]),
     "mvh_profile_enable": (None, [_int]),
     "mvh_profile_reset": (None, []),
     "mvh_profile_snapshot": (_int, [_vp, _sz, C.POINTER(_sz)]),
@@ -249,6 +256,41 @@ class Context:
         n = h.size if isinstance(h, np.ndarray) else h.numel()
         self._check(self.lib.mvh_fp16_to_fp32(self.h, _ptr(h), _ptr(out), n, _kind(h, out)))
         return out
+
+    # -- native block formats (src/quant.cpp, src/quant_kernels.cpp) --
+    def quantize_native(self, x, bsize: int, out=None):
+        """quantize_q8_0 (bsize 36) / quantize_q4_0 (bsize 20) of the flattened x -> uint8 [n/32, bsize]."""
+        fn = self.lib.mvh_quantize_q8_0 if bsize == 36 else self.lib.mvh_quantize_q4_0
+        if out is None:
+            x = np.ascontiguousarray(x, np.float32).ravel()
+            out = np.empty((x.size // 32, bsize), np.uint8)
+        n = x.size if isinstance(x, np.ndarray) else x.numel()
+        self._check(fn(self.h, _ptr(x), n, _ptr(out), _kind(x, out)))
+        return out
+
+    def matvec_q4_q8(self, a: "Tensor", xq, y=None):
+        if y is None:
+            xq = np.ascontiguousarray(xq, np.uint8)
+            y = np.empty(a.ne1, np.float32)
+        self._check(self.lib.mvh_matvec_q4_q8(self.h, a.h, _ptr(xq), _ptr(y), _kind(xq, y)))
+        return y
+
+    def matmul_q4_0_batch(self, a: "Tensor", x, y=None):
+        b = 1 if x.ndim == 1 else x.shape[0]
+        if y is None:
+            x = np.ascontiguousarray(x, np.float32)
+            y = np.empty((b, a.ne1), np.float32)
+        self._check(self.lib.mvh_matmul_q4_0_batch(self.h, a.h, _ptr(x), _ptr(y), b, _kind(x, y)))
+        return y
+
+    def matvec_native(self, a: "Tensor", x, y=None):
+        """matvec_q4_0 / matvec_q8_0 by the tensor's native type."""
+        fn = self.lib.mvh_matvec_q8_0 if a.type == MVH_TYPE_NATIVE_Q8_0 else self.lib.mvh_matvec_q4_0
+        if y is None:
+            x = np.ascontiguousarray(x, np.float32)
+            y = np.empty(a.ne1, np.float32)
+        self._check(fn(self.h, a.h, _ptr(x), _ptr(y), _kind(x, y)))
+        return y
 
     def kv_cache(self, n_layer: int, kv_dim: int, page_tokens: int = 128, max_tokens: int = 2048,
                  kv_type: int = MVH_KV_F16) -> "KVCache":

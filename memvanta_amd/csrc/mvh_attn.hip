@@ -42,8 +42,9 @@ __global__ __launch_bounds__(256) void kv_write_kernel(void* const* __restrict__
 // PagedKVCache::write, Q8 branch (src/llama_model.cpp:22): one scale per
 // token and row (K, V), s = max|x|/127 over the whole kv_dim row (1 when the
 // row is all zero; fmaxf skips a NaN as std::max(m, NaN) keeps m), then
-// q = clamp(round_half_away(x / s), -127, 127) with an IEEE division (a NaN
-// quotient clamps to -127, as lround's x86 result does).  Workgroup = (token,
+// q = clamp(round_half_away(x / s), -127, 127) with an IEEE division (a
+// non-finite quotient -- s underflowed to 0 -- clamps to -127, as lround's
+// x86 result does).  Workgroup = (token,
 // K or V); each thread holds up to kKWV groups of 4 elements in registers, so
 // the row is read once (kv_dim <= 4 * kKW * kKWV).
 constexpr int kKW = 1024;
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(kKW) void kv_write_q8_kernel(void* const* __restric
     uint8_t* page = static_cast<uint8_t*>((which ? pt_v : pt_k)[p / page_tokens]);
     int8_t* row = reinterpret_cast<int8_t*>(page) + static_cast<size_t>(slot) * kv_dim;
     auto qz = [&](float z) {
-        const float r = fminf(fmaxf(roundf(__fdiv_rn(z, s)), -127.0f), 127.0f);
+        const float r = q_round_away(__fdiv_rn(z, s), 127.0f);
         return static_cast<uint32_t>(static_cast<int>(r)) & 0xffu;
     };
 #pragma unroll
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
         const float mq = group_max<32>(fabsf(acc));
         const float dq = mq > 0.0f ? __fdiv_rn(mq, 127.0f) : 1.0f;
         const float id = __fdiv_rn(1.0f, dq);
-        const float rq = fminf(fmaxf(roundf(acc * id), -127.0f), 127.0f);
+        const float rq = q_round_away(acc * id, 127.0f);
         const int col = h * hd + d, D = n_head * hd;
         q8[q8_op ? q8_op_offset(b, col, D) : o] = static_cast<int8_t>(rq);
         if ((threadIdx.x & 31) == 0) q8d[o / 32] = dq;
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
                 const float m = group_max<32>(fabsf(acc));
                 const float d = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
                 const float id = __fdiv_rn(1.0f, d);
-                const float rq = fminf(fmaxf(roundf(acc * id), -127.0f), 127.0f);
+                const float rq = q_round_away(acc * id, 127.0f);
                 q8[o] = static_cast<int8_t>(rq);
                 if (t == 0) q8d[o / 32] = d;
             }
@@ -729,7 +730,7 @@ __global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const void* const* _
         uint32_t packed = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const float rq = fminf(fmaxf(roundf(acc[k] * id), -127.0f), 127.0f);
+            const float rq = q_round_away(acc[k] * id, 127.0f);
             packed |= (static_cast<uint32_t>(static_cast<int>(rq)) & 0xffu) << (8 * k);
         }
         const size_t qo = q8_op ? q8_op_offset(b, col, static_cast<size_t>(n_head) * hd) : o;

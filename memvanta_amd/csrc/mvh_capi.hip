@@ -26,7 +26,7 @@ struct mvh_context {
     Buf act;      // Q8 activations: q | d | s
     Buf xin;      // host-pointer staging of inputs
     Buf yout;     // host-pointer staging of outputs
-    Buf scratch;  // attention scores
+    Buf scores;   // attention scores
 };
 
 struct mvh_tensor {
@@ -55,6 +55,7 @@ namespace {
 
 thread_local std::string g_err;
 
+
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -78,6 +79,8 @@ const char* type_name(uint32_t t) {
         case MVH_TYPE_Q4_0: return "Q4_0";
         case MVH_TYPE_Q8_0: return "Q8_0";
         case MVH_TYPE_Q6_K: return "Q6_K";
+        case MVH_TYPE_NATIVE_Q4_0: return "native Q4_0";
+        case MVH_TYPE_NATIVE_Q8_0: return "native Q8_0";
     }
     return "type-?";
 }
@@ -90,6 +93,8 @@ uint64_t tensor_nbytes(uint32_t t, uint64_t n) {
         case MVH_TYPE_Q4_0: return n % 32 ? 0 : n / 32 * 18;
         case MVH_TYPE_Q8_0: return n % 32 ? 0 : n / 32 * 34;
         case MVH_TYPE_Q6_K: return n % 256 ? 0 : n / 256 * 210;
+        case MVH_TYPE_NATIVE_Q4_0: return n % 32 ? 0 : n / 32 * 20;
+        case MVH_TYPE_NATIVE_Q8_0: return n % 32 ? 0 : n / 32 * 36;
     }
     return 0;
 }
@@ -145,14 +150,22 @@ struct ActView {
     float* d;
     int* s;
 };
-int act_buffers(mvh_context* c, size_t rows, size_t cols, ActView* v) {
+size_t act_bytes(size_t rows, size_t cols) { return up16(rows * cols) + 2 * up16(rows * (cols / 32) * 4); }
+ActView act_carve(void* base_p, size_t rows, size_t cols) {
     const size_t nq = up16(rows * cols), nd = up16(rows * (cols / 32) * 4);
-    if (int rc = grow(c, c->act, nq + 2 * nd)) return rc;
-    auto* base = static_cast<uint8_t*>(c->act.p);
-    v->q = reinterpret_cast<int8_t*>(base);
-    v->d = reinterpret_cast<float*>(base + nq);
-    v->s = reinterpret_cast<int*>(base + nq + nd);
+    auto* base = static_cast<uint8_t*>(base_p);
+    return ActView{reinterpret_cast<int8_t*>(base), reinterpret_cast<float*>(base + nq),
+                   reinterpret_cast<int*>(base + nq + nd)};
+}
+int act_buffers(mvh_context* c, size_t rows, size_t cols, ActView* v) {
+    if (int rc = grow(c, c->act, act_bytes(rows, cols))) return rc;
+    *v = act_carve(c->act.p, rows, cols);
     return MVH_OK;
+}
+// Activation rows the FORCE_Q8 Q4_0 path of tensor_matmul_batch_v06 quantizes
+// into: whole 16-token slabs in the MFMA GEMM's operand order, else one row per token.
+size_t v06_act_rows(size_t batch, size_t cols) {
+    return mvh::gemm_q4_0_mfma_ok(cols) ? mvh::q8_op_bytes(batch, cols) / cols : batch;
 }
 
 #define CHECK_CTX(c)                                                   \
@@ -303,7 +316,7 @@ int mvh_context_destroy(mvh_context* c) {
     if (!c) return MVH_OK;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
-    for (auto* b : {&c->act, &c->xin, &c->yout, &c->scratch})
+    for (auto* b : {&c->act, &c->xin, &c->yout, &c->scores})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -328,7 +341,7 @@ static int make_tensor(mvh_context* c, const char* name, uint32_t type, uint64_t
     *out = nullptr;
     const uint64_t want = tensor_nbytes(type, ne0 * ne1);
     if (type != MVH_TYPE_F32 && type != MVH_TYPE_F16 && type != MVH_TYPE_Q4_0 && type != MVH_TYPE_Q8_0 &&
-        type != MVH_TYPE_Q6_K)
+        type != MVH_TYPE_Q6_K && type != MVH_TYPE_NATIVE_Q4_0 && type != MVH_TYPE_NATIVE_Q8_0)
         return fail(MVH_E_TYPE, "unsupported GGML type %u: %s", type, name ? name : "");
     if (!want || want != nbytes)
         return fail(MVH_E_SHAPE, "tensor byte size %llu does not match %s [%llu x %llu]: %s",
@@ -422,9 +435,15 @@ int mvh_quantize_q8(mvh_context* c, const float* x, size_t batch, size_t cols, i
     return MVH_OK;
 }
 
+static bool is_native(const mvh_tensor* w) {
+    return w->type == MVH_TYPE_NATIVE_Q4_0 || w->type == MVH_TYPE_NATIVE_Q8_0;
+}
+
 int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, int kind) {
     CHECK_CTX(c);
     if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (is_native(w))
+        return fail(MVH_E_TYPE, "unsupported matvec tensor type %s: %s", type_name(w->type), w->name.c_str());
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
     const size_t cols = w->ne0, rows = w->ne1;
     if (!rows) return prof_empty(w, 1);
@@ -500,6 +519,8 @@ int mvh_matvec_q8(mvh_context* c, const mvh_tensor* w, const int8_t* q, const fl
 int mvh_matmul_batch(mvh_context* c, const mvh_tensor* w, const float* x, float* y, size_t batch, int kind) {
     CHECK_CTX(c);
     if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (is_native(w))
+        return fail(MVH_E_TYPE, "unsupported batch matrix tensor type %s: %s", type_name(w->type), w->name.c_str());
     const size_t cols = w->ne0, rows = w->ne1;
     if (!batch || !rows) return prof_empty(w, batch);
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
@@ -516,34 +537,17 @@ int mvh_matmul_batch(mvh_context* c, const mvh_tensor* w, const float* x, float*
     return finish_out(c, y, yd, batch * rows * 4, kind);
 }
 
-int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, float* y, size_t batch, int act_mode,
-                         int kind) {
-    CHECK_CTX(c);
-    if (!w) return fail(MVH_E_INVALID, "null tensor");
-    if (act_mode != MVH_ACT_REF && act_mode != MVH_ACT_Q8) return fail(MVH_E_INVALID, "bad act_mode %d", act_mode);
-    const size_t cols = w->ne0, rows = w->ne1;
-    // fallback conditions of src/gguf_kernels.cpp:263
-    if (batch < 2 || (w->type != MVH_TYPE_Q4_0 && w->type != MVH_TYPE_Q8_0) || cols % 32)
-        return mvh_matmul_batch(c, w, x, y, batch, kind);
-    if (!rows) return prof_empty(w, batch);
-    if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
-    const void* xv = nullptr;
-    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xv)) return rc;
-    const auto* xd = static_cast<const float*>(xv);
-    float* yd = y;
-    if (kind == MVH_HOST) {
-        if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
-        yd = static_cast<float*>(c->yout.p);
-    }
-    ProfSpan span(c, w, batch);
+// tensor_matmul_batch_v06 past its fallback checks (src/gguf_kernels.cpp:264-270),
+// on device buffers: `act` is the Q8 activation scratch of the FORCE_Q8 Q4_0
+// branch (v06_act_rows(batch, cols) rows), unused otherwise.
+static int v06_device(mvh_context* c, const mvh_tensor* w, const float* xd, float* yd, size_t batch, int act_mode,
+                      const ActView& a) {
+    const size_t cols = w->ne0, rows = w->ne1, nb = cols / 32;
     const auto* W = static_cast<const uint8_t*>(w->d);
-    const size_t nb = cols / 32;
     if (act_mode == MVH_ACT_Q8) {
         if (w->type == MVH_TYPE_Q4_0) {
-            ActView a;
             const bool mfma = mvh::gemm_q4_0_mfma_ok(cols);  // int8 MFMA tiles, same per-block chain
             // the MFMA path takes the activations in its operand order (whole 16-token slabs)
-            if (int rc = act_buffers(c, mfma ? mvh::q8_op_bytes(batch, cols) / cols : batch, cols, &a)) return rc;
             MVH_HIP(mvh::launch_quantize_q8(xd, a.q, a.d, a.s, batch, cols, c->stream, mfma));
             if (mfma) {
                 MVH_HIP(mvh::launch_gemm_q4_0_q8_mfma(W, a.q, a.d, yd, rows, cols, batch, c->stream));
@@ -566,6 +570,33 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
                 return rc;
         }
     }
+    return MVH_OK;
+}
+
+int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, float* y, size_t batch, int act_mode,
+                         int kind) {
+    CHECK_CTX(c);
+    if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (act_mode != MVH_ACT_REF && act_mode != MVH_ACT_Q8) return fail(MVH_E_INVALID, "bad act_mode %d", act_mode);
+    const size_t cols = w->ne0, rows = w->ne1;
+    // fallback conditions of src/gguf_kernels.cpp:263
+    if (batch < 2 || (w->type != MVH_TYPE_Q4_0 && w->type != MVH_TYPE_Q8_0) || cols % 32)
+        return mvh_matmul_batch(c, w, x, y, batch, kind);
+    if (!rows) return prof_empty(w, batch);
+    if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
+    const void* xv = nullptr;
+    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xv)) return rc;
+    const auto* xd = static_cast<const float*>(xv);
+    float* yd = y;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
+        yd = static_cast<float*>(c->yout.p);
+    }
+    ProfSpan span(c, w, batch);
+    ActView a{};
+    if (act_mode == MVH_ACT_Q8 && w->type == MVH_TYPE_Q4_0)
+        if (int rc = act_buffers(c, v06_act_rows(batch, cols), cols, &a)) return rc;
+    if (int rc = v06_device(c, w, xd, yd, batch, act_mode, a)) return rc;
     if (int rc = span.end()) return rc;
     return finish_out(c, y, yd, batch * rows * 4, kind);
 }
@@ -573,6 +604,8 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
 int mvh_read_row_f32(mvh_context* c, const mvh_tensor* w, size_t row, float* out, int kind) {
     CHECK_CTX(c);
     if (!w || !out) return fail(MVH_E_INVALID, "null argument");
+    if (is_native(w))
+        return fail(MVH_E_TYPE, "unsupported embedding tensor type %s: %s", type_name(w->type), w->name.c_str());
     if (row >= w->ne1) return fail(MVH_E_RANGE, "tensor row shape mismatch: %s", w->name.c_str());
     if (w->type == MVH_TYPE_Q6_K && w->ne0 % 256)
         return fail(MVH_E_SHAPE, "Q6_K embedding row not block aligned: %s", w->name.c_str());
@@ -613,6 +646,99 @@ int mvh_fp16_to_fp32(mvh_context* c, const uint16_t* h, float* out, size_t n, in
     }
     MVH_HIP(mvh::launch_h2f(static_cast<const uint16_t*>(hd), od, n, c->stream));
     return finish_out(c, out, od, n * 4, kind);
+}
+
+// ---- native block formats (src/quant.cpp, src/quant_kernels.cpp) ----
+
+static int quantize_native(mvh_context* c, uint32_t type, const float* x, size_t n, void* blocks, int kind) {
+    CHECK_CTX(c);
+    const bool q4 = type == mvh::kNQ4_0;
+    if (n % 32) return fail(MVH_E_SHAPE, q4 ? "q4_0 length must be multiple of 32" : "q8_0 length must be multiple of 32");
+    if (!n) return MVH_OK;
+    if (!x || !blocks) return fail(MVH_E_INVALID, "null argument");
+    const size_t out_bytes = n / 32 * (q4 ? 20 : 36);
+    const void* xd = nullptr;
+    if (int rc = stage_in(c, c->xin, x, n * 4, kind, &xd)) return rc;
+    void* od = blocks;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, out_bytes)) return rc;
+        od = c->yout.p;
+    } else if (reinterpret_cast<uintptr_t>(blocks) & 3) {
+        return fail(MVH_E_INVALID, "device blocks must be 4-byte aligned");
+    }
+    MVH_HIP(mvh::launch_quantize_native(type, static_cast<const float*>(xd), static_cast<uint8_t*>(od), n, c->stream));
+    return finish_out(c, blocks, od, out_bytes, kind);
+}
+
+int mvh_quantize_q8_0(mvh_context* c, const float* x, size_t n, void* blocks, int kind) {
+    return quantize_native(c, mvh::kNQ8_0, x, n, blocks, kind);
+}
+
+int mvh_quantize_q4_0(mvh_context* c, const float* x, size_t n, void* blocks, int kind) {
+    return quantize_native(c, mvh::kNQ4_0, x, n, blocks, kind);
+}
+
+static int need_native(const mvh_tensor* w, uint32_t type, const char* fn) {
+    if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (w->type != type)
+        return fail(MVH_E_TYPE, "%s needs a %s tensor, got %s: %s", fn, type_name(type), type_name(w->type),
+                    w->name.c_str());
+    return MVH_OK;
+}
+
+int mvh_matvec_q4_q8(mvh_context* c, const mvh_tensor* w, const void* xq, float* y, int kind) {
+    CHECK_CTX(c);
+    if (int rc = need_native(w, MVH_TYPE_NATIVE_Q4_0, "matvec_q4_q8")) return rc;
+    const size_t cols = w->ne0, rows = w->ne1;
+    if (cols % 32) return fail(MVH_E_SHAPE, "q4_q8 cols must be multiple of 32");
+    if (!rows) return MVH_OK;
+    if (!xq || !y) return fail(MVH_E_INVALID, "null xq/y");
+    if (kind == MVH_DEVICE && (reinterpret_cast<uintptr_t>(xq) & 3))
+        return fail(MVH_E_INVALID, "device xq must be 4-byte aligned");
+    const void* xd = nullptr;
+    if (int rc = stage_in(c, c->xin, xq, cols / 32 * 36, kind, &xd)) return rc;
+    float* yd = y;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, rows * 4)) return rc;
+        yd = static_cast<float*>(c->yout.p);
+    }
+    MVH_HIP(mvh::launch_matvec_q4q8_native(static_cast<const uint8_t*>(w->d), static_cast<const uint8_t*>(xd), yd, rows,
+                                           cols, c->stream));
+    return finish_out(c, y, yd, rows * 4, kind);
+}
+
+static int native_f32act(mvh_context* c, const mvh_tensor* w, uint32_t type, const char* fn, const char* shape_err,
+                         const float* x, float* y, size_t batch, int kind) {
+    CHECK_CTX(c);
+    if (int rc = need_native(w, type, fn)) return rc;
+    const size_t cols = w->ne0, rows = w->ne1;
+    if (cols % 32) return fail(MVH_E_SHAPE, "%s", shape_err);
+    if (!rows || !batch) return MVH_OK;
+    if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
+    const void* xd = nullptr;
+    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
+    float* yd = y;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
+        yd = static_cast<float*>(c->yout.p);
+    }
+    MVH_HIP(mvh::launch_gemv_native_f32act(type == MVH_TYPE_NATIVE_Q4_0 ? mvh::kNQ4_0 : mvh::kNQ8_0,
+                                           static_cast<const uint8_t*>(w->d), static_cast<const float*>(xd), yd, rows,
+                                           cols, batch, c->stream));
+    return finish_out(c, y, yd, batch * rows * 4, kind);
+}
+
+int mvh_matmul_q4_0_batch(mvh_context* c, const mvh_tensor* w, const float* x, float* y, size_t batch, int kind) {
+    return native_f32act(c, w, MVH_TYPE_NATIVE_Q4_0, "matmul_q4_0_batch", "q4_0 cols must be multiple of 32", x, y,
+                         batch, kind);
+}
+
+int mvh_matvec_q4_0(mvh_context* c, const mvh_tensor* w, const float* x, float* y, int kind) {
+    return native_f32act(c, w, MVH_TYPE_NATIVE_Q4_0, "matvec_q4_0", "q4_0 cols must be multiple of 32", x, y, 1, kind);
+}
+
+int mvh_matvec_q8_0(mvh_context* c, const mvh_tensor* w, const float* x, float* y, int kind) {
+    return native_f32act(c, w, MVH_TYPE_NATIVE_Q8_0, "matvec_q8_0", "q8_0 cols must be multiple of 32", x, y, 1, kind);
 }
 
 int mvh_kv_parse_type(const char* s, int* type) {
@@ -781,10 +907,10 @@ int mvh_attn_decode(mvh_context* c, const mvh_kv_cache* kv, size_t layer, const 
         if (int rc = grow(c, c->yout, qn * 4)) return rc;
         od = static_cast<float*>(c->yout.p);
     }
-    if (int rc = grow(c, c->scratch, n_head * (pos + 1) * 4)) return rc;
+    if (int rc = grow(c, c->scores, n_head * (pos + 1) * 4)) return rc;
     const size_t base = layer * kv->max_pages;
     MVH_HIP(mvh::launch_attn_decode(kv->type, kv->dk + base, kv->dv + base, static_cast<const float*>(qd),
-                                    static_cast<float*>(c->scratch.p), od, pos, n_head, n_head_kv, head_dim,
+                                    static_cast<float*>(c->scores.p), od, pos, n_head, n_head_kv, head_dim,
                                     kv->kv_dim, kv->page_tokens, c->stream));
     return finish_out(c, out, od, qn * 4, kind);
 }
@@ -811,10 +937,10 @@ int mvh_attn_batch(mvh_context* c, const mvh_kv_cache* kv, size_t layer, const f
         if (int rc = grow(c, c->yout, qn * 4)) return rc;
         od = static_cast<float*>(c->yout.p);
     }
-    if (int rc = grow(c, c->scratch, n_tokens * n_head * (last + 1) * 4)) return rc;
+    if (int rc = grow(c, c->scores, n_tokens * n_head * (last + 1) * 4)) return rc;
     const size_t base = layer * kv->max_pages;
     const float* qf = static_cast<const float*>(qd);
-    float* sc = static_cast<float*>(c->scratch.p);
+    float* sc = static_cast<float*>(c->scores.p);
     if (head_dim % 32 == 0)  // scores once per (token, head), V tiles shared by groups of 32 tokens
         MVH_HIP(mvh::launch_attn_prefill(kv->type, kv->dk + base, kv->dv + base, qf, n_head * head_dim, sc, od, nullptr,
                                          nullptr, false, nullptr, pos, last + 1, n_tokens, n_head, n_head_kv, head_dim,

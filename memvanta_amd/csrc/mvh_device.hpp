@@ -98,6 +98,18 @@ __device__ __forceinline__ double wave_sum(double v) {
     return mine + other;
 }
 
+// clamp(lround(v), -lim, lim) as the reference's x86 build evaluates it: a
+// finite v rounds half away from zero and clamps; a non-finite v (a scale so
+// small that 1/d overflowed, or 0/0) converts to LONG_MIN, i.e. -lim.
+__device__ __forceinline__ float q_round_away(float v, float lim) {
+    return __builtin_isfinite(v) ? fminf(fmaxf(roundf(v), -lim), lim) : -lim;
+}
+// clamp((int)nearbyint(v), lo, hi) likewise: round half to even, a non-finite v
+// converts to INT_MIN, i.e. lo.
+__device__ __forceinline__ float q_round_even(float v, float lo, float hi) {
+    return __builtin_isfinite(v) ? fminf(fmaxf(__builtin_rintf(v), lo), hi) : lo;
+}
+
 // quantize_q8 (src/gguf_kernels.cpp:160-172) for one 32-element block held as
 // 4 consecutive floats in each lane of an aligned group of 8 lanes:
 //   mx = max|z| (exact in any order), d = mx > 0 ? mx/127 : 1, inv = 1/d,
@@ -109,11 +121,7 @@ __device__ __forceinline__ uint32_t quantize_q8_x4(float4 v, float& d, int& s) {
     m = group_max<8>(m);
     d = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
     const float inv = __fdiv_rn(1.0f, d);
-    auto qz = [&](float z) {
-        float r = roundf(z * inv);
-        r = fminf(fmaxf(r, -127.0f), 127.0f);
-        return static_cast<int>(r);
-    };
+    auto qz = [&](float z) { return static_cast<int>(q_round_away(z * inv, 127.0f)); };
     const int q0 = qz(v.x), q1 = qz(v.y), q2 = qz(v.z), q3 = qz(v.w);
     s = group_sum<8>(q0 + q1 + q2 + q3);
     return (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |

@@ -172,7 +172,8 @@ template <uint32_t TYPE>
 struct Blk;
 template <>
 struct Blk<kQ4_0> {
-    static constexpr int kBytes = 18, kQdw = 4;
+    static constexpr int kBytes = 18, kQdw = 4, kScale = 2;
+    static __device__ __forceinline__ float scale(uint32_t bits) { return h2f(bits); }
     // element e: low nibble of byte e (e < 16) or high nibble of byte e-16, minus 8
     static __device__ __forceinline__ int value(const uint32_t (&qs)[kQdw], int e) {
         const int byte = e & 15;
@@ -182,7 +183,27 @@ struct Blk<kQ4_0> {
 };
 template <>
 struct Blk<kQ8_0> {
-    static constexpr int kBytes = 34, kQdw = 8;
+    static constexpr int kBytes = 34, kQdw = 8, kScale = 2;
+    static __device__ __forceinline__ float scale(uint32_t bits) { return h2f(bits); }
+    static __device__ __forceinline__ int value(const uint32_t (&qs)[kQdw], int e) {
+        return static_cast<int>(static_cast<int8_t>(qs[e >> 2] >> (8 * (e & 3))));
+    }
+};
+// native BlockQ4_0 (src/quant.cpp:79-81): f32 d, element e = nibble e & 1 of
+// byte e >> 1, minus 8 (dot_q4_0 unpacks them back to element order, :121-128)
+template <>
+struct Blk<kNQ4_0> {
+    static constexpr int kBytes = 20, kQdw = 4, kScale = 4;
+    static __device__ __forceinline__ float scale(uint32_t bits) { return __uint_as_float(bits); }
+    static __device__ __forceinline__ int value(const uint32_t (&qs)[kQdw], int e) {
+        return static_cast<int>((qs[e >> 3] >> (8 * ((e >> 1) & 3) + 4 * (e & 1))) & 15u) - 8;
+    }
+};
+// native BlockQ8_0: f32 d, int8 qs[32]
+template <>
+struct Blk<kNQ8_0> {
+    static constexpr int kBytes = 36, kQdw = 8, kScale = 4;
+    static __device__ __forceinline__ float scale(uint32_t bits) { return __uint_as_float(bits); }
     static __device__ __forceinline__ int value(const uint32_t (&qs)[kQdw], int e) {
         return static_cast<int>(static_cast<int8_t>(qs[e >> 2] >> (8 * (e & 3))));
     }
@@ -212,7 +233,11 @@ template <uint32_t TYPE>
 __device__ __forceinline__ void unit_block(const uint32_t* w, int j, uint32_t& dbits,
                                            uint32_t (&qs)[Blk<TYPE>::kQdw]) {
     const int o = Blk<TYPE>::kBytes * j;
-    if ((o & 3) == 0) {
+    if constexpr (Blk<TYPE>::kScale == 4) {  // native blocks: scale and quants dword aligned
+        dbits = w[o / 4];
+#pragma unroll
+        for (int k = 0; k < Blk<TYPE>::kQdw; ++k) qs[k] = w[o / 4 + 1 + k];
+    } else if ((o & 3) == 0) {
         dbits = w[o / 4] & 0xffffu;
 #pragma unroll
         for (int k = 0; k < Blk<TYPE>::kQdw; ++k) qs[k] = align16(w[o / 4 + k + 1], w[o / 4 + k]);
@@ -266,15 +291,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_f32act_kernel(const uint8_t
             for (int j = 0; j < 8; ++j) {
                 uint32_t dbits, qs[Blk<TYPE>::kQdw];
                 unit_block<TYPE>(w, j, dbits, qs);
-                pout[j] = make_float2(h2f(dbits), f32act_block_sum<TYPE>(qs, xg + j * 32));
+                pout[j] = make_float2(Blk<TYPE>::scale(dbits), f32act_block_sum<TYPE>(qs, xg + j * 32));
             }
         } else {
             const uint16_t* src = reinterpret_cast<const uint16_t*>(tile + static_cast<size_t>(u) * BB);
+            constexpr int S = Blk<TYPE>::kScale / 2;  // 16-bit words of the scale
             uint32_t qs[Blk<TYPE>::kQdw];
 #pragma unroll
             for (int k = 0; k < Blk<TYPE>::kQdw; ++k)
-                qs[k] = src[1 + 2 * k] | (static_cast<uint32_t>(src[2 + 2 * k]) << 16);
-            pout[0] = make_float2(h2f(src[0]),
+                qs[k] = src[S + 2 * k] | (static_cast<uint32_t>(src[S + 1 + 2 * k]) << 16);
+            const uint32_t dbits = S == 1 ? src[0] : src[0] | (static_cast<uint32_t>(src[1]) << 16);
+            pout[0] = make_float2(Blk<TYPE>::scale(dbits),
                                   f32act_block_sum<TYPE>(qs, s_x + (b0 >> 3) * kXPitchF + (b0 & 7) * 32));
         }
     }
@@ -331,7 +358,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_f32act_tokens_kernel(const 
         for (int j = 0; j < 8; ++j) {
             uint32_t dbits, qs[Blk<TYPE>::kQdw];
             unit_block<TYPE>(w, j, dbits, qs);
-            const float d = h2f(dbits);
+            const float d = Blk<TYPE>::scale(dbits);
             for (int tk = 0; tk < nt; ++tk)
                 s_pair[(tk * rows_per_wg + row) * pitch + b0 + j] =
                     make_float2(d, f32act_block_sum<TYPE>(qs, s_x + tk * xstride + (b0 >> 3) * kXPitchF + j * 32));
@@ -441,7 +468,7 @@ __device__ __forceinline__ void gemv_f32act_persistent(const uint8_t* __restrict
         for (int j = 0; j < UB; ++j) {
             uint32_t dbits, qs[Blk<TYPE>::kQdw];
             unit_block<TYPE>(w, j, dbits, qs);
-            pr[j] = make_float2(h2f(dbits), f32act_block_sum<TYPE>(qs, xg + j * 32));
+            pr[j] = make_float2(Blk<TYPE>::scale(dbits), f32act_block_sum<TYPE>(qs, xg + j * 32));
         }
         // lane u's value is final from stage u on; after upr stages the last
         // lane of each row holds the in-order chain
@@ -473,6 +500,14 @@ __global__ __launch_bounds__(256) void gemv_f32act_persistent_q4_0(
 __global__ __launch_bounds__(256) void gemv_f32act_persistent_q8_0(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
     gemv_f32act_persistent<kQ8_0, 4>(W, x, y, N, nb, ntiles);
+}
+__global__ __launch_bounds__(256) void gemv_f32act_persistent_nq4_0(
+    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
+    gemv_f32act_persistent<kNQ4_0, 4>(W, x, y, N, nb, ntiles);
+}
+__global__ __launch_bounds__(256) void gemv_f32act_persistent_nq8_0(
+    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
+    gemv_f32act_persistent<kNQ8_0, 4>(W, x, y, N, nb, ntiles);
 }
 
 // The same numerics for K % 256 == 0 with the work spread over lanes: lane
@@ -879,10 +914,15 @@ static hipError_t launch_f32act_any(const uint8_t* W, const float* x, float* y, 
         const int ntiles = static_cast<int>((rows + tr - 1) / tr);
         const int waves = std::min(ntiles, cus * 16);
         const size_t lds = static_cast<size_t>(nb / 8) * kXPitchF * 4;
+        const int g = (waves + 3) / 4, n = static_cast<int>(rows);
         if constexpr (TYPE == kQ4_0)
-            gemv_f32act_persistent_q4_0<<<(waves + 3) / 4, 256, lds, st>>>(W, x, y, static_cast<int>(rows), nb, ntiles);
+            gemv_f32act_persistent_q4_0<<<g, 256, lds, st>>>(W, x, y, n, nb, ntiles);
+        else if constexpr (TYPE == kQ8_0)
+            gemv_f32act_persistent_q8_0<<<g, 256, lds, st>>>(W, x, y, n, nb, ntiles);
+        else if constexpr (TYPE == kNQ4_0)
+            gemv_f32act_persistent_nq4_0<<<g, 256, lds, st>>>(W, x, y, n, nb, ntiles);
         else
-            gemv_f32act_persistent_q8_0<<<(waves + 3) / 4, 256, lds, st>>>(W, x, y, static_cast<int>(rows), nb, ntiles);
+            gemv_f32act_persistent_nq8_0<<<g, 256, lds, st>>>(W, x, y, n, nb, ntiles);
         return hipGetLastError();
     }
     return launch_f32act<TYPE>(W, x, y, rows, cols, batch, st);
@@ -896,6 +936,16 @@ hipError_t launch_gemv_q8_0(const uint8_t* W, const float* x, float* y, size_t r
 hipError_t launch_gemv_q4_0_f32act(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                                    hipStream_t st) {
     return launch_f32act_any<kQ4_0>(W, x, y, rows, cols, batch, st);
+}
+
+// dot_q4_0 / dot_q8_0 of the native blocks (src/quant.cpp:87-156): the same
+// eight-lane block sums and in-order sum = fma(s, d, sum) as dot_q4_0_fp32 /
+// dot_q8_0_fp32, over 20- / 36-byte blocks with an f32 scale.
+hipError_t launch_gemv_native_f32act(uint32_t type, const uint8_t* W, const float* x, float* y, size_t rows,
+                                     size_t cols, size_t batch, hipStream_t st) {
+    if (type == kNQ4_0) return launch_f32act_any<kNQ4_0>(W, x, y, rows, cols, batch, st);
+    if (type == kNQ8_0) return launch_f32act_any<kNQ8_0>(W, x, y, rows, cols, batch, st);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,

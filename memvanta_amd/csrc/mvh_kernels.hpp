@@ -4,8 +4,10 @@
 
 namespace mvh {
 
-// GGML type ids used on the device side.
-enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ6_K = 14 };
+// GGML type ids used on the device side, and the native (non-GGUF) block
+// formats of src/quant.cpp: BlockQ4_0 {float d; uint8 qs[16]} (20 bytes,
+// element 2i = low nibble of qs[i]) and BlockQ8_0 {float d; int8 qs[32]} (36 bytes).
+enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ6_K = 14, kNQ4_0 = 0x1002, kNQ8_0 = 0x1008 };
 
 // ---- activation quantization / conversions (mvh_quant.hip) ----
 // q_op: q in the prefill GEMM's operand order (q8_op_offset; cols % 256 == 0,
@@ -36,6 +38,17 @@ hipError_t launch_gemv_f16(const uint16_t* W, const float* x, float* y, size_t r
 bool gemv_q4_0_persistent_ok(size_t cols);
 hipError_t launch_gemv_q4_0_persistent(const uint8_t* W, const float* x, const int8_t* aq, const float* ad, float* y,
                                        size_t rows, size_t cols, hipStream_t st);
+// Native BlockQ4_0 x BlockQ8_0 (matvec_q4_q8, src/quant_kernels.cpp:68-76):
+// y[r] = dot_q4_q8(row r, xq); xq is rows' cols/32 BlockQ8_0 (36 bytes each,
+// 4-byte aligned).  Any cols % 32 == 0.
+hipError_t launch_matvec_q4q8_native(const uint8_t* W, const uint8_t* xq, float* y, size_t rows, size_t cols,
+                                     hipStream_t st);
+// Native-format fp32-activation dots, y[b*rows + r]: dot_q4_0 (type kNQ4_0,
+// matvec_q4_0 / matmul_q4_0_batch) and dot_q8_0 (kNQ8_0, matvec_q8_0)
+hipError_t launch_gemv_native_f32act(uint32_t type, const uint8_t* W, const float* x, float* y, size_t rows,
+                                     size_t cols, size_t batch, hipStream_t st);
+// quantize_q8_0 / quantize_q4_0 of n floats (n % 32 == 0) into native blocks
+hipError_t launch_quantize_native(uint32_t type, const float* x, uint8_t* out, size_t n, hipStream_t st);
 // dot_q4_0_fp32 per (row, token): y[b*rows + r]
 hipError_t launch_gemv_q4_0_f32act(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                                    hipStream_t st);

@@ -4,11 +4,18 @@ reference's operation order are compared bit for bit; the two places that
 add a double sum in a different order (Q6_K rows, the attention softmax
 denominator) are compared within 2 ulp and must be bit-identical on at least
 99.9% of the outputs."""
+import importlib.util
+import os
+
 import numpy as np
 import pytest
 
-from conftest import assert_bitexact, bits
+from conftest import ROOT, assert_bitexact, bits, golden
 from memvanta_amd import capi, synth
+
+_spec = importlib.util.spec_from_file_location("make_golden", os.path.join(ROOT, "tests", "golden", "make_golden.py"))
+mg = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(mg)
 
 pytestmark = pytest.mark.gpu
 
@@ -80,6 +87,23 @@ def test_quantize_q8_bitexact(ctx, oracle, m, k):
     assert q[0, 41] == 3 and q[0, 42] == -3 and q[0, 43] == 127 and d[0, 0] == 1.0
 
 
+def test_quantize_q8_overflow_edge(ctx, oracle):
+    """Scales whose reciprocal overflows or that underflow to 0: the device
+    converts the non-finite quotients as the reference's x86 lround does (-127),
+    in the quantizer and in the GEMV that quantizes its own input."""
+    g = golden("quant_edge.npz")
+    x = g["x"]
+    q, d = ctx.quantize_q8(x)
+    q_ref, d_ref = oracle.quantize_q8(x)
+    assert np.array_equal(q, q_ref)
+    assert_bitexact(d, d_ref, "edge scales")
+    w = np.ascontiguousarray(mg.probe_matrix(256))
+    t = ctx.upload("probe", synth.Q4_0, 256, 256, w)
+    for i in range(x.shape[0]):
+        assert_bitexact(ctx.matvec(t, x[i]), g["y"][i], f"edge probe {i}")
+    t.free()
+
+
 # ---------------------------------------------------------------- decode GEMV
 
 @pytest.mark.parametrize("k,n", SHAPES_7B + [(288, 768), (768, 288), (2048, 2048), (5632, 2048)])
@@ -90,6 +114,28 @@ def test_gemv_q4_0_bitexact(ctx, oracle, k, n):
     for rep in range(2):
         x = synth.activations(rng, 1, k)[0]
         assert_bitexact(ctx.matvec(t, x), oracle.matvec(w, synth.Q4_0, n, k, x), f"Q4_0 {k}->{n}")
+    t.free()
+
+
+# (K, N) over the persistent GEMV's tile shapes: NP passes of 64 lanes x TR rows
+# (K/256 units per row): 4096 -> NP1 TR4; 11008 -> NP3 TR4; 5632 -> NP2 TR5;
+# 2048 -> NP1 TR8; 16384 -> NP1 TR1;
+# 256 -> NP1 TR16; ragged last tiles, N < TR, and tile counts above the
+# resident wave count (two tiles in flight per wave) at N = 22016 / 32000.
+Q8_INPUT_SHAPES = [(4096, 4096), (11008, 4096), (5632, 2048), (2048, 1003), (16384, 37),
+                   (8192, 4099), (256, 130), (4096, 3), (4096, 22016), (4096, 32000), (11008, 12288)]
+
+
+@pytest.mark.parametrize("k,n", Q8_INPUT_SHAPES)
+def test_gemv_q4_0_prequantized_bitexact(ctx, oracle, k, n):
+    """The model's decode path: Q4_0 x an already quantized Q8 activation
+    (mvh_matvec_q8), against the oracle's tensor_matvec on the fp32 input."""
+    rng = np.random.default_rng(5 * k + n)
+    w = _w(rng, synth.Q4_0, n, k)
+    t = ctx.upload("blk.0.ffn_up.weight", synth.Q4_0, k, n, w)
+    x = synth.activations(rng, 1, k)[0]
+    q, d = oracle.quantize_q8(x)
+    assert_bitexact(ctx.matvec_q8(t, q, d), oracle.matvec(w, synth.Q4_0, n, k, x), f"Q4_0 x Q8 {k}->{n}")
     t.free()
 
 

@@ -117,6 +117,17 @@ def test_quantizer_probe_golden(oracle):
         assert_bitexact(oracle.matvec(w, synth.Q4_0, 256, 256, x[i]), y[i], f"probe {i}")
 
 
+def test_quantizer_overflow_edge_golden(oracle):
+    """Blocks whose scale's reciprocal overflows (or whose scale underflows to
+    0): the reference's x86 lround turns the non-finite quotients into -127."""
+    g = golden("quant_edge.npz")
+    w = mg.probe_matrix(256)
+    for i in range(g["x"].shape[0]):
+        assert_bitexact(oracle.matvec(w, synth.Q4_0, 256, 256, g["x"][i]), g["y"][i], f"edge probe {i}")
+    q, _ = oracle.quantize_q8(g["x"])
+    assert (q[0, :32] == -127).all()
+
+
 def test_quantizer_closed_form(oracle):
     g = golden("kernels.npz")
     x = g["probe__x"]
