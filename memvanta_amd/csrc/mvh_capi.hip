@@ -459,8 +459,8 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
     switch (w->type) {
         case MVH_TYPE_Q4_0: {
             if (cols % 32) return fail(MVH_E_SHAPE, "Q4_0 matrix row not block aligned: %s", w->name.c_str());
-            if (mvh::gemv_q4_0_persistent_ok(cols)) {  // quantization fused into the GEMV
-                MVH_HIP(mvh::launch_gemv_q4_0_persistent(W, static_cast<const float*>(xd), nullptr, nullptr, yd, rows,
+            if (mvh::gemv_q4_0_rows16_ok(cols)) {  // quantization fused into the GEMV
+                MVH_HIP(mvh::launch_gemv_q4_0_rows16(W, static_cast<const float*>(xd), nullptr, nullptr, yd, rows,
                                                          cols, c->stream));
                 break;
             }

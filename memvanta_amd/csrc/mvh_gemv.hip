@@ -832,7 +832,7 @@ int pick_rows_per_wg(size_t rows, size_t nb, size_t pair_budget) {
 
 hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows, size_t cols,
                             hipStream_t st) {
-    if (gemv_q4_0_persistent_ok(cols)) return launch_gemv_q4_0_persistent(W, nullptr, aq, ad, y, rows, cols, st);
+    if (gemv_q4_0_rows16_ok(cols)) return launch_gemv_q4_0_rows16(W, nullptr, aq, ad, y, rows, cols, st);
     static const int mode = [] {
         const char* e = getenv("MVH_GEMV_LOAD");
         return e ? atoi(e) : kLoadStaged;

@@ -33,11 +33,15 @@ hipError_t launch_gemv_f32(const float* W, const float* x, float* y, size_t rows
                            hipStream_t st);
 hipError_t launch_gemv_f16(const uint16_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                            hipStream_t st);
-// Persistent Q4_0 x Q8 GEMV (cols % 256 == 0): x != nullptr quantizes the fp32
-// input inside the kernel; otherwise aq (16-byte aligned) / ad are the Q8 input.
-bool gemv_q4_0_persistent_ok(size_t cols);
-hipError_t launch_gemv_q4_0_persistent(const uint8_t* W, const float* x, const int8_t* aq, const float* ad, float* y,
-                                       size_t rows, size_t cols, hipStream_t st);
+// Q4_0 x Q8 GEMV in 16-lane row groups (cols % 256 == 0, 256 <= cols <= 16384):
+// x != nullptr quantizes the fp32 input inside the kernel; otherwise aq
+// (16-byte aligned) / ad are the Q8 input.
+bool gemv_q4_0_rows16_ok(size_t cols);
+hipError_t launch_gemv_q4_0_rows16(const uint8_t* W, const float* x, const int8_t* aq, const float* ad, float* y,
+                                   size_t rows, size_t cols, hipStream_t st);
+// the same kernel over native BlockQ4_0 x BlockQ8_0 (xq 4-byte aligned)
+hipError_t launch_gemv_q4q8_native_rows16(const uint8_t* W, const uint8_t* xq, float* y, size_t rows, size_t cols,
+                                          hipStream_t st);
 // Native BlockQ4_0 x BlockQ8_0 (matvec_q4_q8, src/quant_kernels.cpp:68-76):
 // y[r] = dot_q4_q8(row r, xq); xq is rows' cols/32 BlockQ8_0 (36 bytes each,
 // 4-byte aligned).  Any cols % 32 == 0.

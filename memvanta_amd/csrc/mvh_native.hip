@@ -6,15 +6,11 @@
 //   BlockQ8_0 {float d; int8 qs[32]}   36 bytes
 // Here: the two quantizers (quantize_q8_0 / quantize_q4_0, src/quant.cpp:44-85)
 // and matvec_q4_q8 (src/quant_kernels.cpp:68-76) for any cols % 32 == 0; the
-// K % 256 == 0 shapes of matvec_q4_q8 run on the persistent Q4 x Q8 GEMV of
+// K % 256 == 0 shapes of matvec_q4_q8 run on the Q4 x Q8 GEMV of
 // mvh_gemv_q4.hip, the fp32-activation dots on the kernels of mvh_gemv.hip.
 #include "mvh_kernels.hpp"
 
 namespace mvh {
-
-bool gemv_q4q8_native_ok(size_t cols);
-hipError_t launch_gemv_q4q8_native(const uint8_t* W, const uint8_t* xq, float* y, size_t rows, size_t cols,
-                                   hipStream_t st);
 
 namespace {
 
@@ -117,7 +113,7 @@ hipError_t launch_quantize_native(uint32_t type, const float* x, uint8_t* out, s
 hipError_t launch_matvec_q4q8_native(const uint8_t* W, const uint8_t* xq, float* y, size_t rows, size_t cols,
                                      hipStream_t st) {
     if (!rows) return hipSuccess;
-    if (gemv_q4q8_native_ok(cols)) return launch_gemv_q4q8_native(W, xq, y, rows, cols, st);
+    if (gemv_q4_0_rows16_ok(cols)) return launch_gemv_q4q8_native_rows16(W, xq, y, rows, cols, st);
     const unsigned grid = static_cast<unsigned>((rows + kRowWaves - 1) / kRowWaves);
     q4q8_native_rows_kernel<<<grid, 64 * kRowWaves, 0, st>>>(W, xq, y, static_cast<int>(rows),
                                                              static_cast<int>(cols / 32));

@@ -285,8 +285,8 @@ void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const f
         case 2:
             if (q8) {
                 e = mvh::launch_gemv_q4_0(W, q8, q8d, y, w.rows, w.cols, stream_);
-            } else if (mvh::gemv_q4_0_persistent_ok(w.cols)) {
-                e = mvh::launch_gemv_q4_0_persistent(W, x, nullptr, nullptr, y, w.rows, w.cols, stream_);
+            } else if (mvh::gemv_q4_0_rows16_ok(w.cols)) {
+                e = mvh::launch_gemv_q4_0_rows16(W, x, nullptr, nullptr, y, w.rows, w.cols, stream_);
             } else {
                 e = mvh::launch_quantize_q8(x, q8s_, q8sd_, q8ss_, 1, w.cols, stream_);
                 if (e == hipSuccess) e = mvh::launch_gemv_q4_0(W, q8s_, q8sd_, y, w.rows, w.cols, stream_);

@@ -4,6 +4,14 @@ import sys
 import numpy as np
 import pytest
 
+# torch (device buffers in the GPU tests) bundles its own HIP runtime; it must
+# be loaded before libmemvanta_hip.so so that both resolve to one runtime.
+# Imported here, it is, however the tests are selected.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    torch = None
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
