@@ -130,6 +130,17 @@ int mvh_matmul_batch(mvh_context* ctx, const mvh_tensor* w, const float* x, floa
  * which tokens of a batch fall in the unblocked tail). */
 int mvh_matmul_batch_v06(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, size_t batch,
                          int act_mode, int ptr_kind);
+/* No counterpart in the reference: tensor_matmul_batch_v06 (same numerics, fallbacks and errors as
+ * mvh_matmul_batch_v06) for callers that cannot allocate device memory -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  x [batch][ne0] and y [batch][ne1] are device
+ * pointers; the call only enqueues on the context's stream and calls no hipMalloc / hipFree.  The FORCE_Q8
+ * Q4_0 branch quantizes into a static per-device array of MVH_NOALLOC_SCRATCH_BYTES (held by every device
+ * the library runs on until the process ends); a batch whose activations need more fails with MVH_E_RANGE
+ * (8 MiB covers 512 tokens at K = 11008).  Every call on one device shares that array: calls that overlap
+ * on one device (other streams, other contexts, other threads) race.  Not recorded by the kernel profiler. */
+#define MVH_NOALLOC_SCRATCH_BYTES (8u << 20)
+int mvh_matmul_batch_v06_noalloc(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, size_t batch,
+                                 int act_mode);
 /* tensor_read_row_f32 (embedding row) */
 int mvh_read_row_f32(mvh_context* ctx, const mvh_tensor* w, size_t row, float* out, int ptr_kind);
 /* fp32_to_fp16 (the reference's rounding, bit for bit) and the exact fp16_to_fp32 */

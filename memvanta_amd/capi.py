@@ -58,6 +58,7 @@ _SIGS = {
     "mvh_matvec_q8": (_int, [_vp, _vp, _vp, _vp, _vp, _int]),
     "mvh_matmul_batch": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
     "mvh_matmul_batch_v06": (_int, [_vp, _vp, _vp, _vp, _sz, _int, _int]),
+    "mvh_matmul_batch_v06_noalloc": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
     "mvh_read_row_f32": (_int, [_vp, _vp, _sz, _vp, _int]),
     "mvh_fp32_to_fp16": (_int, [_vp, _vp, _vp, _sz, _int]),
     "mvh_fp16_to_fp32": (_int, [_vp, _vp, _vp, _sz, _int]),
@@ -233,6 +234,11 @@ class Context:
             x = np.ascontiguousarray(x, np.float32)
             y = np.empty((b, w.ne1), np.float32)
         self._check(self.lib.mvh_matmul_batch_v06(self.h, w.h, _ptr(x), _ptr(y), b, act_mode, _kind(x, y)))
+        return y
+
+    def matmul_batch_v06_noalloc(self, w: "Tensor", x, y, act_mode: int = MVH_ACT_REF):
+        """mvh_matmul_batch_v06_noalloc: device x [batch][ne0] -> device y [batch][ne1], no device allocation."""
+        self._check(self.lib.mvh_matmul_batch_v06_noalloc(self.h, w.h, _ptr(x), _ptr(y), x.shape[0], act_mode))
         return y
 
     def read_row(self, w: "Tensor", row: int, out=None):

@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <mutex>
 #include <optional>
 #include <string>
 #include <vector>
@@ -51,10 +52,20 @@ struct mvh_kv_cache {
     size_t page_stride() const { return (page_bytes() + 255) / 256 * 256; }
 };
 
+// Scratch of mvh_matmul_batch_v06_noalloc (the Q8 activations of its
+// FORCE_Q8 Q4_0 branch): a fixed array in every device's copy of the code
+// object, never allocated or freed at run time.  Host code must not pass this
+// name to a kernel or copy: its device address comes from hipGetSymbolAddress,
+// looked up once per device when a context is created on it (g_scratch_dev).
+static __device__ __align__(256) uint8_t scratch[MVH_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_err;
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};  // device address of `scratch` on each device, once looked up
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -300,7 +311,20 @@ int mvh_device_count(int* count) {
 int mvh_context_create(int device, mvh_context** out) {
     if (!out) return fail(MVH_E_INVALID, "null out");
     *out = nullptr;
+    if (device < 0 || device >= kMaxDevices) return fail(MVH_E_INVALID, "device %d out of range", device);
     MVH_HIP(hipSetDevice(device));
+    {
+        // the no-allocation entry point's scratch: its address on this device
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_dev[device]) {
+            void* ptr = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !ptr)
+                return fail(MVH_E_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                            hipGetErrorString(e));
+            g_scratch_dev[device] = ptr;
+        }
+    }
     auto* c = new (std::nothrow) mvh_context;
     if (!c) return fail(MVH_E_NOMEM, "host allocation failed");
     c->device = device;
@@ -599,6 +623,34 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
     if (int rc = v06_device(c, w, xd, yd, batch, act_mode, a)) return rc;
     if (int rc = span.end()) return rc;
     return finish_out(c, y, yd, batch * rows * 4, kind);
+}
+
+int mvh_matmul_batch_v06_noalloc(mvh_context* c, const mvh_tensor* w, const float* x, float* y, size_t batch,
+                                 int act_mode) {
+    CHECK_CTX(c);
+    if (!w) return fail(MVH_E_INVALID, "null tensor");
+    if (act_mode != MVH_ACT_REF && act_mode != MVH_ACT_Q8) return fail(MVH_E_INVALID, "bad act_mode %d", act_mode);
+    if (is_native(w))
+        return fail(MVH_E_TYPE, "unsupported batch matrix tensor type %s: %s", type_name(w->type), w->name.c_str());
+    const size_t cols = w->ne0, rows = w->ne1;
+    if (!batch || !rows) return MVH_OK;
+    if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
+    // fallback conditions of src/gguf_kernels.cpp:263: tensor_matmul_batch's per-(token, row) dots
+    if (batch < 2 || (w->type != MVH_TYPE_Q4_0 && w->type != MVH_TYPE_Q8_0) || cols % 32)
+        return fp32_rows(c, w, x, y, batch, "batch matrix");
+    ActView a{};
+    if (act_mode == MVH_ACT_Q8 && w->type == MVH_TYPE_Q4_0) {
+        const size_t need = act_bytes(v06_act_rows(batch, cols), cols);
+        if (need > MVH_NOALLOC_SCRATCH_BYTES)
+            return fail(MVH_E_RANGE,
+                        "batch %zu x cols %zu needs %zu bytes of Q8 activation scratch, above the %u-byte static "
+                        "scratch of mvh_matmul_batch_v06_noalloc",
+                        batch, cols, need, static_cast<unsigned>(MVH_NOALLOC_SCRATCH_BYTES));
+        void* base = g_scratch_dev[c->device];  // looked up when the context was created
+        if (!base) return fail(MVH_E_DEVICE, "no scratch address for device %d", c->device);
+        a = act_carve(base, v06_act_rows(batch, cols), cols);
+    }
+    return v06_device(c, w, x, y, batch, act_mode, a);
 }
 
 int mvh_read_row_f32(mvh_context* c, const mvh_tensor* w, size_t row, float* out, int kind) {
