@@ -35,6 +35,7 @@
  *                         (the bytes it returns are copied to HBM once)
  *   mvh_model_*           LlamaModel               include/memvanta/llama_model.hpp:100-138,
  *                                                  src/llama_model.cpp:222-262 (device resident)
+ *   mvh_argmax            Sampler::sample (greedy) include/memvanta/llama_model.hpp:54-66, src/llama_model.cpp:60
  *   mvh_quantize_q8_0     quantize_q8_0            include/memvanta/quant.hpp:15, src/quant.cpp:44-62
  *   mvh_quantize_q4_0     quantize_q4_0            quant.hpp:16, src/quant.cpp:64-85
  *   mvh_matvec_q4_q8      matvec_q4_q8             quant.hpp:27, src/quant_kernels.cpp:68-76 (dot_q4_q8 :52-66)
@@ -143,6 +144,10 @@ int mvh_matmul_batch_v06_noalloc(mvh_context* ctx, const mvh_tensor* w, const fl
                                  int act_mode);
 /* tensor_read_row_f32 (embedding row) */
 int mvh_read_row_f32(mvh_context* ctx, const mvh_tensor* w, size_t row, float* out, int ptr_kind);
+/* greedy sampling, Sampler::sample with temperature <= 0 (src/llama_model.cpp:60): out[r] = the first index of
+ * the maximum of logits[r*n .. r*n+n) (std::max_element), for rows rows of NaN-free logits; n == 0 fails with
+ * "empty logits" */
+int mvh_argmax(mvh_context* ctx, const float* logits, size_t n, size_t rows, int* out, int ptr_kind);
 /* fp32_to_fp16 (the reference's rounding, bit for bit) and the exact fp16_to_fp32 */
 int mvh_fp32_to_fp16(mvh_context* ctx, const float* x, uint16_t* out, size_t n, int ptr_kind);
 int mvh_fp16_to_fp32(mvh_context* ctx, const uint16_t* h, float* out, size_t n, int ptr_kind);

@@ -60,6 +60,7 @@ _SIGS = {
     "mvh_matmul_batch_v06": (_int, [_vp, _vp, _vp, _vp, _sz, _int, _int]),
     "mvh_matmul_batch_v06_noalloc": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
     "mvh_read_row_f32": (_int, [_vp, _vp, _sz, _vp, _int]),
+    "mvh_argmax": (_int, [_vp, _vp, _sz, _sz, _vp, _int]),
     "mvh_fp32_to_fp16": (_int, [_vp, _vp, _vp, _sz, _int]),
     "mvh_fp16_to_fp32": (_int, [_vp, _vp, _vp, _sz, _int]),
     "mvh_kv_parse_type": (_int, [C.c_char_p, C.POINTER(_int)]),
@@ -245,6 +246,18 @@ class Context:
         if out is None:
             out = np.empty(w.ne0, np.float32)
         self._check(self.lib.mvh_read_row_f32(self.h, w.h, row, _ptr(out), _kind(out)))
+        return out
+
+    def argmax(self, logits, out=None):
+        """Greedy sampling per row (first index of the max) of [rows][n] logits."""
+        if out is None:
+            logits = np.ascontiguousarray(logits, np.float32)
+            rows = 1 if logits.ndim == 1 else logits.shape[0]
+            out = np.empty(rows, np.int32)
+        else:
+            rows = 1 if logits.dim() == 1 else logits.shape[0]
+        n = logits.shape[-1]
+        self._check(self.lib.mvh_argmax(self.h, _ptr(logits), n, rows, _ptr(out), _kind(logits, out)))
         return out
 
     def fp32_to_fp16(self, x, out=None):

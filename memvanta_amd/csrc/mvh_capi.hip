@@ -685,6 +685,23 @@ int mvh_fp32_to_fp16(mvh_context* c, const float* x, uint16_t* out, size_t n, in
     return finish_out(c, out, od, n * 2, kind);
 }
 
+int mvh_argmax(mvh_context* c, const float* logits, size_t n, size_t rows, int* out, int kind) {
+    CHECK_CTX(c);
+    if (!n) return fail(MVH_E_INVALID, "empty logits");  // Sampler::sample's check
+    if (!rows) return MVH_OK;
+    if (!logits || !out) return fail(MVH_E_INVALID, "null argument");
+    if (n > 0x7fffffff) return fail(MVH_E_RANGE, "logits row too long");
+    const void* ld = nullptr;
+    if (int rc = stage_in(c, c->xin, logits, rows * n * 4, kind, &ld)) return rc;
+    int* od = out;
+    if (kind == MVH_HOST) {
+        if (int rc = grow(c, c->yout, rows * 4)) return rc;
+        od = static_cast<int*>(c->yout.p);
+    }
+    MVH_HIP(mvh::launch_argmax(static_cast<const float*>(ld), n, rows, od, nullptr, nullptr, c->stream));
+    return finish_out(c, out, od, rows * 4, kind);
+}
+
 int mvh_fp16_to_fp32(mvh_context* c, const uint16_t* h, float* out, size_t n, int kind) {
     CHECK_CTX(c);
     if (!n) return MVH_OK;

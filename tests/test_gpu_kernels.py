@@ -117,11 +117,11 @@ def test_gemv_q4_0_bitexact(ctx, oracle, k, n):
     t.free()
 
 
-# (K, N) over the persistent GEMV's tile shapes: NP passes of 64 lanes x TR rows
-# (K/256 units per row): 4096 -> NP1 TR4; 11008 -> NP3 TR4; 5632 -> NP2 TR5;
-# 2048 -> NP1 TR8; 16384 -> NP1 TR1;
-# 256 -> NP1 TR16; ragged last tiles, N < TR, and tile counts above the
-# resident wave count (two tiles in flight per wave) at N = 22016 / 32000.
+# (K, N) over the row-group GEMV's pass shapes (passes of 16 units of 8
+# blocks; K / 256 units per row): 4096 -> 1 whole pass; 11008 -> 3 passes, the
+# last of 11 units; 5632 -> 2 passes (6 in the last); 2048 -> 1 pass of 8
+# units; 8192 -> 2; 16384 -> 4; 256 -> a single unit; N not a multiple of the
+# 4-row tile, N < 4, and grids larger than the resident wave count.
 Q8_INPUT_SHAPES = [(4096, 4096), (11008, 4096), (5632, 2048), (2048, 1003), (16384, 37),
                    (8192, 4099), (256, 130), (4096, 3), (4096, 22016), (4096, 32000), (11008, 12288)]
 
@@ -253,6 +253,45 @@ def test_prefill_gemm_int8_mfma_bitexact(ctx, oracle, batch, k, n):
     want = oracle.matmul_batch_v06(w, synth.Q4_0, n, k, x, is_ffn=True, force_q8=True)
     assert_bitexact(got, want, f"mfma gemm M={batch} K={k} N={n}")
     t.free()
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 11008), (11008, 4096)])
+@pytest.mark.parametrize("m", [128, 512])
+def test_prefill_gemm_config_shapes_bitexact(ctx, oracle, k, n, m):
+    """The batched-prefill GEMM config at its full sizes (M = 128 / 512 on the
+    7B FFN and attention shapes): the 32-token tile instances the bench times,
+    against the FORCE_Q8 reference chain of every (row, token)."""
+    rng = np.random.default_rng(m + 3 * k + n)
+    w = _w(rng, synth.Q4_0, n, k)
+    t = ctx.upload("blk.0.ffn_up.weight", synth.Q4_0, k, n, w)
+    x = synth.activations(rng, m, k)
+    got = ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8)
+    want = oracle.matmul_batch_v06(w, synth.Q4_0, n, k, x, is_ffn=True, force_q8=True, threads=16)
+    assert_bitexact(got, want, f"mfma gemm M={m} K={k} N={n}")
+    t.free()
+
+
+def test_argmax_first_index_of_max(ctx):
+    """Greedy sampling = std::max_element (src/llama_model.cpp:60): ties go to
+    the first index, at any distance and in any row."""
+    rng = np.random.default_rng(31)
+    V = 32000
+    rows = rng.standard_normal((8, V), dtype=np.float32)
+    rows[0, [17, 9000, 31999]] = 50.0           # a tie across three threads
+    rows[1, :] = 1.25                            # every element equal -> 0
+    rows[2, :] = -np.inf                         # all -inf -> 0
+    rows[3, 31999] = 99.0                        # max at the last index
+    rows[4, [1023, 1024, 2047]] = 7.0            # ties straddling the 1024-lane stride
+    rows[5, [5, 4]] = 9.0                        # adjacent tie
+    rows[6, 0] = 12.0                            # max at index 0
+    rows[7, [30000, 100]] = np.float32(3.0e38)   # the largest finite values
+    got = ctx.argmax(rows)
+    assert got.tolist() == [int(np.argmax(r)) for r in rows] == [17, 0, 0, 31999, 1023, 4, 0, 100]
+    for n in (1, 2, 63, 1025):
+        r = rng.standard_normal(n).astype(np.float32)
+        assert int(ctx.argmax(r)[0]) == int(np.argmax(r))
+    with pytest.raises(capi.MvhError, match="empty logits"):
+        ctx.argmax(np.zeros((1, 0), np.float32))
 
 
 @pytest.mark.parametrize("ty,k", [(synth.Q4_0, 288), (synth.Q8_0, 1024), (synth.Q6_K, 512)])

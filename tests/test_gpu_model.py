@@ -142,6 +142,38 @@ def test_prefill_ragged_chunks_vs_oracle(tmp_path, oracle, max_batch, chunk):
 KV_TYPES = {"f32": capi.MVH_KV_F32, "q8": capi.MVH_KV_Q8}
 
 
+@pytest.mark.parametrize("cfg_name,mode", [("openllama-7b-v2-q4_0", 1), ("tinyllama-1.1b-mixed", 0),
+                                           ("tinyllama-1.1b-mixed", 1)])
+def test_full_depth_greedy_vs_oracle(tmp_path, oracle, cfg_name, mode):
+    """Whole models at their full depth (the 32-layer OpenLLaMA-7B-v2 shape,
+    the 22-layer TinyLlama-1.1B mixed shape) against the oracle: an 8-token
+    prompt prefilled in one chunk, then 8 greedy decode steps on the device
+    (the captured-graph loop) and on the host restatement.  Greedy ids must be
+    identical; every step's logits within 1e-3 relative L2."""
+    cfg = synth.CONFIGS[cfg_name]
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=41, device="cuda", digest=False)
+    prompt = synth.prompt_tokens(13, 8)
+    mo = oracle.model(path, ctx=256, force_q8=bool(mode), threads=16)
+    m = capi.Model(path, ctx=256, act_mode=mode, max_batch=32)
+    want = mo.prefill(prompt, 32)
+    close(m.prefill(prompt, 32), want, f"{cfg_name} prefill")
+    ids_ref, cur = [], int(np.argmax(want))
+    for _ in range(8):
+        ids_ref.append(cur)
+        lg = mo.forward(cur)
+        got = m.forward(cur)
+        close(got, lg, f"{cfg_name} decode")
+        cur = int(np.argmax(lg))
+    ids_ref.append(cur)
+    # the device loop from the same state: reset, prefill, generate
+    m.reset()
+    m.prefill(prompt, 32, logits=False)
+    assert m.generate_greedy(ids_ref[0], 8).tolist() == ids_ref[1:]
+    m.close()
+    mo.close()
+
+
 @pytest.fixture(scope="module")
 def gqa(tmp_path_factory):
     """The 2-layer TinyLlama-shape mixed model of the GQA golden (32 heads, 4 KV heads)."""
