@@ -142,8 +142,14 @@ int mvh_matmul_batch_v06(mvh_context* ctx, const mvh_tensor* w, const float* x, 
 #define MVH_NOALLOC_SCRATCH_BYTES (8u << 20)
 int mvh_matmul_batch_v06_noalloc(mvh_context* ctx, const mvh_tensor* w, const float* x, float* y, size_t batch,
                                  int act_mode);
-/* tensor_read_row_f32 (embedding row) */
-int mvh_read_row_f32(mvh_context* ctx, const mvh_tensor* w, size_t row, float* out, int ptr_kind);
+/* tensor_read_row_f32 (embedding row): out[cols] = row `row` of w; cols must equal ne0 and row < ne1, else
+ * MVH_E_RANGE with the reference's "tensor row shape mismatch: <name>" */
+int mvh_read_row_f32(mvh_context* ctx, const mvh_tensor* w, size_t row, float* out, size_t cols, int ptr_kind);
+/* No counterpart in the reference (a measurement probe): reads the bytes (a multiple of 16, 16-byte aligned)
+ * of the device buffer buf once with coalesced 16-byte loads on the context's stream.  sink is a device
+ * buffer of sink_words words (>= 256 x 8 x the CU count) that receives nothing in practice.  Timed on a
+ * buffer larger than the 256 MB Infinity Cache it gives the device's streaming-read bandwidth. */
+int mvh_stream_read(mvh_context* ctx, const void* buf, size_t bytes, uint32_t* sink, size_t sink_words);
 /* greedy sampling, Sampler::sample with temperature <= 0 (src/llama_model.cpp:60): out[r] = the first index of
  * the maximum of logits[r*n .. r*n+n) (std::max_element), for rows rows of NaN-free logits; n == 0 fails with
  * "empty logits" */

@@ -51,6 +51,9 @@ def build_oracle(with_ref: bool | None = None) -> None:
     if with_ref:
         targets.append("ref")
     _run(["make", "-C", os.path.join(ROOT, "oracle"), "-j4", *targets])
+    if with_ref and os.path.exists(LIB):
+        # the reference-side integration check (INTEGRATION.md's shim, compiled as printed)
+        _run([sys.executable, os.path.join(ROOT, "oracle", "shim_build.py")])
 
 
 if __name__ == "__main__":

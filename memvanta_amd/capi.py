@@ -9,6 +9,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 import re
+import sys
 
 import numpy as np
 
@@ -59,8 +60,9 @@ _SIGS = {
     "mvh_matmul_batch": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
     "mvh_matmul_batch_v06": (_int, [_vp, _vp, _vp, _vp, _sz, _int, _int]),
     "mvh_matmul_batch_v06_noalloc": (_int, [_vp, _vp, _vp, _vp, _sz, _int]),
-    "mvh_read_row_f32": (_int, [_vp, _vp, _sz, _vp, _int]),
+    "mvh_read_row_f32": (_int, [_vp, _vp, _sz, _vp, _sz, _int]),
     "mvh_argmax": (_int, [_vp, _vp, _sz, _sz, _vp, _int]),
+    "mvh_stream_read": (_int, [_vp, _vp, _sz, _vp, _sz]),
     "mvh_fp32_to_fp16": (_int, [_vp, _vp, _vp, _sz, _int]),
     "mvh_fp16_to_fp32": (_int, [_vp, _vp, _vp, _sz, _int]),
     "mvh_kv_parse_type": (_int, [C.c_char_p, C.POINTER(_int)]),
@@ -105,6 +107,22 @@ class ProfileEntry(C.Structure):
                 ("batch", C.c_size_t), ("ms", C.c_double)]
 
 _lib = None
+
+
+def _finalize(release) -> None:
+    """Release a handle from __del__, except while the interpreter is finalizing.
+
+    At interpreter exit the HIP runtime (torch's and this library's) may already
+    be tearing down its device state; a hipFree / hipStreamDestroy issued then
+    from a garbage-collected handle can touch freed runtime structures.  The
+    process is ending and the driver reclaims every allocation, so the handle
+    is left alone.  Explicit close()/free() calls are unaffected."""
+    if sys.is_finalizing():
+        return
+    try:
+        release()
+    except Exception:
+        pass
 
 
 def load_library(path: str = LIB_PATH) -> C.CDLL:
@@ -163,10 +181,7 @@ class Context:
             self.h = None
 
     def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+        _finalize(self.close)
 
     @property
     def stream(self) -> int:
@@ -242,11 +257,17 @@ class Context:
         self._check(self.lib.mvh_matmul_batch_v06_noalloc(self.h, w.h, _ptr(x), _ptr(y), x.shape[0], act_mode))
         return y
 
-    def read_row(self, w: "Tensor", row: int, out=None):
+    def read_row(self, w: "Tensor", row: int, out=None, cols: int | None = None):
+        """tensor_read_row_f32: row `row` of w as fp32 (cols defaults to ne0)."""
+        cols = w.ne0 if cols is None else cols
         if out is None:
-            out = np.empty(w.ne0, np.float32)
-        self._check(self.lib.mvh_read_row_f32(self.h, w.h, row, _ptr(out), _kind(out)))
+            out = np.empty(cols, np.float32)
+        self._check(self.lib.mvh_read_row_f32(self.h, w.h, row, _ptr(out), cols, _kind(out)))
         return out
+
+    def stream_read(self, buf, nbytes: int, sink, sink_words: int):
+        """Enqueue the streaming-read probe over nbytes of device buffer buf (device sink of sink_words words)."""
+        self._check(self.lib.mvh_stream_read(self.h, _ptr(buf), nbytes, _ptr(sink), sink_words))
 
     def argmax(self, logits, out=None):
         """Greedy sampling per row (first index of the max) of [rows][n] logits."""
@@ -326,10 +347,7 @@ class Tensor:
             self.h = None
 
     def __del__(self):
-        try:
-            self.free()
-        except Exception:
-            pass
+        _finalize(self.free)
 
     def info(self):
         ty, n0, n1, nb, dp = _u32(), _u64(), _u64(), _u64(), _vp()
@@ -394,7 +412,8 @@ class KVCache:
             self.ctx.lib.mvh_kv_destroy(self.h)
             self.h = None
 
-    __del__ = close
+    def __del__(self):
+        _finalize(self.close)
 
     def reset(self):
         self.ctx._check(self.ctx.lib.mvh_kv_reset(self.h))
@@ -468,7 +487,8 @@ class Model:
             self.lib.mvh_model_close(self.h)
             self.h = None
 
-    __del__ = close
+    def __del__(self):
+        _finalize(self.close)
 
     def reset(self):
         self._check(self.lib.mvh_model_reset(self.h))

@@ -653,12 +653,13 @@ int mvh_matmul_batch_v06_noalloc(mvh_context* c, const mvh_tensor* w, const floa
     return v06_device(c, w, x, y, batch, act_mode, a);
 }
 
-int mvh_read_row_f32(mvh_context* c, const mvh_tensor* w, size_t row, float* out, int kind) {
+int mvh_read_row_f32(mvh_context* c, const mvh_tensor* w, size_t row, float* out, size_t cols, int kind) {
     CHECK_CTX(c);
     if (!w || !out) return fail(MVH_E_INVALID, "null argument");
+    // the reference checks the shape first (src/gguf_kernels.cpp:226), then the type
+    if (cols != w->ne0 || row >= w->ne1) return fail(MVH_E_RANGE, "tensor row shape mismatch: %s", w->name.c_str());
     if (is_native(w))
         return fail(MVH_E_TYPE, "unsupported embedding tensor type %s: %s", type_name(w->type), w->name.c_str());
-    if (row >= w->ne1) return fail(MVH_E_RANGE, "tensor row shape mismatch: %s", w->name.c_str());
     if (w->type == MVH_TYPE_Q6_K && w->ne0 % 256)
         return fail(MVH_E_SHAPE, "Q6_K embedding row not block aligned: %s", w->name.c_str());
     float* od = out;
@@ -683,6 +684,15 @@ int mvh_fp32_to_fp16(mvh_context* c, const float* x, uint16_t* out, size_t n, in
     }
     MVH_HIP(mvh::launch_f2h(static_cast<const float*>(xd), od, n, c->stream));
     return finish_out(c, out, od, n * 2, kind);
+}
+
+int mvh_stream_read(mvh_context* c, const void* buf, size_t bytes, uint32_t* sink, size_t sink_words) {
+    CHECK_CTX(c);
+    if (!buf || !sink) return fail(MVH_E_INVALID, "null argument");
+    if (bytes % 16 || (reinterpret_cast<uintptr_t>(buf) & 15))
+        return fail(MVH_E_INVALID, "buffer must be 16-byte aligned and a multiple of 16 bytes");
+    MVH_HIP(mvh::launch_stream_read(buf, bytes, sink, sink_words, c->stream));
+    return MVH_OK;
 }
 
 int mvh_argmax(mvh_context* c, const float* logits, size_t n, size_t rows, int* out, int kind) {

@@ -2,6 +2,8 @@
 #pragma once
 #include "mvh_device.hpp"
 
+#include <algorithm>
+
 namespace mvh {
 
 // GGML type ids used on the device side, and the native (non-GGUF) block
@@ -104,6 +106,11 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
 hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
                               float* scores, float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd,
                               size_t kv_dim, size_t page_tokens, hipStream_t st);
+
+// ---- measurement probe (mvh_probe.hip) ----
+// reads bytes (a multiple of 16) of buf once; sink holds sink_words words (at
+// least 256 x the grid: 8 workgroups per CU)
+hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, size_t sink_words, hipStream_t st);
 
 // ---- model step pieces (mvh_model.hip) ----
 hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int* tokens, size_t B, float* out,

@@ -294,6 +294,43 @@ def test_argmax_first_index_of_max(ctx):
         ctx.argmax(np.zeros((1, 0), np.float32))
 
 
+def test_handles_outlive_their_context(oracle):
+    """A tensor or KV cache freed after the context that created it was
+    destroyed touches only its own device and memory (freeing once
+    dereferenced the destroyed context: a use-after-free at process exit when
+    a caller closed the context first); the tensor stays usable from another
+    context on the same device."""
+    rng = np.random.default_rng(404)
+    k, n = 4096, 1003
+    w = _w(rng, synth.Q4_0, n, k)
+    c1 = capi.Context(0)
+    t = c1.upload("blk.0.attn_q.weight", synth.Q4_0, k, n, w)
+    kv = c1.kv_cache(2, 256, 128, 512)
+    c1.close()
+    c2 = capi.Context(0)
+    try:
+        x = synth.activations(rng, 1, k)[0]
+        assert_bitexact(c2.matvec(t, x), oracle.matvec(w, synth.Q4_0, n, k, x), "tensor after its context closed")
+        kv.close()
+        t.free()
+    finally:
+        c2.close()
+
+
+def test_stream_read_probe_arguments(ctx):
+    import torch
+
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device="cuda")
+    ctx.stream_read(buf, buf.numel(), sink, sink.numel())
+    ctx.synchronize()
+    assert int(sink.abs().sum()) == 0  # zeros never produce the sink's trigger value
+    with pytest.raises(capi.MvhError, match="multiple of 16"):
+        ctx.stream_read(buf, 1000, sink, sink.numel())
+    with pytest.raises(capi.MvhError):
+        ctx.stream_read(buf, buf.numel(), sink, 16)  # sink smaller than one workgroup's words
+
+
 @pytest.mark.parametrize("ty,k", [(synth.Q4_0, 288), (synth.Q8_0, 1024), (synth.Q6_K, 512)])
 def test_matmul_batch_fallback(ctx, oracle, ty, k):
     rng = np.random.default_rng(k + ty)
@@ -322,6 +359,8 @@ def test_read_row(ctx, oracle, ty, k):
         assert_bitexact(ctx.read_row(t, row), oracle.read_row(w, ty, n, k, row), f"row {row}")
     with pytest.raises(capi.MvhError, match="tensor row shape mismatch"):
         ctx.read_row(t, n)
+    with pytest.raises(capi.MvhError, match="tensor row shape mismatch: token_embd.weight"):
+        ctx.read_row(t, 0, out=np.empty(k + 32, np.float32), cols=k + 32)  # cols != ne0
     t.free()
 
 
