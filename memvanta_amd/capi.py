@@ -109,15 +109,17 @@ class ProfileEntry(C.Structure):
 _lib = None
 
 
-def _finalize(release) -> None:
+def _finalize(release, _finalizing=sys.is_finalizing) -> None:
     """Release a handle from __del__, except while the interpreter is finalizing.
 
     At interpreter exit the HIP runtime (torch's and this library's) may already
     be tearing down its device state; a hipFree / hipStreamDestroy issued then
     from a garbage-collected handle can touch freed runtime structures.  The
     process is ending and the driver reclaims every allocation, so the handle
-    is left alone.  Explicit close()/free() calls are unaffected."""
-    if sys.is_finalizing():
+    is left alone.  Explicit close()/free() calls are unaffected.  The
+    finalizing test and this function are bound as default arguments: module
+    globals may already be cleared when a late __del__ runs."""
+    if _finalizing():
         return
     try:
         release()
@@ -131,6 +133,15 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         return _lib
     if not os.path.exists(path):
         raise FileNotFoundError(f"HIP backend not built: {path} is missing (run __graft_entry__.build())")
+    # One HIP runtime per process: PyTorch ships its own libamdhip64.  Loaded
+    # first, it also serves this library (same soname); loaded after this
+    # library had brought in the system runtime, torch finds no device.  So
+    # when torch is installed it is imported before the library is opened.
+    if "torch" not in sys.modules:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
     lib = C.CDLL(path)
     for name, (res, args) in _SIGS.items():
         f = getattr(lib, name)
@@ -180,8 +191,8 @@ class Context:
             self.lib.mvh_context_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self.close)
+    def __del__(self, _fin=_finalize):
+        _fin(self.close)
 
     @property
     def stream(self) -> int:
@@ -346,8 +357,8 @@ class Tensor:
             self.ctx.lib.mvh_tensor_free(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self.free)
+    def __del__(self, _fin=_finalize):
+        _fin(self.free)
 
     def info(self):
         ty, n0, n1, nb, dp = _u32(), _u64(), _u64(), _u64(), _vp()
@@ -412,8 +423,8 @@ class KVCache:
             self.ctx.lib.mvh_kv_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self.close)
+    def __del__(self, _fin=_finalize):
+        _fin(self.close)
 
     def reset(self):
         self.ctx._check(self.ctx.lib.mvh_kv_reset(self.h))
@@ -487,8 +498,8 @@ class Model:
             self.lib.mvh_model_close(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self.close)
+    def __del__(self, _fin=_finalize):
+        _fin(self.close)
 
     def reset(self):
         self._check(self.lib.mvh_model_reset(self.h))

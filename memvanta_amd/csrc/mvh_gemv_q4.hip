@@ -18,8 +18,9 @@
 // (p_b, f_b) pairs in registers, then the rows' fma chains walk the group's
 // lanes in unit order (DPP row_ror:1: at each stage a lane continues from its
 // left neighbour's value; lane 0 starts a pass from lane 15's value at the end
-// of the previous pass).  A pass's chain runs while the next pass's units are
-// still arriving; only the last pass's stages follow the last byte.
+// of the previous pass).  Pass p + 1's loads are issued just before pass p is
+// computed, so a pass's chain runs while the next pass's units are still
+// arriving; only the last pass's stages follow the last byte.
 //
 // The activation (Q8 bytes, per-block scale and byte sum) is staged once per
 // workgroup of 4 waves in LDS.  Its global loads are issued before the weight
@@ -144,12 +145,16 @@ __global__ __launch_bounds__(256) void gemv_q4_rows16(const uint8_t* W, const vo
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. the tile's weight units, pass by pass (every load unconditional: rows
-    // past N and units past the row reload the last valid ones)
+    // 2. the tile's weight units of the first pass (every load unconditional:
+    // rows past N and units past the row reload the last valid ones); pass
+    // p + 1 is issued just before pass p is computed, so a wave reaches the
+    // staging barrier after issuing one pass, not all of them (a wave stalls at
+    // the issue of a load while the memory system holds too many of its
+    // requests, and its chain could then only start once nearly all of its
+    // bytes had arrived)
     uint32_t w[NP][kW];
     const int grow_c = min(min(tile, ntiles - 1) * 4 + r, N - 1);
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
+    auto issue = [&](int p) {
         const int u = min(16 * p + g, upr - 1);
         const uint4* src = reinterpret_cast<const uint4*>(W + static_cast<size_t>(grow_c) * row_bytes +
                                                           static_cast<size_t>(u) * 8 * F::kBytes);
@@ -162,7 +167,8 @@ __global__ __launch_bounds__(256) void gemv_q4_rows16(const uint8_t* W, const vo
             w[p][4 * k + 3] = v.w;
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the passes' loads in K order
-    }
+    };
+    issue(0);
 
     // 3. the activation into LDS: Q8 bytes, then (d, byte sum) per block
     if constexpr (SRC == kSrcQ8) {
@@ -217,11 +223,12 @@ __global__ __launch_bounds__(256) void gemv_q4_rows16(const uint8_t* W, const vo
     }
     __syncthreads();
 
-    // 4. pass by pass: pairs in registers, then the chain stages
+    // 4. pass by pass: the next pass's loads, pairs in registers, then the chain stages
     float sum = 0.0f;
     int last = 15;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
+        if (p + 1 < NP) issue(p + 1);
         const int uu = min(16 * p + g, upr - 1);
         const uint8_t* ag = s_aq + uu * kActPitch;
         const uint8_t* dg = s_das + uu * kDasPitch;
@@ -249,6 +256,7 @@ __global__ __launch_bounds__(256) void gemv_q4_rows16(const uint8_t* W, const vo
             sum = acc;
         }
         last = ng - 1;
+        if (NP > 1) __builtin_amdgcn_sched_barrier(0);  // the next pass's loads stay ahead of its pairs
     }
     const int grow = tile * 4 + r;
     if (tile < ntiles && grow < N && g == last) y[grow] = sum;
