@@ -245,8 +245,10 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
 
 // ---- fused decode attention --------------------------------------------------
 //
-// One decode token, one launch.  Workgroup (head h, slice j) owns output
-// elements [j*SW, (j+1)*SW) of head h:
+// One decode token, one launch, for the model's preallocated F16 KV slab (page
+// p of a layer at kbase / vbase + p * page_stride: rows are addressed without a
+// page-table load).  Workgroup (head h, slice j) owns output elements
+// [j*SW, (j+1)*SW) of head h:
 //  1. RoPE of q (head h) and k (kv head h/group) at position p = *d_pos
 //     (LlamaModel::rope_ptr numerics), k and v rounded through the
 //     reference's fp32_to_fp16; the first workgroup of each kv head writes
@@ -261,26 +263,29 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
 //     global loads of round r+1 are in flight while round r is summed);
 //  5. with SW == 32 the slice is one Q8 block of the output: quantize_q8 of
 //     it (the o-projection's activation) is written beside it.
-// Memory round trips on the critical path: (position, page tables, q/k/v)
-// then (cos/sin, the first K row of each thread, V round 0), all issued
-// together.  The scores are recomputed by every slice of a head (K is read
-// from L2).
+// One memory round trip on the critical path: the position, q/k/v, the
+// RoPE row of the position (copied to a fixed buffer by the token's embedding
+// launch), the first K row of each thread (row t) and V round 0 (rows
+// 0..kRV-1) are all issued together, none of their addresses depending on the
+// position (rows past the position are read and ignored; at positions below
+// kAT that is the price of not waiting for the position first).  Later K rows
+// and V rounds follow the position.  The scores are recomputed by every slice
+// of a head (K is read from L2).
 constexpr int kAT = 256;
-constexpr int kRV = 512;        // V rows per staging round
-constexpr int kRVP = kRV + 8;   // LDS pitch of a transposed V dimension: 1040 bytes, so the
-                                // lanes' 16-byte row reads fall in different banks (at 1024
-                                // bytes all 32 lanes hit one bank)
-constexpr int kMaxPages = 128;  // page-table entries staged in LDS
+constexpr int kRV = 256;        // V rows per staging round
+constexpr int kRVP = kRV + 8;   // LDS pitch of a transposed V dimension: 528 bytes (132
+                                // dwords, 4 mod 32), so the lanes' 16-byte row reads fall in
+                                // different banks (at a multiple of 128 bytes they collide)
+constexpr int kMaxPages = 128;  // KV pages a context may span
 
 // HD != 0 fixes head_dim at compile time (the loops over it unroll and the
 // LDS reads of q are scheduled ahead of their use); HD == 0 reads hd_arg.
 template <int SW, int HD>
 __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int* __restrict__ d_pos,
-    uint16_t* const* __restrict__ pt_k, uint16_t* const* __restrict__ pt_v, int page_tokens, int max_pages,
-    float* __restrict__ out, int8_t* __restrict__ q8, float* __restrict__ q8d, int group, int hd_arg, int kv_dim,
-    int ctx_pad, int nslice) {
+    const float* __restrict__ rope, const int* __restrict__ d_pos, uint16_t* kbase, uint16_t* vbase,
+    int page_tokens, size_t page_stride, int rows_alloc, float* __restrict__ out, int8_t* __restrict__ q8,
+    float* __restrict__ q8d, int group, int hd_arg, int kv_dim, int ctx_pad, int nslice) {
     const int hd = HD ? HD : hd_arg;
     constexpr int kCh = SW / 8;                        // 16-byte chunks per V row slice
     constexpr int kVPT = (kRV * kCh + kAT - 1) / kAT;  // chunks per thread per round
@@ -293,41 +298,35 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     __shared__ float red_f[kAT / 64];
     __shared__ double red_d[kAT / 64];
     __shared__ uint64_t s_tab[32];
-    __shared__ uint16_t* s_pk[kMaxPages];
-    __shared__ uint16_t* s_pv[kMaxPages];
 
     const int h = blockIdx.x / nslice, slice = blockIdx.x - h * nslice;
     const int kh = h / group, t = threadIdx.x, half = hd >> 1;
     const int dbase = slice * SW;
+    auto krow_of = [&](int tt) {
+        return kbase + static_cast<size_t>(tt / page_tokens) * page_stride + static_cast<size_t>(tt % page_tokens) * kv_dim +
+               kh * hd;
+    };
+    auto vrow_of = [&](int tt) {
+        return vbase + static_cast<size_t>(tt / page_tokens) * page_stride + static_cast<size_t>(tt % page_tokens) * kv_dim +
+               kh * hd;
+    };
 
-    // round trip 1: position, page tables, q/k/v of this token
+    // The one round trip: position, q/k/v, the RoPE row, row t of K, V round
+    // 0.  Every load is unconditional (threads without a use read an in-bounds
+    // element and ignore it) and issued in this order (the scheduling
+    // barriers keep it): vector loads complete in issue order, so RoPE waits
+    // for q/k/v and the RoPE row alone while the K rows and V are in flight (a
+    // load under a branch makes the compiler's wait cover all of them).
     const int pos = *d_pos;
-    for (int i = t; i < max_pages; i += kAT) {
-        s_pk[i] = pt_k[i];
-        s_pv[i] = pt_v[i];
-    }
     if (t < 32) s_tab[t] = mvh_expf_tab(t);
-    // Every global load of round trips 1 and 2 is unconditional (threads
-    // without a use read an in-bounds element and ignore it): the compiler's
-    // wait counts then let RoPE wait for cos/sin alone while the K rows and
-    // V round 0 are still in flight (a load under a branch makes it wait for
-    // all of them).
     const int th = t < half ? t : 0;
     const float* qh = q + static_cast<size_t>(h) * hd;
     const float* kk = k + static_cast<size_t>(kh) * hd;
     const float* vv = v + static_cast<size_t>(kh) * hd;
     const float q0 = qh[th], q1 = qh[th + half], k0 = kk[th], k1 = kk[th + half], v0 = vv[th], v1 = vv[th + half];
-    __syncthreads();
-
-    // round trip 2: cos/sin, this thread's first K row, V round 0 -- issued
-    // in that order (the scheduling barriers keep it), so RoPE waits for the
-    // first two loads only
-    const float cs = cos_t[static_cast<size_t>(pos) * half + th];
-    const float sn = sin_t[static_cast<size_t>(pos) * half + th];
+    const float cs = rope[th];
+    const float sn = rope[half + th];
     __builtin_amdgcn_sched_barrier(0);
-    auto krow_of = [&](int tt) {
-        return s_pk[tt / page_tokens] + static_cast<size_t>(tt % page_tokens) * kv_dim + kh * hd;
-    };
     uint4 kv[16];
     auto load_k = [&](int tt, int c0) {
         const uint16_t* kr = krow_of(tt) + c0;
@@ -335,20 +334,18 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
         for (int j = 0; j < 16; ++j)
             if (c0 + 8 * j < hd) kv[j] = ld_global16(kr + 8 * j);
     };
-    load_k(t < pos ? t : 0, 0);  // rows past pos: row 0 (written, unused)
+    load_k(min(t, rows_alloc - 1), 0);  // rows at or past pos: read, unused
     uint4 vr[kVPT];
-    auto load_round = [&](int r0) {
+    auto load_round = [&](int r0, int nrows) {
         // branch-free: chunks past the round's rows re-read row r0 (ignored)
-        const int lim = min(kRV, pos - r0) * kCh;
+        const int lim = nrows * kCh;
 #pragma unroll
         for (int i = 0; i < kVPT; ++i) {
             const int c = i * kAT + t < lim ? i * kAT + t : 0;
-            const int row = r0 + c / kCh;
-            vr[i] = ld_global16(s_pv[row / page_tokens] + static_cast<size_t>(row % page_tokens) * kv_dim + kh * hd +
-                                dbase + (c % kCh) * 8);
+            vr[i] = ld_global16(vrow_of(r0 + c / kCh) + dbase + (c % kCh) * 8);
         }
     };
-    load_round(0);  // at pos 0 every chunk reads row 0 (unused)
+    load_round(0, min(kRV, rows_alloc));  // the whole first round, whatever pos is
     __builtin_amdgcn_sched_barrier(0);
 
     // 1. RoPE, K/V of the current position (computed by every thread, so the
@@ -357,7 +354,6 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     const uint16_t hk0 = f2h_ref(fmaf(k0, cs, -(k1 * sn))), hk1 = f2h_ref(fmaf(k0, sn, k1 * cs));
     const uint16_t hv0 = f2h_ref(v0), hv1 = f2h_ref(v1);
     if (t < half) {
-        const size_t off = static_cast<size_t>(pos % page_tokens) * kv_dim + kh * hd;
         s_q[t] = rq0;
         s_q[t + half] = rq1;
         s_k[t] = h2f(hk0);
@@ -365,8 +361,8 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
         s_v[t] = h2f(hv0);
         s_v[t + half] = h2f(hv1);
         if (slice == 0 && h % group == 0) {  // one writer per kv head
-            uint16_t* kc = s_pk[pos / page_tokens] + off;
-            uint16_t* vc = s_pv[pos / page_tokens] + off;
+            uint16_t* kc = krow_of(pos);
+            uint16_t* vc = vrow_of(pos);
             kc[t] = hk0;
             kc[t + half] = hk1;
             vc[t] = hv0;
@@ -449,7 +445,7 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
             }
         }
         __syncthreads();  // also orders the s_a writes above before their reads
-        if (r0 + kRV < pos) load_round(r0 + kRV);
+        if (r0 + kRV < pos) load_round(r0 + kRV, min(kRV, pos - r0 - kRV));
         if (t < SW) {
             const uint16_t* vl = s_vt + t * kRVP;
             const float* al = s_a + r0;
@@ -863,12 +859,12 @@ hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* 
                        hd, kv_dim, page_tokens, st);
 }
 
-hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* cos_t,
-                                    const float* sin_t, const int* d_pos, uint16_t* const* pt_k,
-                                    uint16_t* const* pt_v, size_t page_tokens, float* out, int8_t* q8, float* q8d,
-                                    size_t n_head, size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st) {
+hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* rope,
+                                    const int* d_pos, uint16_t* kbase, uint16_t* vbase, size_t page_tokens,
+                                    size_t page_stride, float* out, int8_t* q8, float* q8d, size_t n_head,
+                                    size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st) {
     if (!attn_decode_fused_ok(hd, max_ctx, page_tokens)) return hipErrorInvalidValue;
-    const int max_pages = static_cast<int>((max_ctx + page_tokens - 1) / page_tokens);
+    const int rows_alloc = static_cast<int>((max_ctx + page_tokens - 1) / page_tokens * page_tokens);
     const int sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
     const int nslice = static_cast<int>(hd) / sw;
     const int ctx_pad = static_cast<int>((max_ctx + 3) / 4 * 4);
@@ -876,10 +872,10 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
     const dim3 grid(static_cast<unsigned>(n_head * nslice));
     const int group = static_cast<int>(n_head / n_head_kv), kvd = static_cast<int>(n_head_kv * hd);
 #define MVH_ATTN_FUSED(SW_, HD_)                                                                                     \
-    attn_decode_fused_kernel<SW_, HD_><<<grid, kAT, lds, st>>>(q, k, v, cos_t, sin_t, d_pos, pt_k, pt_v,            \
-                                                               static_cast<int>(page_tokens), max_pages, out, q8,  \
-                                                               q8d, group, static_cast<int>(hd), kvd, ctx_pad,      \
-                                                               nslice)
+    attn_decode_fused_kernel<SW_, HD_><<<grid, kAT, lds, st>>>(q, k, v, rope, d_pos, kbase, vbase,                 \
+                                                               static_cast<int>(page_tokens), page_stride, rows_alloc, \
+                                                               out, q8, q8d, group, static_cast<int>(hd), kvd,        \
+                                                               ctx_pad, nslice)
     if (sw == 32 && hd == 128) MVH_ATTN_FUSED(32, 128);
     else if (sw == 32) MVH_ATTN_FUSED(32, 0);
     else if (sw == 16) MVH_ATTN_FUSED(16, 0);

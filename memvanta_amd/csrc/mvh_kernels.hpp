@@ -98,10 +98,12 @@ hipError_t launch_attn_prefill(int kv_type, const void* const* pt_k, const void*
 // (when q8 != null, hd % 32 == 0) the Q8 activation of the output.  One
 // workgroup per query head; max_ctx bounds the position.
 bool attn_decode_fused_ok(size_t hd, size_t max_ctx, size_t page_tokens);  // LDS and shape limits of the fused kernel
-hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* cos_t,
-                                    const float* sin_t, const int* d_pos, uint16_t* const* pt_k,
-                                    uint16_t* const* pt_v, size_t page_tokens, float* out, int8_t* q8, float* q8d,
-                                    size_t n_head, size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st);
+// rope: cos then sin of the position (hd/2 floats each); K/V rows of page p at
+// kbase / vbase + p * page_stride (elements) + (row % page_tokens) * kv_dim
+hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* rope,
+                                    const int* d_pos, uint16_t* kbase, uint16_t* vbase, size_t page_tokens,
+                                    size_t page_stride, float* out, int8_t* q8, float* q8d, size_t n_head,
+                                    size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st);
 // scores needs n_head * (pos+1) floats of scratch
 hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
                               float* scores, float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd,
@@ -113,8 +115,11 @@ hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* 
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, size_t sink_words, hipStream_t st);
 
 // ---- model step pieces (mvh_model.hip) ----
+// with rope_cur (one token): also copies cos/sin row *d_pos of the RoPE
+// tables (half floats each) to rope_cur[0 .. 2*half)
 hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int* tokens, size_t B, float* out,
-                        hipStream_t st);
+                        hipStream_t st, const int* d_pos = nullptr, const float* cos_t = nullptr,
+                        const float* sin_t = nullptr, size_t half = 0, float* rope_cur = nullptr);
 // x += add (if add), n = rmsnorm(x)*w, and q/qd = Q8 of n (if q); B rows of D
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
                           size_t D, float eps, hipStream_t st, bool q_op = false);

@@ -37,10 +37,18 @@ namespace {
 
 // Embedding rows of B tokens (token ids in device memory).
 __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t* __restrict__ W, int cols,
-                                                    const int* __restrict__ tokens, float* __restrict__ out) {
+                                                    const int* __restrict__ tokens, float* __restrict__ out,
+                                                    const int* __restrict__ d_pos, const float* __restrict__ cos_t,
+                                                    const float* __restrict__ sin_t, int half,
+                                                    float* __restrict__ rope_cur) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= cols) return;
     out[static_cast<size_t>(blockIdx.y) * cols + i] = dequant_elem(type, W, cols, static_cast<size_t>(tokens[blockIdx.y]), i);
+    if (rope_cur && i < half) {  // the decode attention's RoPE row, read without waiting for the position
+        const size_t p = static_cast<size_t>(*d_pos);
+        rope_cur[i] = cos_t[p * half + i];
+        rope_cur[half + i] = sin_t[p * half + i];
+    }
 }
 
 // x += add (when add != null), then LlamaModel::rmsnorm (src/llama_model.cpp:237)
@@ -204,10 +212,12 @@ __global__ __launch_bounds__(kArgT) void argmax_kernel(const float* __restrict__
 }  // namespace
 
 hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int* tokens, size_t B, float* out,
-                        hipStream_t st) {
+                        hipStream_t st, const int* d_pos, const float* cos_t, const float* sin_t, size_t half,
+                        float* rope_cur) {
     if (!B) return hipSuccess;
+    if (rope_cur && (B != 1 || !d_pos || !cos_t || !sin_t || half > cols)) return hipErrorInvalidValue;
     embed_kernel<<<dim3(static_cast<unsigned>((cols + 255) / 256), static_cast<unsigned>(B)), 256, 0, st>>>(
-        type, W, static_cast<int>(cols), tokens, out);
+        type, W, static_cast<int>(cols), tokens, out, d_pos, cos_t, sin_t, static_cast<int>(half), rope_cur);
     return hipGetLastError();
 }
 

@@ -137,6 +137,7 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     rope_sin_ = static_cast<float*>(dalloc(si.size() * 4));
     check(hipMemcpy(rope_cos_, co.data(), co.size() * 4, hipMemcpyHostToDevice), "upload rope");
     check(hipMemcpy(rope_sin_, si.data(), si.size() * 4, hipMemcpyHostToDevice), "upload rope");
+    rope_cur_ = static_cast<float*>(dalloc(c_.head_dim() * 4));
 
     // paged KV cache: the pages of every layer preallocated in HBM, addressed
     // through per-layer page tables; page stride 256-byte aligned (a Q8 page
@@ -145,6 +146,9 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     const std::size_t stride = (mvh::kv_page_bytes(kv_type_, page_tokens_, c_.kv_dim()) + 255) / 256 * 256;
     auto* kslab = static_cast<uint8_t*>(dalloc(c_.n_layer * max_pages_ * stride));
     auto* vslab = static_cast<uint8_t*>(dalloc(c_.n_layer * max_pages_ * stride));
+    kslab_ = kslab;
+    vslab_ = vslab;
+    kv_stride_ = stride;
     std::vector<void*> tk(c_.n_layer * max_pages_), tv(c_.n_layer * max_pages_);
     for (std::size_t i = 0; i < tk.size(); ++i) {
         tk[i] = kslab + i * stride;
@@ -360,7 +364,10 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
 // token in *d_token at position *d_pos_.
 void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
     const std::size_t D = c_.n_embd, F = c_.n_ff, hd = c_.head_dim();
-    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_token, 1, x_, stream_), "embed");
+    // the embedding launch also copies the RoPE row of the position for the fused attention
+    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_token, 1, x_, stream_, d_pos_,
+                            rope_cos_, rope_sin_, hd / 2, fused_attn_ ? rope_cur_ : nullptr),
+          "embed");
     for (std::size_t li = 0; li < c_.n_layer; ++li) {
         auto& L = layers_[li];
         const auto lay = qkv_layout(L, 1);
@@ -380,9 +387,11 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
         // the attention kernels write the o projection's Q8 activations (32-element head slices are Q8 blocks)
         const bool o_q8 = L.o.type == 2 && hd % 32 == 0 && L.o.cols == c_.n_head * hd;
         if (fused_attn_) {
-            check(mvh::launch_attn_decode_fused(lay.q, lay.k, lay.v, rope_cos_, rope_sin_, d_pos_,
-                                                reinterpret_cast<uint16_t* const*>(pk),
-                                                reinterpret_cast<uint16_t* const*>(pv), page_tokens_, att_,
+            const std::size_t layer_off = li * max_pages_ * kv_stride_;
+            check(mvh::launch_attn_decode_fused(lay.q, lay.k, lay.v, rope_cur_, d_pos_,
+                                                reinterpret_cast<uint16_t*>(kslab_ + layer_off),
+                                                reinterpret_cast<uint16_t*>(vslab_ + layer_off), page_tokens_,
+                                                kv_stride_ / 2, att_,
                                                 o_q8 ? q8_ : nullptr, q8d_, c_.n_head, c_.n_head_kv, hd, c_.n_ctx,
                                                 stream_),
                   "attention");

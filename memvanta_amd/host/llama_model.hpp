@@ -108,6 +108,9 @@ private:
     void** pt_k_{};
     void** pt_v_{};
     float *rope_cos_{}, *rope_sin_{};
+    float* rope_cur_{};                  // cos/sin row of the decode position (written by the embedding launch)
+    uint8_t *kslab_{}, *vslab_{};        // every layer's KV pages, page i of layer l at slab + (l * max_pages_ + i) * kv_stride_
+    std::size_t kv_stride_{};
     // activations ([max_batch][...] for prefill; row 0 for decode)
     float *x_{}, *n_{}, *qkv_{}, *att_{}, *proj_{}, *gu_{}, *ff_{}, *logits_d_{}, *scores_{};
     float* ffo_{};       // down-projection output (the residual added by the next norm)
