@@ -250,6 +250,61 @@ def measure_hbm(ctx, nbytes: int = 1 << 30, reps: int = 8):
     return {"read": nbytes / read_s / 1e9, "read_us": read_s * 1e6, "copy": 2 * nbytes / copy_s / 1e9}
 
 
+def measure_node_floor(ctx, launches: int = 200):
+    """Cost of a near-empty node in a HIP graph: mvh_stream_read of 16 bytes
+    (one workgroup, one load) replayed as a graph of `launches` nodes; the
+    per-node time is the floor every dependent kernel of a decode step pays.
+    Under rocprofv3 --kernel-trace the same launches show the trace's own
+    per-dispatch floor."""
+    import torch
+
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    buf = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(launches):
+            ctx.stream_read(buf, 16, sink, sink.numel())
+    ctx.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        g.replay()
+        a.record(stream)
+        for _ in range(3):
+            g.replay()
+        b.record(stream)
+    b.synchronize()
+    us = a.elapsed_time(b) * 1e3 / (3 * launches)
+    del g
+    return us
+
+
+# exact FORCE_Q8 chain: 3 VALU lane-operations per (output, block) -- the
+# int-to-float conversion of the block sum, the scale product d_w * d_a and the
+# fma (no packed FP32); MI355X: 256 CUs x 64 lanes x 2.4 GHz
+VALU_LANE_OPS_PER_S = 256 * 64 * 2.4e9
+
+
+def prefill_roofline(gemm):
+    """Roofline entries of the prefill GEMM: at M = 512 (4096 x 4096) the
+    exact chain's VALU floor; at M = 32 the HBM bound of its weight bytes."""
+    out = {}
+    for e in gemm:
+        k, n, m = e["K"], e["N"], e["M"]
+        if (k, n) != (4096, 4096) or m not in (32, 512):
+            continue
+        floor_us = 3.0 * m * n * (k // 32) / VALU_LANE_OPS_PER_S * 1e6
+        hbm_us = (n * (k // 32) * 18 + m * (k + k // 8) + 4 * m * n) / (HBM_PEAK_GBS * 1e3)
+        out[f"M{m}"] = {"shape": f"{k}->{n}", "us": e["us"], "valu_floor_us": round(floor_us, 2),
+                        "frac_of_valu_floor": round(floor_us / e["us"], 4), "hbm_bound_us": round(hbm_us, 2),
+                        "frac_of_hbm_bound": round(hbm_us / e["us"], 4), "frac_int8_peak": e["frac_int8_peak"]}
+    out["basis"] = ("VALU floor: 3 lane-operations per output-block (cvt, d_w*d_a, fma) at 256 CUs x 64 lanes x "
+                    "2.4 GHz; HBM bound: the GEMM's algorithmic bytes at 8 TB/s; us includes the activation "
+                    "quantizer launch")
+    return out
+
+
 def time_pp(m, prompt, reps: int = 1):
     """Prefill rate of prompt (chunks of BATCH, last-token logits) after one untimed run."""
     import torch
@@ -573,6 +628,7 @@ def main():
         print(json.dumps({"prefill_gemm": gemm}), flush=True)
         us = time_gemv_kernels(ctx, mats, args.kernel_launches, args.rotate_mb)
         hbm = measure_hbm(ctx, 256 << 20, 2)
+        node_us = measure_node_floor(ctx)
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -580,7 +636,7 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"gemv_us": {f"{k}->{n}": round(v, 3) for (k, n), v in us.items()},
                           "copy_bytes": src.numel() * 4, "read_probe_bytes": 256 << 20,
-                          "read_probe_gbs": round(hbm["read"], 1)}))
+                          "read_probe_gbs": round(hbm["read"], 1), "graph_node_us": round(node_us, 3)}))
         ctx.close()
         return
 
@@ -657,6 +713,7 @@ def main():
                       "GB/s": round(gemv_bytes(k, n) / us[(k, n)] / 1e3, 1)} for k, n in ISOLATED_GEMVS]
         gemm = time_prefill_gemm(ctx, mats, 10, args.rotate_mb)
         hbm = measure_hbm(ctx)
+        node_us = measure_node_floor(ctx)
         log("kernel timings done")
 
         traffic = None
@@ -803,6 +860,7 @@ def main():
             "prefill_gemm_int8_mfma": gemm,
             "prefill_gemm_note": "tensor_matmul_batch_v06 FORCE_Q8 numerics incl. the activation quantizer; "
                                  "frac_int8_peak vs 5 POP/s dense int8",
+            "prefill_roofline": prefill_roofline(gemm),
             "other_kv_cache_types": kv_types,
             "other_models": others,
         },
@@ -817,6 +875,9 @@ def main():
                      "measured_read_basis": "mvh_stream_read over two alternated 1 GiB buffers (16-byte coalesced "
                                             "loads, 8 workgroups per CU), HIP events",
                      "measured_copy_gbs": round(hbm["copy"], 1),
+                     "measured_graph_node_us": round(node_us, 3),
+                     "graph_node_basis": "a one-workgroup 16-byte mvh_stream_read per node, graph of 200 nodes: "
+                                         "the floor each dependent kernel of a decode step pays",
                      "frac_of_measured_read": round(achieved / hbm["read"], 4)},
         "cpu_baseline": cpu_baseline,
     }
