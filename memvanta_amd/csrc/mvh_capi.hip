@@ -576,9 +576,7 @@ static int v06_device(mvh_context* c, const mvh_tensor* w, const float* xd, floa
             if (mfma) {
                 MVH_HIP(mvh::launch_gemm_q4_0_q8_mfma(W, a.q, a.d, yd, rows, cols, batch, c->stream));
             } else {
-                for (size_t b = 0; b < batch; ++b)
-                    MVH_HIP(mvh::launch_gemv_q4_0(W, a.q + b * cols, a.d + b * nb, yd + b * rows, rows, cols,
-                                                  c->stream));
+                MVH_HIP(mvh::launch_gemv_q4_0(W, a.q, a.d, yd, rows, cols, c->stream, batch));
             }
         } else {
             MVH_HIP(mvh::launch_gemv_q8_0(W, xd, yd, rows, cols, batch, c->stream));

@@ -62,12 +62,17 @@ __device__ __forceinline__ void fold_pairs(const float2* s_pair, int pitch, int 
 //                bytes) into LDS, and every lane then reads its unit from LDS.
 enum { kLoadStream = 0, kLoadCached = 1, kLoadStaged = 2 };
 
+// blockIdx.y = token: its Q8 row at aq + token * K, scales at ad + token * nb,
+// outputs at y + token * N (one launch for a batch, each token's chains as for one)
 template <int G, int MODE>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_0_kernel(const uint8_t* __restrict__ W,
                                                                   const int8_t* __restrict__ aq,
                                                                   const float* __restrict__ ad, float* __restrict__ y,
                                                                   int N, int nb, int rows_per_wg) {
     extern __shared__ __align__(16) uint8_t smem[];
+    aq += static_cast<size_t>(blockIdx.y) * nb * 32;
+    ad += static_cast<size_t>(blockIdx.y) * nb;
+    y += static_cast<size_t>(blockIdx.y) * N;
     const int ngrp = (nb + 7) >> 3;
     uint8_t* s_aq = smem;
     float* s_ad = reinterpret_cast<float*>(smem + ngrp * kActPitch);
@@ -831,8 +836,16 @@ int pick_rows_per_wg(size_t rows, size_t nb, size_t pair_budget) {
 }  // namespace
 
 hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows, size_t cols,
-                            hipStream_t st) {
-    if (gemv_q4_0_rows16_ok(cols)) return launch_gemv_q4_0_rows16(W, nullptr, aq, ad, y, rows, cols, st);
+                            hipStream_t st, size_t batch) {
+    if (!rows || !batch) return hipSuccess;
+    if (gemv_q4_0_rows16_ok(cols)) {  // one token per launch
+        const size_t nbk = cols / 32;
+        for (size_t b = 0; b < batch; ++b)
+            if (hipError_t e = launch_gemv_q4_0_rows16(W, nullptr, aq + b * cols, ad + b * nbk, y + b * rows, rows,
+                                                       cols, st))
+                return e;
+        return hipSuccess;
+    }
     static const int mode = [] {
         const char* e = getenv("MVH_GEMV_LOAD");
         return e ? atoi(e) : kLoadStaged;
@@ -846,7 +859,7 @@ hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad,
     int rpw = pick_rows_per_wg(rows, nb, 60 * 1024 - fixed);
     rpw = std::max(1, std::min<int>(rpw, static_cast<int>((60 * 1024 - fixed) / per_row)));
     const size_t lds = fixed + static_cast<size_t>(rpw) * per_row + 16;
-    const unsigned grid = static_cast<unsigned>((rows + rpw - 1) / rpw);
+    const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw), static_cast<unsigned>(batch));
     const int n = static_cast<int>(rows);
     if (nb % 8 != 0)
         gemv_q4_0_kernel<1, kLoadCached><<<grid, kGemvThreads, lds, st>>>(W, aq, ad, y, n, nb, rpw);

@@ -23,9 +23,11 @@ hipError_t launch_read_row(uint32_t type, const uint8_t* W, size_t cols, size_t 
 
 // ---- decode GEMV (mvh_gemv.hip); W is the tensor in native GGUF layout ----
 // y[N] = W[N x K] . x[K]; `rows` are N, `cols` are K.
-// aq must be 16-byte aligned; the kernel derives the per-block sums of aq itself
+// aq must be 16-byte aligned; the kernel derives the per-block sums of aq itself.
+// batch tokens: rows of aq / ad / y at strides cols / cols/32 / rows (one
+// launch unless cols takes the row-group kernel, which runs one per token)
 hipError_t launch_gemv_q4_0(const uint8_t* W, const int8_t* aq, const float* ad, float* y, size_t rows, size_t cols,
-                            hipStream_t st);
+                            hipStream_t st, size_t batch = 1);
 hipError_t launch_gemv_q8_0(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                             hipStream_t st);
 hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,

@@ -339,8 +339,7 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
             if (e == hipSuccess && q8_op) {
                 e = mvh::launch_gemm_q4_0_q8_mfma(W, q8, q8d, y, rows, cols, B, stream_);
             } else {
-                for (std::size_t b = 0; b < B && e == hipSuccess; ++b)
-                    e = mvh::launch_gemv_q4_0(W, q8 + b * cols, q8d + b * nb, y + b * rows, rows, cols, stream_);
+                e = mvh::launch_gemv_q4_0(W, q8, q8d, y, rows, cols, stream_, B);
             }
         } else {
             e = mvh::launch_gemv_q8_0(W, x, y, rows, cols, B, stream_);
