@@ -479,15 +479,18 @@ def _cpu_kernels(lib, kind, spec, threads):
     from memvanta_amd import synth
 
     rng = np.random.default_rng(ACT_SEED)
+    shapes = [tuple(x) for x in spec["shapes"]]
+    names = {shp: nm for shp, nm in zip(shapes, spec["names"])}
+    gemm_shapes = [tuple(x) for x in spec.get("gemm_shapes", [])]
     if kind == "reference":
         g = lib.gguf(spec["path"])
-        mv = lambda k, n, x: g.matvec(MATRIX_NAMES[(k, n)], x, n, threads)  # noqa: E731
-        mm = lambda k, n, x, q8: g.matmul_batch_v06(MATRIX_NAMES[(k, n)], x, n, q8, threads)  # noqa: E731
+        mv = lambda k, n, x: g.matvec(names[(k, n)], x, n, threads)  # noqa: E731
+        mm = lambda k, n, x, q8: g.matmul_batch_v06(names[(k, n)], x, n, q8, threads)  # noqa: E731
     else:
-        w = {tuple(s): np.load(p) for s, p in zip(spec["shapes"], spec["npy"])}
+        w = {shp: np.load(p) for shp, p in zip(shapes, spec["npy"])}
         mv = lambda k, n, x: lib.matvec(w[(k, n)], synth.Q4_0, n, k, x, threads)  # noqa: E731
         mm = lambda k, n, x, q8: lib.matmul_batch_v06(w[(k, n)], synth.Q4_0, n, k, x,  # noqa: E731
-                                                       "ffn" in MATRIX_NAMES[(k, n)], q8, threads)
+                                                       "ffn" in names[(k, n)], q8, threads)
 
     def rep(fn):
         fn()
@@ -499,13 +502,13 @@ def _cpu_kernels(lib, kind, spec, threads):
         return _mean_sd(ts)
 
     gemv = []
-    for k, n in GEMV_CONFIG:
+    for k, n in shapes:
         x = synth.activations(rng, 1, k)[0]
         ms, sd = rep(lambda: mv(k, n, x))
         gemv.append({"shape": f"{k}->{n}", "ms": ms, "sd": sd, "GB/s": round(gemv_bytes(k, n) / ms / 1e6, 2)})
     gemm = []
     if spec.get("gemm", True):
-        for k, n in PREFILL_GEMMS:
+        for k, n in gemm_shapes:
             x = synth.activations(rng, 32, k)
             for q8 in (True, False):
                 ms, sd = rep(lambda: mm(k, n, x, q8))
@@ -754,7 +757,8 @@ def main():
                     "llama7b": {"path": path, "seed_ids": [int(t) for t in seed], "tg_tokens": n_cpu_tg,
                                 "pp_force_q8_tokens": CPU_PP_FORCE_Q8_TOKENS, "seed_4": CPU_SEED_4_THREADS,
                                 "tg_tokens_4": CPU_TG_4_THREADS},
-                    "matrices": {"path": mpath, "shapes": GEMV_CONFIG, "npy": npys},
+                    "matrices": {"path": mpath, "shapes": GEMV_CONFIG, "npy": npys,
+                                 "names": [MATRIX_NAMES[kn] for kn in GEMV_CONFIG], "gemm_shapes": PREFILL_GEMMS},
                     "other_models": other_specs}
             log("cpu leg started (child process)")
             cpu = run_cpu_leg(spec, args.cpu_timeout)
