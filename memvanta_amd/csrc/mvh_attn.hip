@@ -877,6 +877,7 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
                                                                out, q8, q8d, group, static_cast<int>(hd), kvd,        \
                                                                ctx_pad, nslice)
     if (sw == 32 && hd == 128) MVH_ATTN_FUSED(32, 128);
+    else if (sw == 32 && hd == 64) MVH_ATTN_FUSED(32, 64);
     else if (sw == 32) MVH_ATTN_FUSED(32, 0);
     else if (sw == 16) MVH_ATTN_FUSED(16, 0);
     else MVH_ATTN_FUSED(8, 0);
