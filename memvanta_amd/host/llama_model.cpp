@@ -83,7 +83,7 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
         throw std::runtime_error("device path needs n_embd, n_ff % 32 == 0 and head_dim % 8 == 0");
 
     check(hipSetDevice(device_), "hipSetDevice");
-    check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    check(hipStreamCreateWithFlags(&lanes_[0].st, hipStreamNonBlocking), "hipStreamCreate");
     auto dalloc = [&](std::size_t bytes) {
         void* p = nullptr;
         check(hipMalloc(&p, std::max<std::size_t>(bytes, 16)), "hipMalloc");
@@ -160,26 +160,31 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     check(hipMemcpy(pt_v_, tv.data(), tv.size() * sizeof(void*), hipMemcpyHostToDevice), "page table");
 
     const std::size_t B = max_batch_, D = c_.n_embd, F = c_.n_ff, KV = c_.kv_dim(), W = std::max(D, F);
-    x_ = static_cast<float*>(dalloc(B * D * 4));
-    n_ = static_cast<float*>(dalloc(B * D * 4));
-    qkv_ = static_cast<float*>(dalloc(B * (D + 2 * KV) * 4));
-    att_ = static_cast<float*>(dalloc(B * D * 4));
-    proj_ = static_cast<float*>(dalloc(B * D * 4));
-    gu_ = static_cast<float*>(dalloc(B * 2 * F * 4));
-    ff_ = static_cast<float*>(dalloc(B * F * 4));
-    scores_ = static_cast<float*>(dalloc(B * c_.n_head * c_.n_ctx * 4));
+    for (Lane& l : lanes_) {
+        if (&l != &lanes_[0]) check(hipStreamCreateWithFlags(&l.st, hipStreamNonBlocking), "hipStreamCreate");
+        l.x = static_cast<float*>(dalloc(B * D * 4));
+        l.n = static_cast<float*>(dalloc(B * D * 4));
+        l.qkv = static_cast<float*>(dalloc(B * (D + 2 * KV) * 4));
+        l.att = static_cast<float*>(dalloc(B * D * 4));
+        l.proj = static_cast<float*>(dalloc(B * D * 4));
+        l.gu = static_cast<float*>(dalloc(B * 2 * F * 4));
+        l.ff = static_cast<float*>(dalloc(B * F * 4));
+        l.scores = static_cast<float*>(dalloc(B * c_.n_head * c_.n_ctx * 4));
+        l.ffo = static_cast<float*>(dalloc(B * D * 4));
+        l.q8 = static_cast<int8_t*>(dalloc(mvh::q8_op_bytes(B, W)));  // row-major or operand order
+        l.q8d = static_cast<float*>(dalloc(B * (W / 32) * 4));
+        l.q8s = static_cast<int8_t*>(dalloc(mvh::q8_op_bytes(B, W)));
+        l.q8sd = static_cast<float*>(dalloc(B * (W / 32) * 4));
+        l.q8ss = static_cast<int*>(dalloc(B * (W / 32) * 4));
+    }
+    kv_done_.assign(kLanes * c_.n_layer, nullptr);
+    for (hipEvent_t& e : kv_done_) check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
     logits_d_ = static_cast<float*>(dalloc(c_.vocab * 4));
-    q8_ = static_cast<int8_t*>(dalloc(mvh::q8_op_bytes(B, W)));  // row-major or operand order
-    q8d_ = static_cast<float*>(dalloc(B * (W / 32) * 4));
     d_tok_ = static_cast<int*>(dalloc(16));
     d_hist_ = static_cast<int*>(dalloc(4 * (c_.n_ctx + 1)));
     d_pos_ = static_cast<int*>(dalloc(16));
-    d_toks_ = static_cast<int*>(dalloc(B * 4));
-    rec_ = std::make_unique<prof::Recorder>(stream_);
-    ffo_ = static_cast<float*>(dalloc(B * D * 4));
-    q8s_ = static_cast<int8_t*>(dalloc(mvh::q8_op_bytes(B, W)));
-    q8sd_ = static_cast<float*>(dalloc(B * (W / 32) * 4));
-    q8ss_ = static_cast<int*>(dalloc(B * (W / 32) * 4));
+    d_prompt_ = static_cast<int*>(dalloc(4 * (c_.n_ctx + B)));
+    rec_ = std::make_unique<prof::Recorder>(lanes_[0].st);
     check(hipHostMalloc(reinterpret_cast<void**>(&pin_), 4 * (c_.n_ctx + B + 8), hipHostMallocDefault),
           "hipHostMalloc");
     logits_.resize(c_.vocab);
@@ -189,11 +194,15 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
 
 LlamaModel::~LlamaModel() {
     (void)hipSetDevice(device_);
-    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (Lane& l : lanes_)
+        if (l.st) (void)hipStreamSynchronize(l.st);
     if (graph_) (void)hipGraphExecDestroy(graph_);
+    for (hipEvent_t e : kv_done_)
+        if (e) (void)hipEventDestroy(e);
     for (void* p : allocs_) (void)hipFree(p);
     if (pin_) (void)hipHostFree(pin_);
-    if (stream_) (void)hipStreamDestroy(stream_);
+    for (Lane& l : lanes_)
+        if (l.st) (void)hipStreamDestroy(l.st);
 }
 
 void LlamaModel::upload(Tensor& t, const std::string& name) {
@@ -241,8 +250,8 @@ bool LlamaModel::upload_fused(Tensor& t, const std::vector<std::string>& names) 
 
 LlamaModel::QkvLayout LlamaModel::qkv_layout(const Layer& L, std::size_t B) const {
     const std::size_t D = c_.n_embd, KV = c_.kv_dim();
-    if (L.fused_qkv) return {qkv_, qkv_ + D, qkv_ + D + KV, D + 2 * KV, D + 2 * KV};
-    return {qkv_, qkv_ + B * D, qkv_ + B * (D + KV), D, KV};
+    if (L.fused_qkv) return {ln_->qkv, ln_->qkv + D, ln_->qkv + D + KV, D + 2 * KV, D + 2 * KV};
+    return {ln_->qkv, ln_->qkv + B * D, ln_->qkv + B * (D + KV), D, KV};
 }
 
 float* LlamaModel::upload_vector(const std::string& name) {
@@ -288,12 +297,12 @@ void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const f
     switch (w.type) {
         case 2:
             if (q8) {
-                e = mvh::launch_gemv_q4_0(W, q8, q8d, y, w.rows, w.cols, stream_);
+                e = mvh::launch_gemv_q4_0(W, q8, q8d, y, w.rows, w.cols, ln_->st);
             } else if (mvh::gemv_q4_0_rows16_ok(w.cols)) {
-                e = mvh::launch_gemv_q4_0_rows16(W, x, nullptr, nullptr, y, w.rows, w.cols, stream_);
+                e = mvh::launch_gemv_q4_0_rows16(W, x, nullptr, nullptr, y, w.rows, w.cols, ln_->st);
             } else {
-                e = mvh::launch_quantize_q8(x, q8s_, q8sd_, q8ss_, 1, w.cols, stream_);
-                if (e == hipSuccess) e = mvh::launch_gemv_q4_0(W, q8s_, q8sd_, y, w.rows, w.cols, stream_);
+                e = mvh::launch_quantize_q8(x, ln_->q8s, ln_->q8sd, ln_->q8ss, 1, w.cols, ln_->st);
+                if (e == hipSuccess) e = mvh::launch_gemv_q4_0(W, ln_->q8s, ln_->q8sd, y, w.rows, w.cols, ln_->st);
             }
             break;
         default: e = fp32_gemv(w, x, y, 1); break;
@@ -307,10 +316,10 @@ void LlamaModel::gemv(const Tensor& w, const float* x, const int8_t* q8, const f
 hipError_t LlamaModel::fp32_gemv(const Tensor& w, const float* x, float* y, std::size_t B) {
     const auto* W = static_cast<const uint8_t*>(w.d);
     switch (w.type) {
-        case 8: return mvh::launch_gemv_q8_0(W, x, y, w.rows, w.cols, B, stream_);
-        case 14: return mvh::launch_gemv_q6_k(W, x, y, w.rows, w.cols, B, stream_);
-        case 0: return mvh::launch_gemv_f32(reinterpret_cast<const float*>(W), x, y, w.rows, w.cols, B, stream_);
-        case 1: return mvh::launch_gemv_f16(reinterpret_cast<const uint16_t*>(W), x, y, w.rows, w.cols, B, stream_);
+        case 8: return mvh::launch_gemv_q8_0(W, x, y, w.rows, w.cols, B, ln_->st);
+        case 14: return mvh::launch_gemv_q6_k(W, x, y, w.rows, w.cols, B, ln_->st);
+        case 0: return mvh::launch_gemv_f32(reinterpret_cast<const float*>(W), x, y, w.rows, w.cols, B, ln_->st);
+        case 1: return mvh::launch_gemv_f16(reinterpret_cast<const uint16_t*>(W), x, y, w.rows, w.cols, B, ln_->st);
     }
     return hipErrorInvalidValue;
 }
@@ -325,34 +334,35 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
     hipError_t e = hipSuccess;
     prof_start();
     if (B < 2 || (w.type != 2 && w.type != 8) || cols % 32) {  // tensor_matmul_batch: fp32 per token
-        if (w.type == 2) e = mvh::launch_gemv_q4_0_f32act(W, x, y, rows, cols, B, stream_);
+        if (w.type == 2) e = mvh::launch_gemv_q4_0_f32act(W, x, y, rows, cols, B, ln_->st);
         else e = fp32_gemv(w, x, y, B);
     } else if (mode_ == PrefillMode::Q8) {
         if (w.type == 2) {
             if (!q8) {
                 q8_op = mfma_gemm(w);
-                e = mvh::launch_quantize_q8(x, q8s_, q8sd_, q8ss_, B, cols, stream_, q8_op);
-                q8 = q8s_;
-                q8d = q8sd_;
+                e = mvh::launch_quantize_q8(x, ln_->q8s, ln_->q8sd, ln_->q8ss, B, cols, ln_->st, q8_op);
+                q8 = ln_->q8s;
+                q8d = ln_->q8sd;
             }
-            if (q8_op && !mfma_gemm(w)) throw std::logic_error("operand-order activations for a non-MFMA tensor: " + w.sname);
+            if (q8_op && !mfma_gemm(w))
+                throw std::logic_error("operand-order activations for a non-MFMA tensor: " + w.sname);
             if (e == hipSuccess && q8_op) {
-                e = mvh::launch_gemm_q4_0_q8_mfma(W, q8, q8d, y, rows, cols, B, stream_);
+                e = mvh::launch_gemm_q4_0_q8_mfma(W, q8, q8d, y, rows, cols, B, ln_->st);
             } else {
-                e = mvh::launch_gemv_q4_0(W, q8, q8d, y, rows, cols, stream_, B);
+                e = mvh::launch_gemv_q4_0(W, q8, q8d, y, rows, cols, ln_->st, B);
             }
         } else {
-            e = mvh::launch_gemv_q8_0(W, x, y, rows, cols, B, stream_);
+            e = mvh::launch_gemv_q8_0(W, x, y, rows, cols, B, ln_->st);
         }
     } else {
         const std::size_t step = is_ffn(w.sname) ? 8 : 4, blocked = B / step * step;
-        e = mvh::launch_batch4_f32act(w.type, W, x, y, rows, cols, blocked, stream_);
+        e = mvh::launch_batch4_f32act(w.type, W, x, y, rows, cols, blocked, ln_->st);
         if (e == hipSuccess && blocked < B) {
             if (w.type == 2)
                 e = mvh::launch_gemv_q4_0_f32act(W, x + blocked * cols, y + blocked * rows, rows, cols, B - blocked,
-                                                 stream_);
+                                                 ln_->st);
             else
-                e = mvh::launch_gemv_q8_0(W, x + blocked * cols, y + blocked * rows, rows, cols, B - blocked, stream_);
+                e = mvh::launch_gemv_q8_0(W, x + blocked * cols, y + blocked * rows, rows, cols, B - blocked, ln_->st);
         }
     }
     check(e, w.sname.c_str());
@@ -362,24 +372,25 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
 // One decode step (LlamaModel::forward, src/llama_model.cpp:253-259) for the
 // token in *d_token at position *d_pos_.
 void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
+    const Lane& a = *ln_;
     const std::size_t D = c_.n_embd, F = c_.n_ff, hd = c_.head_dim();
     // the embedding launch also copies the RoPE row of the position for the fused attention
-    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_token, 1, x_, stream_, d_pos_,
+    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_token, 1, a.x, a.st, d_pos_,
                             rope_cos_, rope_sin_, hd / 2, fused_attn_ ? rope_cur_ : nullptr),
           "embed");
     for (std::size_t li = 0; li < c_.n_layer; ++li) {
         auto& L = layers_[li];
         const auto lay = qkv_layout(L, 1);
         const bool q8_in = L.fused_qkv ? L.qkv.type == 2 : (L.q.type == 2 || L.k.type == 2 || L.v.type == 2);
-        check(mvh::launch_rmsnorm(x_, li ? ffo_ : nullptr, L.attn_norm, n_, q8_in ? q8_ : nullptr, q8d_, 1, D,
-                                  c_.rms_eps, stream_),
+        check(mvh::launch_rmsnorm(a.x, li ? a.ffo : nullptr, L.attn_norm, a.n, q8_in ? a.q8 : nullptr, a.q8d, 1, D,
+                                  c_.rms_eps, a.st),
               "rmsnorm");
         if (L.fused_qkv) {
-            gemv(L.qkv, n_, L.qkv.type == 2 ? q8_ : nullptr, q8d_, qkv_);
+            gemv(L.qkv, a.n, L.qkv.type == 2 ? a.q8 : nullptr, a.q8d, a.qkv);
         } else {
-            gemv(L.q, n_, L.q.type == 2 ? q8_ : nullptr, q8d_, lay.q);
-            gemv(L.k, n_, L.k.type == 2 ? q8_ : nullptr, q8d_, lay.k);
-            gemv(L.v, n_, L.v.type == 2 ? q8_ : nullptr, q8d_, lay.v);
+            gemv(L.q, a.n, L.q.type == 2 ? a.q8 : nullptr, a.q8d, lay.q);
+            gemv(L.k, a.n, L.k.type == 2 ? a.q8 : nullptr, a.q8d, lay.k);
+            gemv(L.v, a.n, L.v.type == 2 ? a.q8 : nullptr, a.q8d, lay.v);
         }
         void* const* pk = pt_k_ + li * max_pages_;
         void* const* pv = pt_v_ + li * max_pages_;
@@ -390,51 +401,53 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
             check(mvh::launch_attn_decode_fused(lay.q, lay.k, lay.v, rope_cur_, d_pos_,
                                                 reinterpret_cast<uint16_t*>(kslab_ + layer_off),
                                                 reinterpret_cast<uint16_t*>(vslab_ + layer_off), page_tokens_,
-                                                kv_stride_ / 2, att_,
-                                                o_q8 ? q8_ : nullptr, q8d_, c_.n_head, c_.n_head_kv, hd, c_.n_ctx,
-                                                stream_),
+                                                kv_stride_ / 2, a.att,
+                                                o_q8 ? a.q8 : nullptr, a.q8d, c_.n_head, c_.n_head_kv, hd, c_.n_ctx,
+                                                a.st),
                   "attention");
         } else if (hd % 32 == 0) {  // F32 / Q8 pages: the chunk kernels with one query token
             store_kv(lay, pk, pv, d_pos_, 0, 1);
-            check(mvh::launch_attn_prefill(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, o_q8 ? q8_ : nullptr,
-                                           q8d_, false, d_pos_, 0, c_.n_ctx, 1, c_.n_head, c_.n_head_kv, hd,
-                                           c_.kv_dim(), page_tokens_, stream_),
+            check(mvh::launch_attn_prefill(kv_type_, pk, pv, lay.q, lay.q_pitch, a.scores, a.att, o_q8 ? a.q8 : nullptr,
+                                           a.q8d, false, d_pos_, 0, c_.n_ctx, 1, c_.n_head, c_.n_head_kv, hd,
+                                           c_.kv_dim(), page_tokens_, a.st),
                   "attention");
         } else {
             store_kv(lay, pk, pv, d_pos_, 0, 1);
-            check(mvh::launch_attn(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, d_pos_, 0, c_.n_ctx, 1,
-                                   c_.n_head, c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_,
-                                   o_q8 ? q8_ : nullptr, q8d_),
+            check(mvh::launch_attn(kv_type_, pk, pv, lay.q, lay.q_pitch, a.scores, a.att, d_pos_, 0, c_.n_ctx, 1,
+                                   c_.n_head, c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, a.st,
+                                   o_q8 ? a.q8 : nullptr, a.q8d),
                   "attention");
         }
-        gemv(L.o, att_, o_q8 ? q8_ : nullptr, q8d_, proj_);
+        gemv(L.o, a.att, o_q8 ? a.q8 : nullptr, a.q8d, a.proj);
         const bool q8_ffn = L.fused_gu ? L.gate_up.type == 2 : (L.gate.type == 2 || L.up.type == 2);
-        check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8_ffn ? q8_ : nullptr, q8d_, 1, D, c_.rms_eps, stream_),
+        check(mvh::launch_rmsnorm(a.x, a.proj, L.ffn_norm, a.n, q8_ffn ? a.q8 : nullptr, a.q8d, 1, D, c_.rms_eps, a.st),
               "rmsnorm");
-        float* g = gu_;
-        float* u = gu_ + F;  // one token: the fused and the separate layouts coincide
+        float* g = a.gu;
+        float* u = a.gu + F;  // one token: the fused and the separate layouts coincide
         if (L.fused_gu) {
-            gemv(L.gate_up, n_, L.gate_up.type == 2 ? q8_ : nullptr, q8d_, gu_);
+            gemv(L.gate_up, a.n, L.gate_up.type == 2 ? a.q8 : nullptr, a.q8d, a.gu);
         } else {
-            gemv(L.gate, n_, L.gate.type == 2 ? q8_ : nullptr, q8d_, g);
-            gemv(L.up, n_, L.up.type == 2 ? q8_ : nullptr, q8d_, u);
+            gemv(L.gate, a.n, L.gate.type == 2 ? a.q8 : nullptr, a.q8d, g);
+            gemv(L.up, a.n, L.up.type == 2 ? a.q8 : nullptr, a.q8d, u);
         }
-        check(mvh::launch_swiglu(g, u, 2 * F, ff_, L.down.type == 2 ? q8_ : nullptr, q8d_, 1, F, stream_), "swiglu");
-        gemv(L.down, ff_, L.down.type == 2 ? q8_ : nullptr, q8d_, ffo_);
+        check(mvh::launch_swiglu(g, u, 2 * F, a.ff, L.down.type == 2 ? a.q8 : nullptr, a.q8d, 1, F, a.st), "swiglu");
+        gemv(L.down, a.ff, L.down.type == 2 ? a.q8 : nullptr, a.q8d, a.ffo);
     }
     if (logits || argmax) {
-        check(mvh::launch_rmsnorm(x_, ffo_, out_norm_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, 1, D, c_.rms_eps,
-                                  stream_),
+        check(mvh::launch_rmsnorm(a.x, a.ffo, out_norm_, a.n, out_.type == 2 ? a.q8 : nullptr, a.q8d, 1, D, c_.rms_eps,
+                                  a.st),
               "rmsnorm");
-        gemv(out_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, logits_d_);
+        gemv(out_, a.n, out_.type == 2 ? a.q8 : nullptr, a.q8d, logits_d_);
     }
-    if (argmax) check(mvh::launch_argmax(logits_d_, c_.vocab, 1, d_tok_, d_pos_, d_hist_, stream_), "argmax");
+    if (argmax) check(mvh::launch_argmax(logits_d_, c_.vocab, 1, d_tok_, d_pos_, d_hist_, a.st), "argmax");
 }
 
 // One prefill chunk (LlamaModel::forward_batch_impl, src/llama_model.cpp:240-252).
-void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
+void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits, int prev_lane) {
+    const Lane& a = *ln_;
+    const int lane = static_cast<int>(ln_ - lanes_);
     const std::size_t D = c_.n_embd, F = c_.n_ff, hd = c_.head_dim();
-    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_tokens, B, x_, stream_), "embed");
+    check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_tokens, B, a.x, a.st), "embed");
     const bool q8mode = mode_ == PrefillMode::Q8 && B >= 2;
     for (std::size_t li = 0; li < c_.n_layer; ++li) {
         auto& L = layers_[li];
@@ -445,59 +458,64 @@ void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits) {
                                                    : mfma_gemm(L.q) && mfma_gemm(L.k) && mfma_gemm(L.v));
         const bool op_gu = q8mode && (L.fused_gu ? mfma_gemm(L.gate_up) : mfma_gemm(L.gate) && mfma_gemm(L.up));
         const bool op_down = q8mode && mfma_gemm(L.down);
-        check(mvh::launch_rmsnorm(x_, li ? ffo_ : nullptr, L.attn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D,
-                                  c_.rms_eps, stream_, op_qkv),
+        check(mvh::launch_rmsnorm(a.x, li ? a.ffo : nullptr, L.attn_norm, a.n, q8mode ? a.q8 : nullptr, a.q8d, B, D,
+                                  c_.rms_eps, a.st, op_qkv),
               "rmsnorm");
         if (L.fused_qkv) {
-            gemm(L.qkv, n_, q8mode ? q8_ : nullptr, q8d_, qkv_, B, op_qkv);
+            gemm(L.qkv, a.n, q8mode ? a.q8 : nullptr, a.q8d, a.qkv, B, op_qkv);
         } else {
-            gemm(L.q, n_, q8mode ? q8_ : nullptr, q8d_, lay.q, B, op_qkv);
-            gemm(L.k, n_, q8mode ? q8_ : nullptr, q8d_, lay.k, B, op_qkv);
-            gemm(L.v, n_, q8mode ? q8_ : nullptr, q8d_, lay.v, B, op_qkv);
+            gemm(L.q, a.n, q8mode ? a.q8 : nullptr, a.q8d, lay.q, B, op_qkv);
+            gemm(L.k, a.n, q8mode ? a.q8 : nullptr, a.q8d, lay.k, B, op_qkv);
+            gemm(L.v, a.n, q8mode ? a.q8 : nullptr, a.q8d, lay.v, B, op_qkv);
         }
         void* const* pk = pt_k_ + li * max_pages_;
         void* const* pv = pt_v_ + li * max_pages_;
         store_kv(lay, pk, pv, nullptr, pos_, B);
+        // the next chunk's attention of this layer reads these rows; this
+        // chunk's reads the previous chunk's
+        check(hipEventRecord(kv_done_[lane * c_.n_layer + li], a.st), "event record");
+        if (prev_lane >= 0)
+            check(hipStreamWaitEvent(a.st, kv_done_[prev_lane * c_.n_layer + li], 0), "event wait");
         // the softmax-V kernel also writes the o projection's Q8 activations
         // (32-element head slices are Q8 blocks), in the MFMA GEMM's operand
         // order when the projection runs there
         const bool o_q8 = q8mode && L.o.type == 2 && hd % 32 == 0 && L.o.cols == c_.n_head * hd;
         const bool o_op = o_q8 && mfma_gemm(L.o);
         if (hd % 32 == 0) {  // scores + softmax once per (token, head), V tiles shared by the chunk's tokens
-            check(mvh::launch_attn_prefill(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, o_q8 ? q8_ : nullptr,
-                                           q8d_,
+            check(mvh::launch_attn_prefill(kv_type_, pk, pv, lay.q, lay.q_pitch, a.scores, a.att, o_q8 ? a.q8 : nullptr,
+                                           a.q8d,
                                            o_op, nullptr, pos_, pos_ + B, B, c_.n_head, c_.n_head_kv, hd,
-                                           c_.kv_dim(), page_tokens_, stream_),
+                                           c_.kv_dim(), page_tokens_, a.st),
                   "attention");
         } else {
-            check(mvh::launch_attn(kv_type_, pk, pv, lay.q, lay.q_pitch, scores_, att_, nullptr, pos_, pos_ + B, B,
+            check(mvh::launch_attn(kv_type_, pk, pv, lay.q, lay.q_pitch, a.scores, a.att, nullptr, pos_, pos_ + B, B,
                                    c_.n_head,
-                                   c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, stream_, o_q8 ? q8_ : nullptr, q8d_,
+                                   c_.n_head_kv, hd, c_.kv_dim(), page_tokens_, a.st, o_q8 ? a.q8 : nullptr, a.q8d,
                                    o_op),
                   "attention");
         }
-        gemm(L.o, att_, o_q8 ? q8_ : nullptr, q8d_, proj_, B, o_op);
-        check(mvh::launch_rmsnorm(x_, proj_, L.ffn_norm, n_, q8mode ? q8_ : nullptr, q8d_, B, D, c_.rms_eps, stream_,
+        gemm(L.o, a.att, o_q8 ? a.q8 : nullptr, a.q8d, a.proj, B, o_op);
+        check(mvh::launch_rmsnorm(a.x, a.proj, L.ffn_norm, a.n, q8mode ? a.q8 : nullptr, a.q8d, B, D, c_.rms_eps, a.st,
                                   op_gu),
               "rmsnorm");
-        float* g = gu_;
-        float* u = L.fused_gu ? gu_ + F : gu_ + B * F;
+        float* g = a.gu;
+        float* u = L.fused_gu ? a.gu + F : a.gu + B * F;
         const std::size_t pitch = L.fused_gu ? 2 * F : F;
         if (L.fused_gu) {
-            gemm(L.gate_up, n_, q8mode ? q8_ : nullptr, q8d_, gu_, B, op_gu);
+            gemm(L.gate_up, a.n, q8mode ? a.q8 : nullptr, a.q8d, a.gu, B, op_gu);
         } else {
-            gemm(L.gate, n_, q8mode ? q8_ : nullptr, q8d_, g, B, op_gu);
-            gemm(L.up, n_, q8mode ? q8_ : nullptr, q8d_, u, B, op_gu);
+            gemm(L.gate, a.n, q8mode ? a.q8 : nullptr, a.q8d, g, B, op_gu);
+            gemm(L.up, a.n, q8mode ? a.q8 : nullptr, a.q8d, u, B, op_gu);
         }
-        check(mvh::launch_swiglu(g, u, pitch, ff_, q8mode ? q8_ : nullptr, q8d_, B, F, stream_, op_down), "swiglu");
-        gemm(L.down, ff_, q8mode ? q8_ : nullptr, q8d_, ffo_, B, op_down);
+        check(mvh::launch_swiglu(g, u, pitch, a.ff, q8mode ? a.q8 : nullptr, a.q8d, B, F, a.st, op_down), "swiglu");
+        gemm(L.down, a.ff, q8mode ? a.q8 : nullptr, a.q8d, a.ffo, B, op_down);
     }
     if (logits) {
-        float* xl = x_ + (B - 1) * D;
-        check(mvh::launch_rmsnorm(xl, ffo_ + (B - 1) * D, out_norm_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, 1, D,
-                                  c_.rms_eps, stream_),
+        float* xl = a.x + (B - 1) * D;
+        check(mvh::launch_rmsnorm(xl, a.ffo + (B - 1) * D, out_norm_, a.n, out_.type == 2 ? a.q8 : nullptr, a.q8d, 1, D,
+                                  c_.rms_eps, a.st),
               "rmsnorm");
-        gemv(out_, n_, out_.type == 2 ? q8_ : nullptr, q8d_, logits_d_);
+        gemv(out_, a.n, out_.type == 2 ? a.q8 : nullptr, a.q8d, logits_d_);
     }
 }
 
@@ -523,35 +541,36 @@ void LlamaModel::store_kv(const QkvLayout& lay, void* const* pk, void* const* pv
     const bool fused = kv_type_ != mvh::kKvQ8;
     check(mvh::launch_rope_kv(lay.q, lay.q_pitch, lay.k, lay.v, lay.kv_pitch, rope_cos_, rope_sin_, d_pos, pos, B,
                               c_.n_head, c_.n_head_kv, c_.head_dim(), kv_type_, fused ? pk : nullptr,
-                              fused ? pv : nullptr, page_tokens_, stream_),
+                              fused ? pv : nullptr, page_tokens_, ln_->st),
           "rope/kv");
     if (!fused)
         check(mvh::launch_kv_write(kv_type_, pk, pv, lay.k, lay.v, lay.kv_pitch, d_pos, pos, B, c_.kv_dim(),
-                                   page_tokens_, stream_),
+                                   page_tokens_, ln_->st),
               "kv write");
 }
 
 const std::vector<float>& LlamaModel::logits() {
-    check(hipMemcpyAsync(logits_.data(), logits_d_, c_.vocab * 4, hipMemcpyDeviceToHost, stream_), "logits copy");
-    check(hipStreamSynchronize(stream_), "sync");
+    check(hipMemcpyAsync(logits_.data(), logits_d_, c_.vocab * 4, hipMemcpyDeviceToHost, ln_->st), "logits copy");
+    check(hipStreamSynchronize(ln_->st), "sync");
     return logits_;
 }
 
 const std::vector<float>& LlamaModel::forward(int token, bool compute_logits) {
+    ln_ = &lanes_[0];
     if (token < 0 || static_cast<std::size_t>(token) >= c_.vocab) throw std::runtime_error("token id out of range");
     if (pos_ >= c_.n_ctx) throw std::runtime_error("context exhausted");
     check(hipSetDevice(device_), "hipSetDevice");
     pin_[0] = token;
     pin_[1] = static_cast<int>(pos_);
-    check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, stream_), "token upload");
-    check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, stream_), "pos upload");
+    check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, ln_->st), "token upload");
+    check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, ln_->st), "pos upload");
     profiling_ = prof::enabled();
     decode_step(d_tok_, compute_logits, false);
     prof_flush();
     ++pos_;
     kv_hi_ = std::max(kv_hi_, pos_);
     if (compute_logits) return logits();
-    check(hipStreamSynchronize(stream_), "sync");
+    check(hipStreamSynchronize(ln_->st), "sync");
     return logits_;
 }
 
@@ -561,27 +580,46 @@ const std::vector<float>& LlamaModel::prefill(const std::vector<int>& tokens, st
     batch_size = std::max<std::size_t>(1, batch_size);
     if (batch_size > max_batch_) throw std::runtime_error("prefill batch larger than the model's max_batch");
     check(hipSetDevice(device_), "hipSetDevice");
-    for (std::size_t i = 0; i < tokens.size(); i += batch_size) {
+    // chunks take the lanes in turn (one lane while profiling: the profiler's
+    // events live on lane 0); a chunk's tokens are staged at its own offset,
+    // so no staging slot is reused before the final sync
+    profiling_ = prof::enabled();
+    const int lanes = profiling_ ? 1 : kLanes;
+    int prev = -1;
+    std::size_t chunk = 0;
+    auto drain = [&] {
+        for (Lane& l : lanes_) check(hipStreamSynchronize(l.st), "sync");
+        ln_ = &lanes_[0];
+    };
+    for (std::size_t i = 0; i < tokens.size(); i += batch_size, ++chunk) {
         const std::size_t B = std::min(batch_size, tokens.size() - i);
-        if (pos_ + B > c_.n_ctx) throw std::runtime_error("context exhausted");
-        for (std::size_t b = 0; b < B; ++b)
-            if (tokens[i + b] < 0 || static_cast<std::size_t>(tokens[i + b]) >= c_.vocab)
-                throw std::runtime_error("token id out of range");
+        const char* err = nullptr;
+        if (pos_ + B > c_.n_ctx) err = "context exhausted";
+        for (std::size_t b = 0; b < B && !err; ++b)
+            if (tokens[i + b] < 0 || static_cast<std::size_t>(tokens[i + b]) >= c_.vocab) err = "token id out of range";
+        if (err) {  // the chunks before this one complete, as in a chunk-by-chunk run
+            drain();
+            throw std::runtime_error(err);
+        }
         const bool last = compute_logits_last && i + B == tokens.size();
-        std::memcpy(pin_, tokens.data() + i, B * 4);
-        check(hipMemcpyAsync(d_toks_, pin_, B * 4, hipMemcpyHostToDevice, stream_), "token upload");
-        profiling_ = prof::enabled();
-        batch_step(d_toks_, B, last);
+        const int lane = static_cast<int>(chunk % lanes);
+        ln_ = &lanes_[lane];
+        std::memcpy(pin_ + i, tokens.data() + i, B * 4);
+        check(hipMemcpyAsync(d_prompt_ + i, pin_ + i, B * 4, hipMemcpyHostToDevice, ln_->st), "token upload");
+        batch_step(d_prompt_ + i, B, last, lanes > 1 ? prev : -1);
         prof_flush();
-        check(hipStreamSynchronize(stream_), "sync");  // pin_ is reused by the next chunk
+        prev = lane;
         pos_ += B;
         kv_hi_ = std::max(kv_hi_, pos_);
-        if (last) logits();
+        if (last) check(hipMemcpyAsync(logits_.data(), logits_d_, c_.vocab * 4, hipMemcpyDeviceToHost, ln_->st),
+                        "logits copy");
     }
+    drain();
     return logits_;
 }
 
 std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
+    ln_ = &lanes_[0];
     if (token < 0 || static_cast<std::size_t>(token) >= c_.vocab) throw std::runtime_error("token id out of range");
     if (pos_ + n > c_.n_ctx) throw std::runtime_error("context exhausted");
     std::vector<int> out(n);
@@ -589,8 +627,8 @@ std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
     check(hipSetDevice(device_), "hipSetDevice");
     pin_[0] = token;
     pin_[1] = static_cast<int>(pos_);
-    check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, stream_), "token upload");
-    check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, stream_), "pos upload");
+    check(hipMemcpyAsync(d_tok_, &pin_[0], 4, hipMemcpyHostToDevice, ln_->st), "token upload");
+    check(hipMemcpyAsync(d_pos_, &pin_[1], 4, hipMemcpyHostToDevice, ln_->st), "pos upload");
     profiling_ = prof::enabled();
     if (profiling_) {
         // the same steps without the graph, so every GEMV can be timed
@@ -603,16 +641,16 @@ std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
         // writes the next token and advances the position: one graph serves
         // every step
         hipGraph_t g{};
-        check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+        check(hipStreamBeginCapture(ln_->st, hipStreamCaptureModeThreadLocal), "begin capture");
         decode_step(d_tok_, true, true);
-        check(hipStreamEndCapture(stream_, &g), "end capture");
+        check(hipStreamEndCapture(ln_->st, &g), "end capture");
         check(hipGraphInstantiate(&graph_, g, nullptr, nullptr, 0), "graph instantiate");
         (void)hipGraphDestroy(g);
     }
     if (!profiling_)
-        for (std::size_t i = 0; i < n; ++i) check(hipGraphLaunch(graph_, stream_), "graph launch");
-    check(hipMemcpyAsync(pin_, d_hist_ + pos_, n * 4, hipMemcpyDeviceToHost, stream_), "token copy");
-    check(hipStreamSynchronize(stream_), "sync");
+        for (std::size_t i = 0; i < n; ++i) check(hipGraphLaunch(graph_, ln_->st), "graph launch");
+    check(hipMemcpyAsync(pin_, d_hist_ + pos_, n * 4, hipMemcpyDeviceToHost, ln_->st), "token copy");
+    check(hipStreamSynchronize(ln_->st), "sync");
     std::memcpy(out.data(), pin_, n * 4);
     pos_ += n;
     kv_hi_ = std::max(kv_hi_, pos_);

@@ -51,7 +51,7 @@ public:
     std::size_t position() const { return pos_; }
     std::size_t kv_bytes_allocated() const;
     int kv_type() const { return kv_type_; }
-    hipStream_t stream() const { return stream_; }
+    hipStream_t stream() const { return lanes_[0].st; }
     const std::vector<float>& logits();  // copies the device logits of the last step
 
 private:
@@ -90,13 +90,33 @@ private:
     void decode_step(const int* d_token, bool logits, bool argmax);
     void store_kv(const QkvLayout& lay, void* const* pk, void* const* pv, const int* d_pos, std::size_t pos,
                   std::size_t B);
-    void batch_step(const int* tokens, std::size_t B, bool logits);
+    // one prefill chunk on lane ln_; prev_lane >= 0: the previous chunk runs on
+    // that lane and this chunk's attention of layer l waits for its KV of layer l
+    void batch_step(const int* tokens, std::size_t B, bool logits, int prev_lane = -1);
     void check(hipError_t e, const char* what) const;
+
+    // A lane: a stream and the activation buffers of one step in flight
+    // ([max_batch][...] for prefill; row 0 for decode).  Decode runs on lane 0;
+    // consecutive prefill chunks take the lanes in turn, so chunk c + 1
+    // computes layer l while chunk c computes layer l + 1.
+    struct Lane {
+        hipStream_t st{};
+        float *x{}, *n{}, *qkv{}, *att{}, *proj{}, *gu{}, *ff{}, *scores{};
+        float* ffo{};  // down-projection output (the residual added by the next norm)
+        int8_t *q8{}, *q8s{};
+        float *q8d{}, *q8sd{};
+        int* q8ss{};  // block sums written by the stand-alone quantizer
+    };
 
     std::unique_ptr<GgufFile> file_;
     LlamaConfig c_;
     int device_{};
-    hipStream_t stream_{};
+    // three lanes: pp512 of the 7B shape 7.55 K (one) / 10.3 K (two) / 11.1 K
+    // (three) / 10.1 K (four) tok/s; GPU_MAX_HW_QUEUES is 4
+    static constexpr int kLanes = 3;
+    Lane lanes_[kLanes];
+    Lane* ln_{&lanes_[0]};             // the lane the step helpers launch on
+    std::vector<hipEvent_t> kv_done_;  // [lane][layer]: the KV rows of the lane's chunk at that layer are written
     int kv_type_{1};
     PrefillMode mode_;
     std::size_t page_tokens_{}, max_pages_{}, max_batch_{}, pos_{}, kv_hi_{};
@@ -111,13 +131,9 @@ private:
     float* rope_cur_{};                  // cos/sin row of the decode position (written by the embedding launch)
     uint8_t *kslab_{}, *vslab_{};        // every layer's KV pages, page i of layer l at slab + (l * max_pages_ + i) * kv_stride_
     std::size_t kv_stride_{};
-    // activations ([max_batch][...] for prefill; row 0 for decode)
-    float *x_{}, *n_{}, *qkv_{}, *att_{}, *proj_{}, *gu_{}, *ff_{}, *logits_d_{}, *scores_{};
-    float* ffo_{};       // down-projection output (the residual added by the next norm)
-    int8_t *q8_{}, *q8s_{};
-    float *q8d_{}, *q8sd_{};
-    int* q8ss_{};        // block sums written by the stand-alone quantizer
-    int *d_tok_{}, *d_pos_{}, *d_toks_{}, *d_hist_{};  // d_hist_[p] = greedy token sampled at position p
+    float* logits_d_{};
+    int *d_tok_{}, *d_pos_{}, *d_hist_{};  // d_hist_[p] = greedy token sampled at position p
+    int* d_prompt_{};                       // token ids of a prefill call, chunk i's at d_prompt_ + i
     int* pin_{};         // pinned host staging
     std::vector<float> logits_;
     hipGraphExec_t graph_{};

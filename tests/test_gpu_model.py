@@ -79,6 +79,50 @@ def test_model_errors(tiny):
     m.close()
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("kv", [capi.MVH_KV_F16, capi.MVH_KV_Q8])
+def test_pipelined_prefill_equals_chunk_by_chunk(tiny, mode, kv):
+    """The chunks of one prefill call take three streams in turn (chunk c + 1
+    computes layer l beside chunk c's layer l + 1, its attention of layer l
+    ordered after chunk c's KV write of layer l).  Logits, KV bytes and the
+    greedy ids that follow must be bit-identical to one call per chunk, where
+    nothing runs beside a chunk."""
+    prompt = synth.prompt_tokens(9, 150)  # four full chunks of 32 and a ragged 22: the lanes wrap
+    runs = []
+    for split in (False, True):
+        m = capi.Model(tiny, ctx=256, act_mode=mode, max_batch=32, kv_type=kv)
+        if split:
+            for i in range(0, len(prompt), 32):
+                lg = m.prefill(prompt[i:i + 32], 32, logits=i + 32 >= len(prompt))
+        else:
+            lg = m.prefill(prompt, 32)
+        runs.append((lg.copy(), m.kv_bytes(), m.position, m.generate_greedy(17, 6).tolist()))
+        m.close()
+    (a, kb_a, pos_a, ids_a), (b, kb_b, pos_b, ids_b) = runs
+    assert (bits(a) == bits(b)).all()
+    assert (kb_a, pos_a, ids_a) == (kb_b, pos_b, ids_b)
+
+
+def test_pipelined_prefill_error_completes_earlier_chunks(tiny):
+    """A bad token id in the third chunk: the two chunks before it complete (as
+    in a chunk-by-chunk run), the position stops after them, and decoding from
+    there equals decoding after a prefill of just those two chunks."""
+    prompt = synth.prompt_tokens(4, 96)
+    bad = prompt.copy()
+    bad[70] = 32000
+    m = capi.Model(tiny, ctx=256, max_batch=32)
+    with pytest.raises(capi.MvhError, match="token id out of range"):
+        m.prefill(bad, 32)
+    assert m.position == 64
+    got = m.forward(5)
+    ref = capi.Model(tiny, ctx=256, max_batch=32)
+    ref.prefill(prompt[:64], 32, logits=False)
+    want = ref.forward(5)
+    assert (bits(got) == bits(want)).all()
+    m.close()
+    ref.close()
+
+
 @pytest.mark.parametrize("cfg_name", ["tinyllama-1.1b-mixed-2layer", "openllama-7b-v2-q4_0-1layer"])
 @pytest.mark.parametrize("mode", [0, 1])
 def test_large_shapes_vs_oracle(tmp_path, oracle, cfg_name, mode):
