@@ -247,7 +247,10 @@ int mvh_model_config(const mvh_model* m, size_t out[7]);
 int mvh_model_reset(mvh_model* m);
 /* LlamaModel::forward: one decode step; logits (host, vocab floats) may be NULL */
 int mvh_model_forward(mvh_model* m, int token, float* logits);
-/* LlamaModel::prefill: chunks of `batch`; logits of the last token when logits != NULL */
+/* LlamaModel::prefill: chunks of `batch`; logits of the last token when logits != NULL.  Consecutive chunks
+ * run on three internal streams (chunk c + 1's layer l beside chunk c's layer l + 1, results identical to a
+ * chunk-by-chunk run); every stream is drained before the call returns, also when a later chunk's error is
+ * returned after the earlier chunks completed */
 int mvh_model_prefill(mvh_model* m, const int* tokens, size_t n, size_t batch, float* logits);
 /* n greedy decode steps from `token`, run on the device from one HIP graph (the argmax of each step
  * feeds the next); out_tokens (host) receives the n sampled ids, last_logits (host) may be NULL */
@@ -255,6 +258,7 @@ int mvh_model_generate_greedy(mvh_model* m, int token, size_t n, int* out_tokens
 int mvh_model_position(const mvh_model* m, size_t* pos);
 int mvh_model_kv_bytes(const mvh_model* m, size_t* bytes);
 int mvh_model_kv_type(const mvh_model* m, int* kv_type); /* LlamaModel::kv_type */
+/* the stream decode steps run on (prefill's first lane) */
 int mvh_model_stream(mvh_model* m, void** stream);
 
 #ifdef __cplusplus
