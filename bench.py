@@ -178,6 +178,38 @@ def time_gemv_kernels(ctx, mats, launches: int, rotate_mb: float):
     return out
 
 
+def time_gemm_streams(ctx, ts, x, reps: int, lanes: int) -> float:
+    """us per GEMM with `lanes` independent chains of reps GEMMs (own context, stream and
+    output each) started together: the prefill's operating point, where consecutive chunks
+    run on three streams and their M = 32 GEMMs overlap."""
+    import torch
+
+    from memvanta_amd import capi
+
+    ctxs = [ctx] + [capi.Context(ctx.device) for _ in range(lanes - 1)]
+    streams = [torch.cuda.ExternalStream(c.stream) for c in ctxs]
+    ys = [torch.empty((x.shape[0], ts[0].ne1), dtype=torch.float32, device="cuda") for _ in ctxs]
+    for c, y in zip(ctxs, ys):
+        c.matmul_batch_v06(ts[0], x, capi.MVH_ACT_Q8, y=y)  # warm-up (each context's quantizer scratch)
+        c.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(streams[0])
+    for st in streams[1:]:
+        st.wait_event(start)
+    for r in range(reps):
+        for i, (c, y) in enumerate(zip(ctxs, ys)):
+            c.matmul_batch_v06(ts[(r * lanes + i) % len(ts)], x, capi.MVH_ACT_Q8, y=y)
+    for st in streams[1:]:
+        done = torch.cuda.Event()
+        done.record(st)
+        streams[0].wait_event(done)
+    stop.record(streams[0])
+    stop.synchronize()
+    for c in ctxs[1:]:
+        c.close()
+    return start.elapsed_time(stop) * 1e3 / (reps * lanes)
+
+
 def time_prefill_gemm(ctx, mats, reps: int, rotate_mb: float):
     """Q4_0 x Q8 prefill GEMM (int8 MFMA) at the GEMM config shapes: us, TOP/s, GB/s."""
     import numpy as np
@@ -206,9 +238,11 @@ def time_prefill_gemm(ctx, mats, reps: int, rotate_mb: float):
             us = a.elapsed_time(b) * 1e3 / reps
             ops = 2.0 * m * n * k
             byts = n * (k // 32) * 18 + m * (k + k // 8) + 4 * m * n
-            out.append({"K": k, "N": n, "M": m, "us": round(us, 2), "TOP/s": round(ops / us / 1e6, 2),
-                        "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
-                        "GB/s": round(byts / us / 1e3, 1)})
+            e = {"K": k, "N": n, "M": m, "us": round(us, 2), "TOP/s": round(ops / us / 1e6, 2),
+                 "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4), "GB/s": round(byts / us / 1e3, 1)}
+            if m == BATCH:
+                e["us_per_gemm_3_streams"] = round(time_gemm_streams(ctx, ts, x, reps, 3), 2)
+            out.append(e)
         for t in ts:
             t.free()
     return out
@@ -863,7 +897,10 @@ def main():
             "gemv_kernel_per_shape": per_shape,
             "prefill_gemm_int8_mfma": gemm,
             "prefill_gemm_note": "tensor_matmul_batch_v06 FORCE_Q8 numerics incl. the activation quantizer; "
-                                 "frac_int8_peak vs 5 POP/s dense int8",
+                                 "frac_int8_peak vs 5 POP/s dense int8; us: one GEMM at a time; "
+                                 "us_per_gemm_3_streams (M = 32): three independent chains of the same GEMM, "
+                                 "each on its own stream, started together (the three-stream prefill's "
+                                 "operating point)",
             "prefill_roofline": prefill_roofline(gemm),
             "other_kv_cache_types": kv_types,
             "other_models": others,
