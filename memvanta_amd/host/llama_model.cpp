@@ -471,11 +471,13 @@ void LlamaModel::batch_step(const int* d_tokens, std::size_t B, bool logits, int
         void* const* pk = pt_k_ + li * max_pages_;
         void* const* pv = pt_v_ + li * max_pages_;
         store_kv(lay, pk, pv, nullptr, pos_, B);
-        // the next chunk's attention of this layer reads these rows; this
-        // chunk's reads the previous chunk's
-        check(hipEventRecord(kv_done_[lane * c_.n_layer + li], a.st), "event record");
+        // this chunk's attention of the layer reads the rows of every earlier
+        // chunk: it waits for the previous chunk's event, and records its own
+        // only after that wait, so the event of chunk c stands for the rows
+        // of chunks 0..c (with three lanes chunk c - 2 runs on a third stream)
         if (prev_lane >= 0)
             check(hipStreamWaitEvent(a.st, kv_done_[prev_lane * c_.n_layer + li], 0), "event wait");
+        check(hipEventRecord(kv_done_[lane * c_.n_layer + li], a.st), "event record");
         // the softmax-V kernel also writes the o projection's Q8 activations
         // (32-element head slices are Q8 blocks), in the MFMA GEMM's operand
         // order when the projection runs there

@@ -79,23 +79,26 @@ def test_model_errors(tiny):
     m.close()
 
 
+@pytest.mark.parametrize("n_prompt,chunk", [(150, 32), (230, 16)])
 @pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("kv", [capi.MVH_KV_F16, capi.MVH_KV_Q8])
-def test_pipelined_prefill_equals_chunk_by_chunk(tiny, mode, kv):
+def test_pipelined_prefill_equals_chunk_by_chunk(tiny, mode, kv, n_prompt, chunk):
     """The chunks of one prefill call take three streams in turn (chunk c + 1
     computes layer l beside chunk c's layer l + 1, its attention of layer l
-    ordered after chunk c's KV write of layer l).  Logits, KV bytes and the
-    greedy ids that follow must be bit-identical to one call per chunk, where
-    nothing runs beside a chunk."""
-    prompt = synth.prompt_tokens(9, 150)  # four full chunks of 32 and a ragged 22: the lanes wrap
+    ordered after the KV writes of layer l of every earlier chunk).  Logits,
+    KV bytes and the greedy ids that follow must be bit-identical to one call
+    per chunk, where nothing runs beside a chunk.  150 / 32: four full chunks
+    and a ragged 22, the lanes wrap once; 230 / 16: fifteen chunks, the
+    lanes wrap four times."""
+    prompt = synth.prompt_tokens(9, n_prompt)
     runs = []
     for split in (False, True):
         m = capi.Model(tiny, ctx=256, act_mode=mode, max_batch=32, kv_type=kv)
         if split:
-            for i in range(0, len(prompt), 32):
-                lg = m.prefill(prompt[i:i + 32], 32, logits=i + 32 >= len(prompt))
+            for i in range(0, len(prompt), chunk):
+                lg = m.prefill(prompt[i:i + chunk], chunk, logits=i + chunk >= len(prompt))
         else:
-            lg = m.prefill(prompt, 32)
+            lg = m.prefill(prompt, chunk)
         runs.append((lg.copy(), m.kv_bytes(), m.position, m.generate_greedy(17, 6).tolist()))
         m.close()
     (a, kb_a, pos_a, ids_a), (b, kb_b, pos_b, ids_b) = runs
