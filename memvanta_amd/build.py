@@ -52,7 +52,7 @@ def build_oracle(with_ref: bool | None = None) -> None:
         targets.append("ref")
     _run(["make", "-C", os.path.join(ROOT, "oracle"), "-j4", *targets])
     if with_ref and os.path.exists(LIB):
-        # the reference-side integration check (INTEGRATION.md's shim, compiled as printed)
+        # the reference-side integration check (the integration guide's shim, compiled as printed)
         _run([sys.executable, os.path.join(ROOT, "oracle", "shim_build.py")])
 
 

@@ -1,6 +1,6 @@
 """Builds the reference-side integration check -- TEST INFRASTRUCTURE ONLY.
 
-Extracts the shim that INTEGRATION.md prints (the ```cpp block headed
+Extracts the shim that the integration guide prints (the ```cpp block headed
 ``// src/gguf_kernels_hip.cpp``) into _ref/gguf_kernels_hip.cpp, then compiles
 shim_check.cpp, which includes it, against the reference checkout's headers
 and links it with the reference compiled from its sources (_ref/libmvref.so,

@@ -1,6 +1,6 @@
 // shim_check -- TEST INFRASTRUCTURE ONLY (never the product).
 //
-// Compiles the reference-side shim exactly as INTEGRATION.md prints it
+// Compiles the reference-side shim exactly as the integration guide prints it
 // (extracted to _ref/gguf_kernels_hip.cpp by shim_build.py) against the
 // reference's own headers, checks at compile time that every shim function
 // has the signature of the reference function it replaces

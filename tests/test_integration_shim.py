@@ -1,6 +1,6 @@
-"""The reference-side shim of INTEGRATION.md, compiled as printed there.
+"""The reference-side shim of the integration guide, compiled as printed there.
 
-CPU: the shim text is extracted from INTEGRATION.md, compiled against the
+CPU: the shim text is extracted from the integration guide, compiled against the
 reference checkout's own headers (include/memvanta/gguf_kernels.hpp) with
 compile-time checks that each shim function has the signature of the
 reference function it replaces, and linked with libmemvanta_hip.so and the
