@@ -79,7 +79,7 @@ def test_model_errors(tiny):
     m.close()
 
 
-@pytest.mark.parametrize("n_prompt,chunk", [(150, 32), (230, 16)])
+@pytest.mark.parametrize("n_prompt,chunk", [(150, 32), (230, 16), (77, 5), (24, 1)])
 @pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("kv", [capi.MVH_KV_F16, capi.MVH_KV_Q8])
 def test_pipelined_prefill_equals_chunk_by_chunk(tiny, mode, kv, n_prompt, chunk):
@@ -89,7 +89,8 @@ def test_pipelined_prefill_equals_chunk_by_chunk(tiny, mode, kv, n_prompt, chunk
     KV bytes and the greedy ids that follow must be bit-identical to one call
     per chunk, where nothing runs beside a chunk.  150 / 32: four full chunks
     and a ragged 22, the lanes wrap once; 230 / 16: fifteen chunks, the
-    lanes wrap four times."""
+    lanes wrap four times; 77 / 5: chunks that are not whole 16-token GEMM
+    slabs; 24 / 1: one-token chunks (the per-token matmul path)."""
     prompt = synth.prompt_tokens(9, n_prompt)
     runs = []
     for split in (False, True):
