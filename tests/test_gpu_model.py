@@ -81,7 +81,7 @@ def test_model_errors(tiny):
 
 @pytest.mark.parametrize("n_prompt,chunk", [(150, 32), (230, 16), (77, 5), (24, 1)])
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("kv", [capi.MVH_KV_F16, capi.MVH_KV_Q8])
+@pytest.mark.parametrize("kv", [capi.MVH_KV_F16, capi.MVH_KV_Q8, capi.MVH_KV_F32])
 def test_pipelined_prefill_equals_chunk_by_chunk(tiny, mode, kv, n_prompt, chunk):
     """The chunks of one prefill call take three streams in turn (chunk c + 1
     computes layer l beside chunk c's layer l + 1, its attention of layer l
@@ -105,6 +105,29 @@ def test_pipelined_prefill_equals_chunk_by_chunk(tiny, mode, kv, n_prompt, chunk
     (a, kb_a, pos_a, ids_a), (b, kb_b, pos_b, ids_b) = runs
     assert (bits(a) == bits(b)).all()
     assert (kb_a, pos_a, ids_a) == (kb_b, pos_b, ids_b)
+
+
+@pytest.mark.parametrize("chunk", [32, 16])
+def test_pipelined_prefill_equals_chunk_by_chunk_hd128(tmp_path, chunk):
+    """As above on a one-layer 7B-shape model (head_dim 128: the chunked
+    scores/softmax + value kernels and the int8-MFMA GEMM in every chunk)."""
+    cfg = synth.dataclasses.replace(synth.LLAMA7B_1L, name="openllama-7b-v2-q4_0-1layer-pipe", ctx=256)
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=41)
+    prompt = synth.prompt_tokens(12, 120)
+    runs = []
+    for split in (False, True):
+        m = capi.Model(path, ctx=256, act_mode=1, max_batch=32)
+        if split:
+            for i in range(0, len(prompt), chunk):
+                lg = m.prefill(prompt[i:i + chunk], chunk, logits=i + chunk >= len(prompt))
+        else:
+            lg = m.prefill(prompt, chunk)
+        runs.append((lg.copy(), m.kv_bytes(), m.generate_greedy(3, 4).tolist()))
+        m.close()
+    (a, kb_a, ids_a), (b, kb_b, ids_b) = runs
+    assert (bits(a) == bits(b)).all()
+    assert (kb_a, ids_a) == (kb_b, ids_b)
 
 
 def test_pipelined_prefill_error_completes_earlier_chunks(tiny):
