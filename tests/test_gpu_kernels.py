@@ -349,7 +349,8 @@ def test_matmul_batch_fallback(ctx, oracle, ty, k):
     t.free()
 
 
-@pytest.mark.parametrize("ty,k", [(synth.Q4_0, 288), (synth.Q8_0, 4096), (synth.Q6_K, 2048)])
+@pytest.mark.parametrize("ty,k", [(synth.Q4_0, 288), (synth.Q8_0, 4096), (synth.Q6_K, 2048), (synth.F32, 100),
+                                  (synth.F16, 300)])
 def test_read_row(ctx, oracle, ty, k):
     rng = np.random.default_rng(k)
     n = 50
