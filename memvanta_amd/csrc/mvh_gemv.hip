@@ -698,6 +698,152 @@ __global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* 
     }
 }
 
+// q4/q8_row_batch4_fp32 numerics (src/gguf_kernels.cpp:191-216) for Q4_0 and
+// Q8_0 with K % 256 == 0, each activation read feeding two rows: lane (row
+// pair, j) owns accumulator j of two rows for kR2T tokens, elements j, j+8,
+// j+16, j+24 of every block in that order (the reference's 8-wide vector
+// lane j).  A workgroup covers 32 rows x 2*kR2T tokens; per 8-block unit it
+// stages the 32 rows' raw bytes (one copy, 16-byte loads) and the activations
+// ([token][block][j][m], as batch_f32act_lanes_kernel) in LDS, double
+// buffered.  Lane j reads its four weights of a block and the f16 scale:
+// Q4_0 bytes j and j+8 of the nibbles, float(q - 8) * d with q - 8 formed
+// exactly in float; Q8_0 bytes j, j+8, j+16, j+24, float(q) * d.  Each row's
+// t0 + t1 + ... + t7 then runs in order through LDS.  Against
+// batch_f32act_lanes_kernel: fewer VALU instructions per fma (the eight lanes
+// of a row no longer each unpack the whole unit from registers) and half the
+// activation reads from LDS per fma.
+constexpr int kR2T = 8;       // tokens per thread (16 measured slower: 214 VGPRs, half the workgroups)
+constexpr int kR2Rows = 32;   // rows per workgroup
+constexpr int kR2Tok = 2 * kR2T;
+
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* __restrict__ W,
+                                                                 const float* __restrict__ x,
+                                                                 float* __restrict__ y, int N, int nb) {
+    constexpr int kB = Blk<TYPE>::kBytes;     // 18 or 34
+    constexpr int kU = 8 * kB;                // bytes of an 8-block unit of one row (144 or 272)
+    constexpr int kP = kU / 16;               // 16-byte pieces per row and unit (9 or 17)
+    constexpr int kNP = (kR2Rows * kP + 255) / 256;  // pieces per thread (2 or 3)
+    __shared__ __align__(16) uint8_t s_w[2][kR2Rows * kU + 16];  // + a 16-byte slot for unused stores
+    __shared__ __align__(16) float s_x[2][kR2Tok * kBChunk];     // [token][block][j][m]
+    const int t = threadIdx.x, j = t & 7, slot = t >> 3;
+    const int rp = slot & 15, tg = slot >> 4;  // rows 2rp, 2rp+1; tokens tg*kR2T ..
+    const int row0 = blockIdx.x * kR2Rows;
+    const int tok0 = blockIdx.y * kR2Tok;
+    const int K = nb * 32, units = nb / 8;
+    const size_t row_bytes = static_cast<size_t>(nb) * kB;
+
+    // staging of unit c: pieces t + 256 i of the 32 rows' 16-byte pieces (row
+    // p / kP, bytes 16 (p % kP); pieces past the last load it again and store
+    // to the spare slot); kR2Tok * 64 float4 of activations, kXs per thread
+    constexpr int kXs = kR2Tok * kBChunk / 4 / 256;
+    const uint8_t* wsrc[kNP];
+    int wdst[kNP];
+#pragma unroll
+    for (int i = 0; i < kNP; ++i) {
+        const int p = t + 256 * i, pc = min(p, kR2Rows * kP - 1);
+        wsrc[i] = W + static_cast<size_t>(min(row0 + pc / kP, N - 1)) * row_bytes + 16 * (pc % kP);
+        wdst[i] = p < kR2Rows * kP ? (pc / kP) * kU + 16 * (pc % kP) : kR2Rows * kU;
+    }
+    auto stage_load = [&](int c, uint4 (&w)[kNP], float4 (&v)[kXs]) {
+#pragma unroll
+        for (int i = 0; i < kNP; ++i) w[i] = *reinterpret_cast<const uint4*>(wsrc[i] + static_cast<size_t>(c) * kU);
+#pragma unroll
+        for (int k = 0; k < kXs; ++k) {
+            const int f = t + 256 * k;  // token f / 64, element 4 (f % 64)
+            v[k] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(tok0 + (f >> 6)) * K + c * kBChunk +
+                                                    4 * (f & 63));
+        }
+    };
+    auto stage_store = [&](const uint4 (&w)[kNP], const float4 (&v)[kXs], int buf) {
+#pragma unroll
+        for (int i = 0; i < kNP; ++i) *reinterpret_cast<uint4*>(&s_w[buf][wdst[i]]) = w[i];
+#pragma unroll
+        for (int k = 0; k < kXs; ++k) {
+            const int f = t + 256 * k;
+            const int tk = f >> 6, e = 4 * (f & 63);
+            const float vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // element e+i: block (e+i)/32, lane (e+i)%8, m = ((e+i)%32)/8
+                const int ei = e + i;
+                s_x[buf][((tk * 8 + (ei >> 5)) * 8 + (ei & 7)) * 4 + ((ei & 31) >> 3)] = vv[i];
+            }
+        }
+    };
+
+    float acc[2][kR2T];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int k = 0; k < kR2T; ++k) acc[r][k] = 0.0f;
+    uint4 ws[kNP];
+    float4 xs[kXs];
+    stage_load(0, ws, xs);
+    stage_store(ws, xs, 0);
+    __syncthreads();
+    for (int u = 0; u < units; ++u) {
+        const int buf = u & 1;
+        // the next unit's loads and staging run unconditionally (the last
+        // unit reloads itself into the idle buffer)
+        stage_load(min(u + 1, units - 1), ws, xs);
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+            float q[2][4];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint8_t* blk = &s_w[buf][(2 * rp + r) * kU + kB * jb];
+                const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
+                if constexpr (TYPE == kQ4_0) {
+                    const uint32_t pair =
+                        static_cast<uint32_t>(blk[2 + j]) | (static_cast<uint32_t>(blk[10 + j]) << 8);
+                    const uint32_t lo = pair & 0x0f0fu, hi = (pair >> 4) & 0x0f0fu;
+                    // float(q - 8): the nibble converted exactly, minus 8 exactly
+                    q[r][0] = (static_cast<float>(lo & 0xffu) - 8.0f) * d;
+                    q[r][1] = (static_cast<float>(lo >> 8) - 8.0f) * d;
+                    q[r][2] = (static_cast<float>(hi & 0xffu) - 8.0f) * d;
+                    q[r][3] = (static_cast<float>(hi >> 8) - 8.0f) * d;
+                } else {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        q[r][m] = static_cast<float>(static_cast<int8_t>(blk[2 + j + 8 * m])) * d;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kR2T; ++k) {
+                const float4 xv =
+                    *reinterpret_cast<const float4*>(&s_x[buf][(((tg * kR2T + k) * 8 + jb) * 8 + j) * 4]);
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    acc[r][k] = fmaf(q[r][0], xv.x, acc[r][k]);
+                    acc[r][k] = fmaf(q[r][1], xv.y, acc[r][k]);
+                    acc[r][k] = fmaf(q[r][2], xv.z, acc[r][k]);
+                    acc[r][k] = fmaf(q[r][3], xv.w, acc[r][k]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        stage_store(ws, xs, buf ^ 1);  // buffer buf ^ 1 was last read by unit u - 1
+        __syncthreads();
+    }
+    // t0 + t1 + ... + t7 per (row, token), in order, through LDS
+    float* s_red = &s_x[0][0];  // [row][token][j]: 32 * kR2Tok * 8 floats
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int k = 0; k < kR2T; ++k) s_red[((2 * rp + r) * kR2Tok + tg * kR2T + k) * 8 + j] = acc[r][k];
+    __syncthreads();
+#pragma unroll
+    for (int o = 0; o < kR2Rows * kR2Tok / 256; ++o) {
+        const int idx = t + 256 * o, tk = idx / kR2Rows, row = idx % kR2Rows;  // rows fastest
+        const float* p = s_red + (row * kR2Tok + tk) * 8;
+        float sum = p[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) sum = sum + p[i];
+        const int orow = row0 + row;
+        if (orow < N) y[static_cast<size_t>(tok0 + tk) * N + orow] = sum;
+    }
+}
+
 // Q6_K with fp32 activations (dot_q6_k_fp32, src/gguf_kernels.cpp:138-146):
 // w = (d*sc[i/16])*q in f32, exact products summed in double.  One wave per
 // row; each lane owns 64 elements of one half super-block and keeps its own
@@ -966,6 +1112,20 @@ hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x,
     if (!rows || !batch) return hipSuccess;
     const int nb = static_cast<int>(cols / 32);
     static_assert(kBT * kBRows == 256, "one output per thread in the final sum");
+    if (cols % 256 == 0 && batch >= kR2Tok) {
+        // whole groups of kR2Tok tokens with two rows per lane, the rest below
+        const size_t groups = batch / kR2Tok;
+        const dim3 grid(static_cast<unsigned>((rows + kR2Rows - 1) / kR2Rows), static_cast<unsigned>(groups));
+        if (type == kQ4_0)
+            batch_f32act_rows2_kernel<kQ4_0><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
+        else
+            batch_f32act_rows2_kernel<kQ8_0><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
+        const size_t done = groups * kR2Tok;
+        if (done == batch) return hipGetLastError();
+        x += done * cols;
+        y += done * rows;
+        batch -= done;
+    }
     if (cols % 256 == 0 && batch >= kBT) {
         // whole groups of kBT tokens on the lane-spread kernel, the rest per token below
         const size_t groups = batch / kBT;

@@ -103,7 +103,8 @@ __device__ __forceinline__ float row_ror1(float v) {
 }
 
 // NP passes (one per 128 blocks of K); CH activation loads per thread: 16-byte
-// Q8 chunks (kSrcQ8, nb * 2 <= 256 CH) or native blocks (kSrcNative, nb <= 256 CH).
+// Q8 chunks (kSrcQ8, nb * 2 <= 256 CH), native blocks (kSrcNative, nb <= 256 CH)
+// or fp32 float4s (kSrcF32, nb * 8 <= 256 CH), all issued before the weights.
 // W, act and ad are deliberately not __restrict__: with it the compiler may
 // sink the weight loads past the staging barrier (nothing could write
 // restrict-qualified read-only memory), and they would then be issued only
@@ -126,7 +127,12 @@ __global__ __launch_bounds__(256) void gemv_q4_rows16(const uint8_t* W, const vo
     uint4 aqv[SRC == kSrcQ8 ? CH : 1];
     float adv[SRC == kSrcQ8 ? CH : 1];
     uint32_t anv[SRC == kSrcNative ? CH : 1][9];
-    if constexpr (SRC == kSrcQ8) {
+    float4 axv[SRC == kSrcF32 ? CH : 1];
+    if constexpr (SRC == kSrcF32) {  // fp32 input: CH float4 per thread, all issued here
+        const float4* x4 = static_cast<const float4*>(act);
+#pragma unroll
+        for (int i = 0; i < CH; ++i) axv[i] = x4[min(t + 256 * i, nb * 8 - 1)];
+    } else if constexpr (SRC == kSrcQ8) {
         const uint4* aq4 = static_cast<const uint4*>(act);
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
@@ -206,14 +212,13 @@ __global__ __launch_bounds__(256) void gemv_q4_rows16(const uint8_t* W, const vo
                 make_int2(static_cast<int>(anv[i][0]), byte_sum16(ev) + byte_sum16(od));
         }
     } else {  // kSrcF32: quantize_q8 of the fp32 input, 8 lanes per block
-        const float4* x4 = static_cast<const float4*>(act);
         const int n4 = nb * 8;
-        for (int i0 = 0; i0 < n4; i0 += 256) {
-            const int i = i0 + t;
-            const float4 v = x4[min(i, n4 - 1)];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int i = t + 256 * c;
             float d;
             int s;
-            const uint32_t q = quantize_q8_x4(v, d, s);
+            const uint32_t q = quantize_q8_x4(axv[c], d, s);
             const bool ok = i < n4;
             const int b = ok ? i >> 3 : 0;
             *reinterpret_cast<uint32_t*>(ok ? s_aq + (b >> 3) * kActPitch + (b & 7) * 32 + (i & 7) * 4 : dummy) = q;
@@ -272,6 +277,8 @@ hipError_t launch_np(const uint8_t* W, const void* act, const float* ad, float* 
             gemv_q4_rows16<F, SRC, NP, 1><<<grid, 256, lds, st>>>(W, act, ad, y, N, nb, ntiles);
         else
             gemv_q4_rows16<F, SRC, NP, 2><<<grid, 256, lds, st>>>(W, act, ad, y, N, nb, ntiles);
+    } else if constexpr (SRC == kSrcF32) {  // float4 per thread: nb * 8 / 256 <= 4 * NP
+        gemv_q4_rows16<F, SRC, NP, 4 * NP><<<grid, 256, lds, st>>>(W, act, ad, y, N, nb, ntiles);
     } else {  // Q8 chunks per thread: nb * 2 / 256 = NP
         gemv_q4_rows16<F, SRC, NP, NP><<<grid, 256, lds, st>>>(W, act, ad, y, N, nb, ntiles);
     }

@@ -211,12 +211,14 @@ def test_matmul_v06_ref_mode_bitexact(ctx, oracle, ty, name, batch):
 @pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0])
 @pytest.mark.parametrize("name,batch,k,n", [("blk.0.attn_q.weight", 32, 4096, 300), ("blk.0.attn_q.weight", 12, 4096, 33),
                                             ("blk.0.ffn_up.weight", 24, 11008, 40), ("blk.0.attn_q.weight", 27, 768, 64),
-                                            ("blk.0.ffn_up.weight", 8, 2048, 1)])
+                                            ("blk.0.ffn_up.weight", 8, 2048, 1), ("blk.0.ffn_up.weight", 40, 4096, 7),
+                                            ("blk.0.attn_q.weight", 16, 256, 45)])
 def test_matmul_v06_ref_mode_lanes_bitexact(ctx, oracle, ty, name, batch, k, n):
     """Default prefill numerics (batch4 / batch8 accumulators) at 7B-scale K:
-    whole 8-token groups run on the lane-spread kernel, the rest of the blocked
-    tokens per token, the unblocked tail with dot_*_fp32; row counts off the
-    32-row tile."""
+    for Q4_0 whole 16-token groups run two rows per lane, then whole 8-token
+    groups on the lane-spread kernel, the rest of the blocked tokens per
+    token, the unblocked tail with dot_*_fp32; row counts off the 32-row tile
+    (down to a single partial tile), a one-unit row (K = 256)."""
     rng = np.random.default_rng(batch * 13 + k + n + ty)
     w = _w(rng, ty, n, k)
     t = ctx.upload(name, ty, k, n, w)
