@@ -339,21 +339,36 @@ def prefill_roofline(gemm):
     return out
 
 
-def time_pp(m, prompt, reps: int = 1):
-    """Prefill rate of prompt (chunks of BATCH, last-token logits) after one untimed run."""
+def time_pp(m, prompt, reps: int = 1, batch: int = BATCH):
+    """Prefill rate of prompt (chunks of `batch`, last-token logits) after one untimed run."""
     import torch
 
     m.reset()
-    m.prefill(prompt, BATCH, logits=True)
+    m.prefill(prompt, batch, logits=True)
     out = []
     for _ in range(reps):
         m.reset()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        m.prefill(prompt, BATCH, logits=True)
+        m.prefill(prompt, batch, logits=True)
         torch.cuda.synchronize()
         out.append(len(prompt) / (time.perf_counter() - t0))
     return out
+
+
+def pp_whole_prompt(m, prompt, reps: int):
+    """The prompt as one prefill batch (every GEMM at M = len(prompt)): rate,
+    and whether its last-token logits are bit-identical to chunks of BATCH
+    (they are when the chunk boundaries fall on multiples of 8 tokens: every
+    output then takes the same batch4/batch8 or FORCE_Q8 arithmetic)."""
+    import numpy as np
+
+    m.reset()
+    ref = np.array(m.prefill(prompt, BATCH, logits=True), copy=True)
+    rates = time_pp(m, prompt, reps, batch=len(prompt))
+    m.reset()
+    got = np.array(m.prefill(prompt, len(prompt), logits=True), copy=True)
+    return rates, bool(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))
 
 
 def time_tg(m, seed, steps: int, warmup: int):
@@ -380,12 +395,13 @@ def default_numerics_run(path: str, prompt, ctx_len: int, seed, n_ids: int):
     of seed (the CPU leg's protocol, for the id comparison)."""
     from memvanta_amd import capi
 
-    m = capi.Model(path, ctx=ctx_len, page_tokens=PAGE, act_mode=capi.MVH_ACT_REF, max_batch=BATCH)
+    m = capi.Model(path, ctx=ctx_len, page_tokens=PAGE, act_mode=capi.MVH_ACT_REF, max_batch=len(prompt))
     try:
         pp = time_pp(m, prompt)[0]
+        whole, same = pp_whole_prompt(m, prompt, 1)
         m.reset()
         m.prefill(seed, BATCH, logits=False)
-        return pp, [int(i) for i in m.generate_greedy(FIRST_TOKEN, n_ids)]
+        return pp, [int(i) for i in m.generate_greedy(FIRST_TOKEN, n_ids)], whole[0], same
     finally:
         m.close()
 
@@ -428,7 +444,7 @@ def time_other_model(tmpdir: str, label: str, cfg_name: str, ctx_len: int, pp_n:
     finally:
         m.close()
     cpu_seed, cpu_tg = cpu_run
-    pp_default, ref_ids = default_numerics_run(path, prompt, ctx_len, prompt[:cpu_seed], cpu_tg)
+    pp_default, ref_ids, _, _ = default_numerics_run(path, prompt, ctx_len, prompt[:cpu_seed], cpu_tg)
     res = {"workload": f"{label}: {cfg.name} (dim {cfg.dim}, FFN {cfg.ffn}, {cfg.layers} layers, "
                        f"{cfg.heads}/{cfg.kv_heads} heads, vocab {cfg.vocab}), ctx {ctx_len}, batch {BATCH}, "
                        f"paged F16 KV, prompt ids uniform from seed {prompt_seed}",
@@ -691,7 +707,7 @@ def main():
     ctx = None
     try:
         t0 = time.perf_counter()
-        m = capi.Model(path, ctx=CTX, page_tokens=PAGE, act_mode=capi.MVH_ACT_Q8, max_batch=BATCH)
+        m = capi.Model(path, ctx=CTX, page_tokens=PAGE, act_mode=capi.MVH_ACT_Q8, max_batch=PROMPT_TOKENS)
         t_load = time.perf_counter() - t0
         stream = torch.cuda.ExternalStream(m.stream)
         vocab = m.vocab
@@ -699,6 +715,7 @@ def main():
 
         # pp512 (host-driven chunks of 32, last-token logits), after one untimed run
         pp = time_pp(m, prompt, args.pp_reps)
+        pp_whole, pp_whole_same = pp_whole_prompt(m, prompt, args.pp_reps)
 
         # tg: warm-up (captures the decode graph), then the K timed tokens
         m.reset()
@@ -736,7 +753,8 @@ def main():
         log(f"7B pp512 / tg{args.steps} done")
 
         n_cpu_tg = args.cpu_tg_tokens
-        pp_default, ref_ids = default_numerics_run(path, prompt, CTX, seed, n_cpu_tg)
+        pp_default, ref_ids, pp_default_whole, pp_default_whole_same = default_numerics_run(
+            path, prompt, CTX, seed, n_cpu_tg)
 
         # dominant kernel alone: Q4_0 x Q8 GEMV; prefill GEMM; measured ceilings
         ctx = capi.Context(0)
@@ -884,6 +902,12 @@ def main():
             "pp512_default_numerics_tok_s": round(pp_default, 1),
             "pp_default_numerics": "tensor_matmul_batch_v06 without MEMVANTA_FORCE_Q8_ACT (fp32 activations, "
                                    "batch8 / batch4 accumulators)",
+            "pp512_batch512_tok_s": round(float(np.mean(pp_whole)), 1),
+            "pp512_batch512_default_numerics_tok_s": round(pp_default_whole, 1),
+            "pp512_batch512_logits_identical_to_batch32": pp_whole_same and pp_default_whole_same,
+            "pp512_batch512_basis": "the 512-token prompt as one prefill batch (every GEMM at M = 512), "
+                                    "not the config's batch 32; last-token logits compared bit for bit with "
+                                    "the batch-32 run in both numerics",
             "greedy_ids_head": ids[:8],
             "model_write_s": round(t_write, 1),
             "model_load_s": round(t_load, 2),

@@ -190,6 +190,177 @@ __global__ __launch_bounds__(64) void gemm_q4_0_q8_mfma_kernel(const uint8_t* __
     }
 }
 
+// The same numerics with a workgroup of 4 waves sharing one LDS copy of each
+// K-chunk: 64 weight rows (wave w computes rows 16w .. 16w+15) x 16*TG
+// tokens.  The chunk's raw weights (64 rows x 144 B), activation operands (TG
+// x 4 KB, operand order) and scales come in with 16-byte loads one chunk
+// ahead into registers, go to the idle half of a double-buffered LDS copy
+// after the current chunk's compute, and one workgroup barrier per chunk
+// hands them over; the staging also copies each row's f16 block scales to a
+// [block][row] table.  The weights are the MFMA's A operand, so a lane holds
+// rows 4h .. 4h+3 of one token (li) and reads, per block, four row scales
+// (8 bytes) and one activation scale per token group; C = (-8) x A for the
+// next block is issued before the current block's sums are used.  Against
+// the wave-private kernel: no register ring of activation operands (about
+// half the VGPRs, twice the resident waves), a quarter of the activation
+// traffic and a third of the LDS bytes per block.
+template <int TG>
+__global__ __launch_bounds__(256) void gemm_q4_0_q8_mfma_wg_kernel(const uint8_t* __restrict__ W,
+                                                                   const int8_t* __restrict__ aq,
+                                                                   const float* __restrict__ ad,
+                                                                   float* __restrict__ y, int N, int nb, int B) {
+    constexpr int kToks = 16 * TG;
+    constexpr int kWgRows = 64;
+    constexpr int kRaw = kWgRows * kUnit;        // 9216 bytes of raw weights per chunk
+    constexpr int kPieces = kRaw / 16;           // 576
+    constexpr int kWLd = (kPieces + 255) / 256;  // 3 weight loads per thread
+    constexpr int kA = TG * 4096;                // activation operand bytes per chunk
+    constexpr int kDa = kChunk * kToks;          // activation scales per chunk
+    __shared__ __align__(16) uint8_t s_raw[2][kRaw + 16];                // + a spare slot for unused stores
+    __shared__ __align__(16) uint16_t s_dw[2][kChunk * kWgRows + 8];      // [block][row] f16 scales + spare
+    __shared__ __align__(16) int8_t s_a[2][kA];
+    __shared__ __align__(16) float s_da[2][kDa];                          // [block][token]
+
+    const int t = threadIdx.x, l = t & 63, wv = t >> 6, li = l & 15, h = l >> 4;
+    const int r0 = blockIdx.x * kWgRows, t0 = blockIdx.y * kToks;
+    const size_t row_bytes = static_cast<size_t>(nb) * 18, K = static_cast<size_t>(nb) * 32;
+    const int nchunks = nb / kChunk;
+
+    // weight piece p = t + 256 i: row p / 9, unit bytes 16 (p % 9); piece k < 8 of a
+    // row holds block k's scale at its byte 2k
+    const uint8_t* wsrc[kWLd];
+    int wdst[kWLd], sdst[kWLd], sdw[kWLd];
+#pragma unroll
+    for (int i = 0; i < kWLd; ++i) {
+        const int p = t + 256 * i, pc = min(p, kPieces - 1), k = pc % 9;
+        wsrc[i] = W + static_cast<size_t>(min(r0 + pc / 9, N - 1)) * row_bytes + k * 16;
+        wdst[i] = p < kPieces ? (pc / 9) * kUnit + k * 16 : kRaw;
+        sdst[i] = p < kPieces && k < 8 ? k * kWgRows + pc / 9 : kChunk * kWgRows;
+        sdw[i] = k & 7;  // the scale's halfword within the piece
+    }
+    const int8_t* asrc[TG];
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+        asrc[g] = aq + static_cast<size_t>(min(blockIdx.y * TG + g, (B - 1) / 16)) * 16 * K + 16 * t;
+    // scale e = t + 256 i: token e / 8, block e % 8 (TG = 1: threads t, t + 128 load the same scale)
+    constexpr int kDL = (kDa + 255) / 256;
+    const float* dsrc[kDL];
+    int ddst[kDL];
+#pragma unroll
+    for (int i = 0; i < kDL; ++i) {
+        const int e = (t + 256 * i) % kDa, d_tok = e / 8, d_blk = e % 8;
+        dsrc[i] = ad + static_cast<size_t>(min(t0 + d_tok, B - 1)) * nb + d_blk;
+        ddst[i] = d_blk * kToks + d_tok;
+    }
+
+    uint4 wreg[kWLd];
+    uint4 areg[TG];
+    float dreg[kDL];
+    auto load = [&](int c) {
+        const size_t wc = static_cast<size_t>(c) * kUnit;
+#pragma unroll
+        for (int i = 0; i < kWLd; ++i) wreg[i] = ld_global16(wsrc[i] + wc);
+#pragma unroll
+        for (int g = 0; g < TG; ++g) areg[g] = ld_global16(asrc[g] + static_cast<size_t>(c) * 4096);
+#pragma unroll
+        for (int i = 0; i < kDL; ++i) dreg[i] = dsrc[i][c * kChunk];
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < kWLd; ++i) {
+            *reinterpret_cast<uint4*>(&s_raw[buf][wdst[i]]) = wreg[i];
+            // halfword sdw[i] of the piece (dword sdw / 2, half sdw % 2)
+            const bool upper = (sdw[i] & 4) != 0;
+            const uint32_t d0 = upper ? wreg[i].z : wreg[i].x, d1 = upper ? wreg[i].w : wreg[i].y;
+            const uint32_t dd = (sdw[i] & 2) ? d1 : d0;
+            s_dw[buf][sdst[i]] = static_cast<uint16_t>(dd >> (16 * (sdw[i] & 1)));
+        }
+#pragma unroll
+        for (int g = 0; g < TG; ++g) *reinterpret_cast<uint4*>(&s_a[buf][g * 4096 + 16 * t]) = areg[g];
+#pragma unroll
+        for (int i = 0; i < kDL; ++i) s_da[buf][ddst[i]] = dreg[i];
+    };
+
+    float acc[TG][4];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.f;
+    // the lane's weight operand bytes: row 16 wv + li, qs[8(h&1) .. +8) of each block, nibble half h >> 1
+    const int my_row = (16 * wv + li) * kUnit;
+    const uint32_t nib_shift = 4u * static_cast<uint32_t>(h >> 1);
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int buf = c & 1;
+        load(min(c + 1, nchunks - 1));  // unconditional: the last chunk reloads itself
+        const uint8_t* my_q = &s_raw[buf][my_row + 2 + 8 * (h & 1)];
+        long a_cur[TG];
+        v4i c8_cur[TG];
+#pragma unroll
+        for (int g = 0; g < TG; ++g) {
+            a_cur[g] = *reinterpret_cast<const long*>(&s_a[buf][g * 4096 + 8 * l]);
+            c8_cur[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(kMinus8, a_cur[g], v4i{0, 0, 0, 0}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            uint32_t q0, q1;
+            if ((j & 1) == 0) {  // 18j + 2 + 8(h&1) is 2 mod 4: three dwords, shifted by 2 bytes
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(my_q + 18 * j - 2);
+                const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+                q0 = align16(w1, w0);
+                q1 = align16(w2, w1);
+            } else {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(my_q + 18 * j);
+                q0 = p[0];
+                q1 = p[1];
+            }
+            const uint32_t n0 = (q0 >> nib_shift) & 0x0f0f0f0fu, n1 = (q1 >> nib_shift) & 0x0f0f0f0fu;
+            const long wop = static_cast<long>((static_cast<unsigned long>(n1) << 32) | n0);
+            // f16 scales of rows 16 wv + 4h .. +3
+            const uint2 dwb = *reinterpret_cast<const uint2*>(&s_dw[buf][j * kWgRows + 16 * wv + 4 * h]);
+            const float dw[4] = {h2f(dwb.x & 0xffffu), h2f(dwb.x >> 16), h2f(dwb.y & 0xffffu), h2f(dwb.y >> 16)};
+            long a_nxt[TG];
+            v4i c8_nxt[TG];
+#pragma unroll
+            for (int g = 0; g < TG; ++g) {
+                const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(wop, a_cur[g], c8_cur[g], 0, 0, 0);
+                if (j + 1 < kChunk) {
+                    a_nxt[g] = *reinterpret_cast<const long*>(&s_a[buf][g * 4096 + (j + 1) * 512 + 8 * l]);
+                    c8_nxt[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(kMinus8, a_nxt[g], v4i{0, 0, 0, 0}, 0, 0, 0);
+                }
+                const float da = s_da[buf][j * kToks + 16 * g + li];
+                acc[g][0] = fmaf(dw[0] * da, static_cast<float>(is[0]), acc[g][0]);
+                acc[g][1] = fmaf(dw[1] * da, static_cast<float>(is[1]), acc[g][1]);
+                acc[g][2] = fmaf(dw[2] * da, static_cast<float>(is[2]), acc[g][2]);
+                acc[g][3] = fmaf(dw[3] * da, static_cast<float>(is[3]), acc[g][3]);
+            }
+            if (j + 1 < kChunk) {
+#pragma unroll
+                for (int g = 0; g < TG; ++g) {
+                    a_cur[g] = a_nxt[g];
+                    c8_cur[g] = c8_nxt[g];
+                }
+            }
+        }
+        store(buf ^ 1);  // the idle buffer was last read in chunk c - 1, before the barrier that ended it
+        __syncthreads();
+    }
+
+    // lane holds (row 16 wv + 4h + v, token 16g + li) of each token group g
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+        const int tk = t0 + 16 * g + li;
+        if (tk < B) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int orow = r0 + 16 * wv + 4 * h + v;
+                if (orow < N) y[static_cast<size_t>(tk) * N + orow] = acc[g][v];
+            }
+        }
+    }
+}
+
 }  // namespace
 
 bool gemm_q4_0_mfma_ok(size_t cols) { return cols >= 256 && cols % 256 == 0; }
@@ -212,6 +383,24 @@ hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const fl
         const char* e = getenv("MVH_GEMM_TG2_ROWTILES");
         return e ? static_cast<size_t>(atoll(e)) : static_cast<size_t>(512);
     }();
+    // From 256 tokens the workgroup kernel (64 rows x 32 tokens per workgroup)
+    // is a few percent faster (M = 512: 68-69 against 70-71 us at 4096^2,
+    // 160 against 165-172 us at the other two shapes); at M = 128 it is slower.
+    // Tuning override: MVH_GEMM_WG=0 never, 1 always (16-token tiles at M <= 32).
+    static const int wg_mode = [] {
+        const char* e = getenv("MVH_GEMM_WG");
+        return e ? atoi(e) : -1;
+    }();
+    const size_t gw = (rows + 63) / 64;
+    if (wg_mode == 1 || (wg_mode != 0 && batch >= 256)) {
+        if (wg_mode == 1 && batch <= 32)
+            gemm_q4_0_q8_mfma_wg_kernel<1><<<dim3(static_cast<unsigned>(gw), static_cast<unsigned>(g16)), 256, 0, st>>>(
+                W, aq, ad, y, N, nb, Bn);
+        else
+            gemm_q4_0_q8_mfma_wg_kernel<2><<<dim3(static_cast<unsigned>(gw), static_cast<unsigned>(g32)), 256, 0, st>>>(
+                W, aq, ad, y, N, nb, Bn);
+        return hipGetLastError();
+    }
     if ((batch <= 32 && gx < tg2_min) || gx * g32 <= 1024) {
         if (gx * g16 <= 1024)
             gemm_q4_0_q8_mfma_kernel<1, 4><<<dim3(gx, static_cast<unsigned>(g16)), 64, 0, st>>>(W, aq, ad, y, N, nb, Bn);

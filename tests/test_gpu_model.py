@@ -130,6 +130,29 @@ def test_pipelined_prefill_equals_chunk_by_chunk_hd128(tmp_path, chunk):
     assert (kb_a, ids_a) == (kb_b, ids_b)
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_whole_prompt_batch_equals_chunks_of_32(tmp_path, mode):
+    """One prefill batch for the whole prompt (every GEMM at M = 256: the
+    workgroup int8-MFMA kernel in FORCE_Q8 mode, 16-token groups two rows per
+    lane in the default numerics) against chunks of 32 on a one-layer 7B-shape
+    model: chunk boundaries on multiples of 8 tokens leave every output's
+    arithmetic unchanged, so logits, KV bytes and the ids that follow are
+    bit-identical."""
+    cfg = synth.dataclasses.replace(synth.LLAMA7B_1L, name="openllama-7b-v2-q4_0-1layer-whole", ctx=320)
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(cfg, path, seed=43)
+    prompt = synth.prompt_tokens(14, 256)
+    runs = []
+    for batch in (32, 256):
+        m = capi.Model(path, ctx=320, act_mode=mode, max_batch=256)
+        lg = m.prefill(prompt, batch)
+        runs.append((lg.copy(), m.kv_bytes(), m.generate_greedy(5, 4).tolist()))
+        m.close()
+    (a, kb_a, ids_a), (b, kb_b, ids_b) = runs
+    assert (bits(a) == bits(b)).all()
+    assert (kb_a, ids_a) == (kb_b, ids_b)
+
+
 def test_pipelined_prefill_error_completes_earlier_chunks(tiny):
     """A bad token id in the third chunk: the two chunks before it complete (as
     in a chunk-by-chunk run), the position stops after them, and decoding from
