@@ -243,10 +243,13 @@ def test_matmul_v06_q8_mode_bitexact(ctx, oracle, ty, batch, k, n):
 
 
 @pytest.mark.parametrize("batch,k,n", [(32, 4096, 4096), (128, 4096, 1024), (512, 4096, 256), (32, 4096, 11008),
-                                        (32, 11008, 4096), (33, 256, 100), (3, 512, 17), (70, 768, 45)])
+                                        (32, 11008, 4096), (33, 256, 100), (3, 512, 17), (70, 768, 45),
+                                        (300, 4096, 1000), (257, 256, 63), (400, 11008, 70)])
 def test_prefill_gemm_int8_mfma_bitexact(ctx, oracle, batch, k, n):
     """The int8-MFMA Q4_0 x Q8 GEMM (K % 256 == 0) against the FORCE_Q8 reference
-    chain: the GEMM config shapes, plus token and row counts off the 32 x 32 tile."""
+    chain: the GEMM config shapes, plus token and row counts off the 32 x 32 tile
+    and, from 256 tokens (the workgroup kernel), off its 64-row x 32-token tile
+    (a partial last token group, a partial last row group, one K-chunk)."""
     rng = np.random.default_rng(batch * 7 + k + n)
     w = _w(rng, synth.Q4_0, n, k)
     t = ctx.upload("blk.0.ffn_gate.weight", synth.Q4_0, k, n, w)
