@@ -712,11 +712,25 @@ __global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* 
 // batch_f32act_lanes_kernel: fewer VALU instructions per fma (the eight lanes
 // of a row no longer each unpack the whole unit from registers) and half the
 // activation reads from LDS per fma.
+//
+// BS = true: dot_q4_0_fp32 / dot_q8_0_fp32 numerics (src/gguf_kernels.cpp:
+// 93-120, tensor_matmul_batch_v06 with MEMVANTA_FORCE_Q8_ACT for Q8_0
+// weights, and the per-token remainders): per block, lane j's t_j over
+// elements j, j+8, j+16, j+24 from zero, s = t0 + ... + t7 in order, then
+// sum = fma(d, s, sum) over the blocks in order.  The same tile and staging;
+// thread (block jb, row pair, token group) owns block jb of each unit for two
+// rows x kR2T tokens, all eight lanes of it, so a block's in-order lane sum
+// stays in the thread.  The block sums go to LDS, and after a barrier thread
+// t carries the chains of (row, token) t and t + 256 over the unit's eight
+// blocks.  The activation blocks are padded to 36 floats in LDS so the eight
+// blocks of a token fall in different banks.
 constexpr int kR2T = 8;       // tokens per thread (16 measured slower: 214 VGPRs, half the workgroups)
 constexpr int kR2Rows = 32;   // rows per workgroup
 constexpr int kR2Tok = 2 * kR2T;
+constexpr int kBsPitch = kR2Tok + 4;                 // block sums: floats per row (16-byte aligned)
+constexpr int kBsBlk = kR2Rows * kBsPitch + 4;       // block sums: floats per block of the unit
 
-template <uint32_t TYPE>
+template <uint32_t TYPE, bool BS>
 __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* __restrict__ W,
                                                                  const float* __restrict__ x,
                                                                  float* __restrict__ y, int N, int nb) {
@@ -724,8 +738,11 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
     constexpr int kU = 8 * kB;                // bytes of an 8-block unit of one row (144 or 272)
     constexpr int kP = kU / 16;               // 16-byte pieces per row and unit (9 or 17)
     constexpr int kNP = (kR2Rows * kP + 255) / 256;  // pieces per thread (2 or 3)
+    constexpr int kXP = BS ? 36 : 32;         // LDS floats per activation block
     __shared__ __align__(16) uint8_t s_w[2][kR2Rows * kU + 16];  // + a 16-byte slot for unused stores
-    __shared__ __align__(16) float s_x[2][kR2Tok * kBChunk];     // [token][block][j][m]
+    __shared__ __align__(16) float s_x[2][kR2Tok * 8 * kXP];     // [token][block][j][m]
+    __shared__ __align__(16) float s_bs[BS ? 8 * kBsBlk : 1];    // [block][row][token]
+    __shared__ float s_d[BS ? 8 * kR2Rows : 1];                  // [block][row]
     const int t = threadIdx.x, j = t & 7, slot = t >> 3;
     const int rp = slot & 15, tg = slot >> 4;  // rows 2rp, 2rp+1; tokens tg*kR2T ..
     const int row0 = blockIdx.x * kR2Rows;
@@ -745,7 +762,7 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
         wsrc[i] = W + static_cast<size_t>(min(row0 + pc / kP, N - 1)) * row_bytes + 16 * (pc % kP);
         wdst[i] = p < kR2Rows * kP ? (pc / kP) * kU + 16 * (pc % kP) : kR2Rows * kU;
     }
-    auto stage_load = [&](int c, uint4 (&w)[kNP], float4 (&v)[kXs]) {
+    auto stage_load = [&](int c, uint4 (&w)[kNP], float4 (&v)[kXs]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < kNP; ++i) w[i] = *reinterpret_cast<const uint4*>(wsrc[i] + static_cast<size_t>(c) * kU);
 #pragma unroll
@@ -755,7 +772,7 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
                                                     4 * (f & 63));
         }
     };
-    auto stage_store = [&](const uint4 (&w)[kNP], const float4 (&v)[kXs], int buf) {
+    auto stage_store = [&](const uint4 (&w)[kNP], const float4 (&v)[kXs], int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < kNP; ++i) *reinterpret_cast<uint4*>(&s_w[buf][wdst[i]]) = w[i];
 #pragma unroll
@@ -766,16 +783,17 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
 #pragma unroll
             for (int i = 0; i < 4; ++i) {  // element e+i: block (e+i)/32, lane (e+i)%8, m = ((e+i)%32)/8
                 const int ei = e + i;
-                s_x[buf][((tk * 8 + (ei >> 5)) * 8 + (ei & 7)) * 4 + ((ei & 31) >> 3)] = vv[i];
+                s_x[buf][(tk * 8 + (ei >> 5)) * kXP + (ei & 7) * 4 + ((ei & 31) >> 3)] = vv[i];
             }
         }
     };
 
-    float acc[2][kR2T];
+    float acc[2][kR2T];  // BS: the block sums of the current unit
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
         for (int k = 0; k < kR2T; ++k) acc[r][k] = 0.0f;
+    float chain[2] = {0.0f, 0.0f};  // BS: sums of (row, token) = (c / 16, c % 16), c = t and t + 256
     uint4 ws[kNP];
     float4 xs[kXs];
     stage_load(0, ws, xs);
@@ -786,44 +804,116 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
         // the next unit's loads and staging run unconditionally (the last
         // unit reloads itself into the idle buffer)
         stage_load(min(u + 1, units - 1), ws, xs);
+        if constexpr (!BS) {
 #pragma unroll
-        for (int jb = 0; jb < 8; ++jb) {
-            float q[2][4];
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const uint8_t* blk = &s_w[buf][(2 * rp + r) * kU + kB * jb];
-                const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
-                if constexpr (TYPE == kQ4_0) {
-                    const uint32_t pair =
-                        static_cast<uint32_t>(blk[2 + j]) | (static_cast<uint32_t>(blk[10 + j]) << 8);
-                    const uint32_t lo = pair & 0x0f0fu, hi = (pair >> 4) & 0x0f0fu;
-                    // float(q - 8): the nibble converted exactly, minus 8 exactly
-                    q[r][0] = (static_cast<float>(lo & 0xffu) - 8.0f) * d;
-                    q[r][1] = (static_cast<float>(lo >> 8) - 8.0f) * d;
-                    q[r][2] = (static_cast<float>(hi & 0xffu) - 8.0f) * d;
-                    q[r][3] = (static_cast<float>(hi >> 8) - 8.0f) * d;
-                } else {
-#pragma unroll
-                    for (int m = 0; m < 4; ++m)
-                        q[r][m] = static_cast<float>(static_cast<int8_t>(blk[2 + j + 8 * m])) * d;
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < kR2T; ++k) {
-                const float4 xv =
-                    *reinterpret_cast<const float4*>(&s_x[buf][(((tg * kR2T + k) * 8 + jb) * 8 + j) * 4]);
+            for (int jb = 0; jb < 8; ++jb) {
+                float q[2][4];
 #pragma unroll
                 for (int r = 0; r < 2; ++r) {
-                    acc[r][k] = fmaf(q[r][0], xv.x, acc[r][k]);
-                    acc[r][k] = fmaf(q[r][1], xv.y, acc[r][k]);
-                    acc[r][k] = fmaf(q[r][2], xv.z, acc[r][k]);
-                    acc[r][k] = fmaf(q[r][3], xv.w, acc[r][k]);
+                    const uint8_t* blk = &s_w[buf][(2 * rp + r) * kU + kB * jb];
+                    const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
+                    if constexpr (TYPE == kQ4_0) {
+                        const uint32_t pair =
+                            static_cast<uint32_t>(blk[2 + j]) | (static_cast<uint32_t>(blk[10 + j]) << 8);
+                        const uint32_t lo = pair & 0x0f0fu, hi = (pair >> 4) & 0x0f0fu;
+                        // float(q - 8): the nibble converted exactly, minus 8 exactly
+                        q[r][0] = (static_cast<float>(lo & 0xffu) - 8.0f) * d;
+                        q[r][1] = (static_cast<float>(lo >> 8) - 8.0f) * d;
+                        q[r][2] = (static_cast<float>(hi & 0xffu) - 8.0f) * d;
+                        q[r][3] = (static_cast<float>(hi >> 8) - 8.0f) * d;
+                    } else {
+#pragma unroll
+                        for (int m = 0; m < 4; ++m)
+                            q[r][m] = static_cast<float>(static_cast<int8_t>(blk[2 + j + 8 * m])) * d;
+                    }
                 }
+#pragma unroll
+                for (int k = 0; k < kR2T; ++k) {
+                    const float4 xv = *reinterpret_cast<const float4*>(
+                        &s_x[buf][((tg * kR2T + k) * 8 + jb) * kXP + j * 4]);
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        acc[r][k] = fmaf(q[r][0], xv.x, acc[r][k]);
+                        acc[r][k] = fmaf(q[r][1], xv.y, acc[r][k]);
+                        acc[r][k] = fmaf(q[r][2], xv.z, acc[r][k]);
+                        acc[r][k] = fmaf(q[r][3], xv.w, acc[r][k]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
+            stage_store(ws, xs, buf ^ 1);  // buffer buf ^ 1 was last read by unit u - 1
+            __syncthreads();
+        } else {
+            // block j of the unit: lane sums t_l, l = 0..7, each from zero,
+            // added into s in lane order
+            const uint8_t* blk0 = &s_w[buf][(2 * rp) * kU + kB * j];
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int k = 0; k < kR2T; ++k) acc[r][k] = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                float q[2][4];
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const uint8_t* blk = blk0 + r * kU;
+                    if constexpr (TYPE == kQ4_0) {
+                        const uint32_t pair =
+                            static_cast<uint32_t>(blk[2 + l]) | (static_cast<uint32_t>(blk[10 + l]) << 8);
+                        const uint32_t lo = pair & 0x0f0fu, hi = (pair >> 4) & 0x0f0fu;
+                        q[r][0] = static_cast<float>(lo & 0xffu) - 8.0f;
+                        q[r][1] = static_cast<float>(lo >> 8) - 8.0f;
+                        q[r][2] = static_cast<float>(hi & 0xffu) - 8.0f;
+                        q[r][3] = static_cast<float>(hi >> 8) - 8.0f;
+                    } else {
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) q[r][m] = static_cast<float>(static_cast<int8_t>(blk[2 + l + 8 * m]));
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < kR2T; ++k) {
+                    const float4 xv = *reinterpret_cast<const float4*>(
+                        &s_x[buf][((tg * kR2T + k) * 8 + j) * kXP + l * 4]);
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        float tl = fmaf(q[r][0], xv.x, 0.0f);
+                        tl = fmaf(q[r][1], xv.y, tl);
+                        tl = fmaf(q[r][2], xv.z, tl);
+                        tl = fmaf(q[r][3], xv.w, tl);
+                        acc[r][k] = acc[r][k] + tl;
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                float* dst = &s_bs[j * kBsBlk + (2 * rp + r) * kBsPitch + tg * kR2T];
+#pragma unroll
+                for (int k = 0; k < kR2T; k += 4)
+                    *reinterpret_cast<float4*>(dst + k) = make_float4(acc[r][k], acc[r][k + 1], acc[r][k + 2], acc[r][k + 3]);
+                if (tg == 0) s_d[j * kR2Rows + 2 * rp + r] = h2f(*reinterpret_cast<const uint16_t*>(blk0 + r * kU));
+            }
+            stage_store(ws, xs, buf ^ 1);  // buffer buf ^ 1 was last read by unit u - 1
+            __syncthreads();
+            // sum = fma(d, s, sum) over the unit's blocks in order
+#pragma unroll
+            for (int o = 0; o < 2; ++o) {
+                const int c = t + 256 * o, row = c >> 4, tk = c & 15;
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    chain[o] = fmaf(s_d[b * kR2Rows + row], s_bs[b * kBsBlk + row * kBsPitch + tk], chain[o]);
+            }
+            __syncthreads();  // the reads of s_bs / s_d end before the next unit's writes
         }
-        stage_store(ws, xs, buf ^ 1);  // buffer buf ^ 1 was last read by unit u - 1
-        __syncthreads();
+    }
+    if constexpr (BS) {
+#pragma unroll
+        for (int o = 0; o < 2; ++o) {
+            const int c = t + 256 * o, row = c >> 4, tk = c & 15;
+            const int orow = row0 + row;
+            if (orow < N) y[static_cast<size_t>(tok0 + tk) * N + orow] = chain[o];
+        }
+        return;
     }
     // t0 + t1 + ... + t7 per (row, token), in order, through LDS
     float* s_red = &s_x[0][0];  // [row][token][j]: 32 * kR2Tok * 8 floats
@@ -1084,6 +1174,20 @@ static hipError_t launch_f32act_any(const uint8_t* W, const float* x, float* y, 
             gemv_f32act_persistent_nq8_0<<<g, 256, lds, st>>>(W, x, y, n, nb, ntiles);
         return hipGetLastError();
     }
+    if constexpr (TYPE == kQ4_0 || TYPE == kQ8_0) {
+        if (cols % 256 == 0 && batch >= kR2Tok) {
+            // whole groups of kR2Tok tokens on the staged two-row kernel, the rest below
+            const size_t groups = batch / kR2Tok;
+            const dim3 grid(static_cast<unsigned>((rows + kR2Rows - 1) / kR2Rows), static_cast<unsigned>(groups));
+            batch_f32act_rows2_kernel<TYPE, true><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows),
+                                                                        static_cast<int>(cols / 32));
+            const size_t done = groups * kR2Tok;
+            if (done == batch) return hipGetLastError();
+            x += done * cols;
+            y += done * rows;
+            batch -= done;
+        }
+    }
     return launch_f32act<TYPE>(W, x, y, rows, cols, batch, st);
 }
 
@@ -1117,9 +1221,9 @@ hipError_t launch_batch4_f32act(uint32_t type, const uint8_t* W, const float* x,
         const size_t groups = batch / kR2Tok;
         const dim3 grid(static_cast<unsigned>((rows + kR2Rows - 1) / kR2Rows), static_cast<unsigned>(groups));
         if (type == kQ4_0)
-            batch_f32act_rows2_kernel<kQ4_0><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
+            batch_f32act_rows2_kernel<kQ4_0, false><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
         else
-            batch_f32act_rows2_kernel<kQ8_0><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
+            batch_f32act_rows2_kernel<kQ8_0, false><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), nb);
         const size_t done = groups * kR2Tok;
         if (done == batch) return hipGetLastError();
         x += done * cols;

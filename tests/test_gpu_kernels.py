@@ -242,6 +242,28 @@ def test_matmul_v06_q8_mode_bitexact(ctx, oracle, ty, batch, k, n):
     t.free()
 
 
+@pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0])
+@pytest.mark.parametrize("batch,k,n", [(32, 2048, 2048), (32, 2048, 256), (37, 4096, 300), (16, 256, 45),
+                                       (48, 5632, 33), (17, 11008, 1)])
+def test_blocksum_rows_bitexact(ctx, oracle, ty, batch, k, n):
+    """dot_q4_0_fp32 / dot_q8_0_fp32 numerics on whole 16-token groups of the
+    staged two-row kernel (K % 256 == 0), the rest of the tokens per token:
+    tensor_matmul_batch for both types and tensor_matmul_batch_v06 with
+    MEMVANTA_FORCE_Q8_ACT for Q8_0; the TinyLlama-1.1B attention shapes, rows
+    off the 32-row tile down to one row, one-unit rows, ragged batches."""
+    rng = np.random.default_rng(batch * 7 + k + n + ty)
+    w = _w(rng, ty, n, k)
+    t = ctx.upload("blk.0.attn_q.weight", ty, k, n, w)
+    x = synth.activations(rng, batch, k)
+    want = oracle.matmul_batch(w, ty, n, k, x)
+    assert_bitexact(ctx.matmul_batch(t, x), want, f"matmul_batch B={batch} K={k} N={n}")
+    if ty == synth.Q8_0:
+        want_v06 = oracle.matmul_batch_v06(w, ty, n, k, x, is_ffn=False, force_q8=True)
+        assert_bitexact(want_v06, want, "FORCE_Q8 Q8_0 is the per-token dot")
+        assert_bitexact(ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8), want, f"v06 q8 B={batch} K={k} N={n}")
+    t.free()
+
+
 @pytest.mark.parametrize("batch,k,n", [(32, 4096, 4096), (128, 4096, 1024), (512, 4096, 256), (32, 4096, 11008),
                                         (32, 11008, 4096), (33, 256, 100), (3, 512, 17), (70, 768, 45),
                                         (300, 4096, 1000), (257, 256, 63), (400, 11008, 70)])
