@@ -996,6 +996,107 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
     }
 }
 
+// Q6_K for whole groups of 16 tokens (tensor_matmul_batch / the model's
+// prefill): the same exact f32 weights (d*sc)*q and double products as
+// gemv_q6_k_kernel, each weight dequantized once for eight tokens.  A
+// workgroup covers 16 rows x 16 tokens; thread (row quad, token half, unit
+// slot s) sums rows 4rq..4rq+3 x tokens 8th..8th+7 over the 64-element units
+// u = s, s + 32, .. of the rows (unit u: super-block u / 4, half g, sixteen-
+// column group h, as gemv_q6_k_kernel's), keeping 32 double partials; the
+// 32 slot partials of each (row, token) are then added in slot order.  The
+// four row-quad lanes of a unit read the same activations, so a wave's loads
+// touch 16 units.  Like gemv_q6_k_kernel the double sum runs in another
+// order than the reference's, with the same bound on the difference.
+constexpr int kQ6BRows = 16, kQ6BTok = 16, kQ6BSlots = 32;
+
+__global__ __launch_bounds__(256) void gemv_q6_k_batch_kernel(const uint8_t* __restrict__ W,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              int N, int K) {
+    __shared__ double s_part[kQ6BSlots][kQ6BRows * kQ6BTok + 1];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int rq = lane & 3, th = wave & 1, slot = (lane >> 2) + 16 * (wave >> 1);
+    const int nsb = K / 256, nunits = 4 * nsb;
+    const int row0 = blockIdx.x * kQ6BRows + 4 * rq;
+    const int tok0 = blockIdx.y * kQ6BTok + 8 * th;
+    const size_t row_bytes = static_cast<size_t>(nsb) * 210;
+    const uint8_t* rbase[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rbase[r] = W + static_cast<size_t>(min(row0 + r, N - 1)) * row_bytes;
+
+    double acc[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[r][k] = 0.0;
+    for (int u = slot; u < nunits; u += kQ6BSlots) {
+        const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
+        // the unit's bytes of each row: ql at g*64 + h*16 (l = 0, 2) and
+        // g*64 + 32 + h*16 (l = 1, 3), qh at 128 + g*32 + h*16, scales
+        // 192 + g*8 + h + 2l, d at 208 (2-byte aligned: 16-bit loads)
+        uint32_t qa[4][4], qb[4][4], qh[4][4];
+        float dsc[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint8_t* b = rbase[r] + static_cast<size_t>(sb) * 210;
+            const uint16_t* pa = reinterpret_cast<const uint16_t*>(b + g * 64 + h * 16);
+            const uint16_t* pb = reinterpret_cast<const uint16_t*>(b + g * 64 + 32 + h * 16);
+            const uint16_t* ph = reinterpret_cast<const uint16_t*>(b + 128 + g * 32 + h * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qa[r][i] = pa[2 * i] | (static_cast<uint32_t>(pa[2 * i + 1]) << 16);
+                qb[r][i] = pb[2 * i] | (static_cast<uint32_t>(pb[2 * i + 1]) << 16);
+                qh[r][i] = ph[2 * i] | (static_cast<uint32_t>(ph[2 * i + 1]) << 16);
+            }
+            const float d = h2f(*reinterpret_cast<const uint16_t*>(b + 208));
+            const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + g * 8 + h);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) dsc[r][l] = d * static_cast<float>(sc[2 * l]);
+        }
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {  // columns 4jq .. 4jq+3 of the group
+                float4 xv[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    xv[k] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(tok0 + k) * K + sb * 256 +
+                                                             g * 128 + l * 32 + h * 16 + 4 * jq);
+                double wv[4][4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t lw = (l & 1) ? qb[r][jq] : qa[r][jq];
+                    const uint32_t hw = qh[r][jq];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int lo = static_cast<int>((lw >> (8 * e + 4 * (l >> 1))) & 15u);
+                        const int hi = static_cast<int>((hw >> (8 * e + 2 * l)) & 3u);
+                        wv[r][e] = static_cast<double>(dsc[r][l] * static_cast<float>((lo | (hi << 4)) - 32));
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const double xd[4] = {static_cast<double>(xv[k].x), static_cast<double>(xv[k].y),
+                                          static_cast<double>(xv[k].z), static_cast<double>(xv[k].w)};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[r][k] = fma(wv[r][e], xd[e], acc[r][k]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s_part[slot][(4 * rq + r) * kQ6BTok + 8 * th + k] = acc[r][k];
+    __syncthreads();
+    const int orow = blockIdx.x * kQ6BRows + t / kQ6BTok, otok = blockIdx.y * kQ6BTok + t % kQ6BTok;
+    double tot = 0.0;
+#pragma unroll
+    for (int s2 = 0; s2 < kQ6BSlots; ++s2) tot += s_part[s2][t];
+    if (orow < N) y[static_cast<size_t>(otok) * N + orow] = static_cast<float>(tot);
+}
+
 // F32 weights (dot_f32_simd, src/gguf_kernels.cpp:228-234, as tensor_matvec
 // and tensor_matmul_batch call it): per (row, token) eight accumulators
 // t_j = fma(w[i+j], x[i+j], t_j) over i = 0, 8, .. (< cols & ~7), held by a
@@ -1270,6 +1371,18 @@ hipError_t launch_gemv_f16(const uint16_t* W, const float* x, float* y, size_t r
 
 hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                             hipStream_t st) {
+    if (!rows || !batch) return hipSuccess;
+    if (batch >= kQ6BTok) {
+        // whole groups of kQ6BTok tokens on the batch kernel, the rest per token below
+        const size_t groups = batch / kQ6BTok;
+        const dim3 bgrid(static_cast<unsigned>((rows + kQ6BRows - 1) / kQ6BRows), static_cast<unsigned>(groups));
+        gemv_q6_k_batch_kernel<<<bgrid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), static_cast<int>(cols));
+        const size_t done = groups * kQ6BTok;
+        if (done == batch) return hipGetLastError();
+        x += done * cols;
+        y += done * rows;
+        batch -= done;
+    }
     const dim3 grid(static_cast<unsigned>((rows + kQ6RowsPerWg - 1) / kQ6RowsPerWg), static_cast<unsigned>(batch));
     gemv_q6_k_kernel<<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
                                                                      static_cast<int>(cols));

@@ -182,6 +182,27 @@ def test_gemv_q6_k(ctx, oracle, k, n):
     t.free()
 
 
+@pytest.mark.parametrize("k,n,batch", [(5632, 2048, 32), (2048, 300, 37), (11008, 17, 16), (256, 64, 20),
+                                       (6144, 1, 48)])
+def test_q6_k_token_groups(ctx, oracle, k, n, batch):
+    """tensor_matmul_batch of Q6_K weights (dot_q6_k_fp32 per token) with whole
+    16-token groups on the batch kernel and the rest per token: the
+    TinyLlama-1.1B ffn_down shape, rows off the 16-row tile down to one row,
+    odd super-block counts, one super-block per row; every token within 2 ulp
+    of the oracle, nearly all bit-identical."""
+    rng = np.random.default_rng(5 * k + n + batch)
+    w = _w(rng, synth.Q6_K, n, k)
+    t = ctx.upload("blk.0.ffn_down.weight", synth.Q6_K, k, n, w)
+    x = synth.activations(rng, batch, k)
+    got = ctx.matmul_batch(t, x)
+    want = oracle.matmul_batch(w, synth.Q6_K, n, k, x, threads=16)
+    u = ulp_diff(got, want)
+    assert u.max() <= 2, u.max()
+    assert (u == 0).mean() >= 0.999, (u == 0).mean()
+    assert_bitexact(ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8), got, "v06 of Q6_K is the same per-token dot")
+    t.free()
+
+
 def test_matvec_errors_match_reference_text(ctx):
     w = np.zeros(210, np.uint8)
     t = ctx.upload("blk.3.ffn_down.weight", synth.Q6_K, 128, 2, w)
