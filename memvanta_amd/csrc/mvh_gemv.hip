@@ -942,58 +942,121 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
 // can differ from it only when the exact sum lies within ~1e-13 (relative) of
 // an f32 rounding boundary.
 constexpr int kQ6Threads = 256;
-constexpr int kQ6RowsPerWg = 4;  // one row per wave
 
+// LPR lanes per row (64: one row per wave; 32: two), chosen per K so that
+// the rows' 64-element units fill the lanes (K = 2048: 32 units; K = 5632: 88
+// units in three rounds of 32 rather than two of 64 with 40 lanes idle in
+// the second).
+template <int LPR>
 __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __restrict__ W,
                                                                const float* __restrict__ x, float* __restrict__ y,
                                                                int N, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
     float* s_x = reinterpret_cast<float*>(smem);
+    constexpr int kRpw = 64 / LPR;  // rows per wave
+    const int nsb = K / 256;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l = lane % LPR;
+    const int row = blockIdx.x * (kQ6Threads / 64) * kRpw + wave * kRpw + lane / LPR;
+    // rows past N sum row N - 1 (the lane groups reduce together) and are not written
+    const uint8_t* rb = W + static_cast<size_t>(min(row, N - 1)) * nsb * 210;
+    const int units = 4 * nsb;
+    // unit u of the row: ql bytes g*64 + h*16 (elements j = 0, 2) and
+    // g*64 + 32 + h*16 (j = 1, 3), qh bytes 128 + g*32 + h*16, scales
+    // 192 + g*8 + h + 2j, d at 208; the bytes are 2-aligned (16-bit loads)
+    struct Raw {
+        uint32_t qa[4], qb[4], qh[4];
+        int sc[4];
+        uint32_t d;
+    };
+    auto load_unit = [&](int u, Raw& w) __attribute__((always_inline)) {
+        const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
+        const uint8_t* b = rb + static_cast<size_t>(sb) * 210;
+        const uint16_t* pa = reinterpret_cast<const uint16_t*>(b + g * 64 + h * 16);
+        const uint16_t* pb = reinterpret_cast<const uint16_t*>(b + g * 64 + 32 + h * 16);
+        const uint16_t* ph = reinterpret_cast<const uint16_t*>(b + 128 + g * 32 + h * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w.qa[i] = pa[2 * i] | (static_cast<uint32_t>(pa[2 * i + 1]) << 16);
+            w.qb[i] = pb[2 * i] | (static_cast<uint32_t>(pb[2 * i + 1]) << 16);
+            w.qh[i] = ph[2 * i] | (static_cast<uint32_t>(ph[2 * i + 1]) << 16);
+        }
+        const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + g * 8 + h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w.sc[j] = sc[2 * j];
+        w.d = *reinterpret_cast<const uint16_t*>(b + 208);
+    };
+    double acc = 0.0;
+    auto sum_unit = [&](int u, const Raw& w) __attribute__((always_inline)) {
+        const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
+        const float d = h2f(w.d);
+        float dsc[4], off[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            dsc[j] = d * static_cast<float>(w.sc[j]);
+            off[j] = -32.0f * dsc[j];  // exact (a power-of-two multiple)
+        }
+        const float* xb = s_x + sb * 256 + g * 128 + h * 16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // columns 4c .. 4c+3 of the group
+            // the 6-bit codes u = q + 32 of element group j as four bytes:
+            // low nibbles (j = 0, 1) or high nibbles (j = 2, 3) of ql, bits
+            // 2j..2j+1 of qh above them
+            const uint32_t qa = w.qa[c], qb = w.qb[c], qh = w.qh[c];
+            const uint32_t u[4] = {(qa & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u),
+                                   (qb & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u),
+                                   ((qa >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u),
+                                   ((qb >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // (d*sc)*(u - 32) rounded once: fma(u, d*sc, -32*d*sc) is
+                    // the exact product before its one rounding
+                    const float uf = static_cast<float>((u[j] >> (8 * e)) & 0xffu);
+                    const float wv = fmaf(uf, dsc[j], off[j]);
+                    acc = fma(static_cast<double>(wv), static_cast<double>(xb[j * 32 + 4 * c + e]), acc);
+                }
+            }
+        }
+    };
+    // up to three units per lane: every unit's bytes are loaded before the
+    // activation is staged and before any unit is summed (one memory round
+    // trip per lane rather than one per unit); a lane without a third (or
+    // second) unit reloads its first and skips it
+    const bool pre = units <= 3 * LPR;
+    Raw w[3];
+    if (pre) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) load_unit(l + i * LPR < units ? l + i * LPR : l, w[i]);
+    }
     const float* xt = x + static_cast<size_t>(blockIdx.y) * K;
     for (int c = threadIdx.x; c < K / 4; c += blockDim.x)
         reinterpret_cast<float4*>(s_x)[c] = reinterpret_cast<const float4*>(xt)[c];
     __syncthreads();
-    const int nsb = K / 256;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = blockIdx.x * kQ6RowsPerWg;
-    for (int rr = wave; rr < kQ6RowsPerWg; rr += kQ6Threads / 64) {
-        const int row = r0 + rr;
-        if (row >= N) break;
-        const uint8_t* rb = W + static_cast<size_t>(row) * nsb * 210;
-        double acc = 0.0;
-        for (int u = lane; u < 4 * nsb; u += 64) {
-            const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
-            const uint8_t* b = rb + static_cast<size_t>(sb) * 210;
-            const uint16_t* qla = reinterpret_cast<const uint16_t*>(b + g * 64 + h * 16);
-            const uint16_t* qlb = reinterpret_cast<const uint16_t*>(b + g * 64 + 32 + h * 16);
-            const uint16_t* qh = reinterpret_cast<const uint16_t*>(b + 128 + g * 32 + h * 16);
-            const float d = h2f(*reinterpret_cast<const uint16_t*>(b + 208));
-            const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + g * 8 + h);
-            float dsc[4];
+    if (pre) {
 #pragma unroll
-            for (int l = 0; l < 4; ++l) dsc[l] = d * static_cast<float>(sc[2 * l]);
-            const float* xb = s_x + sb * 256 + g * 128 + h * 16;
-#pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                const uint32_t a = qla[p], bb = qlb[p], hh = qh[p];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int jj = 2 * p + e;
-                    const uint32_t la = (a >> (8 * e)) & 0xffu, lb = (bb >> (8 * e)) & 0xffu, hb = (hh >> (8 * e)) & 0xffu;
-                    const int lo[4] = {static_cast<int>(la & 15), static_cast<int>(lb & 15), static_cast<int>(la >> 4),
-                                       static_cast<int>(lb >> 4)};
-#pragma unroll
-                    for (int l = 0; l < 4; ++l) {
-                        const int q = (lo[l] | static_cast<int>(((hb >> (2 * l)) & 3u) << 4)) - 32;
-                        const float wv = dsc[l] * static_cast<float>(q);
-                        acc = fma(static_cast<double>(wv), static_cast<double>(xb[l * 32 + jj]), acc);
-                    }
-                }
-            }
+        for (int i = 0; i < 3; ++i)
+            if (l + i * LPR < units) sum_unit(l + i * LPR, w[i]);
+    } else {
+        for (int u = l; u < units; u += LPR) {
+            Raw w;
+            load_unit(u, w);
+            sum_unit(u, w);
         }
-        const double tot = wave_sum(acc);
-        if (lane == 0) y[static_cast<size_t>(blockIdx.y) * N + row] = static_cast<float>(tot);
     }
+    double tot;
+    if constexpr (LPR == 64) {
+        tot = wave_sum(acc);
+    } else {  // within each 32-lane half
+        acc += swz_xor<16>(acc);
+        acc += swz_xor<8>(acc);
+        acc += swz_xor<4>(acc);
+        acc += swz_xor<2>(acc);
+        acc += swz_xor<1>(acc);
+        tot = acc;
+    }
+    if (l == 0 && row < N) y[static_cast<size_t>(blockIdx.y) * N + row] = static_cast<float>(tot);
 }
 
 // Q6_K for whole groups of 16 tokens (tensor_matmul_batch / the model's
@@ -1383,9 +1446,16 @@ hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t r
         y += done * rows;
         batch -= done;
     }
-    const dim3 grid(static_cast<unsigned>((rows + kQ6RowsPerWg - 1) / kQ6RowsPerWg), static_cast<unsigned>(batch));
-    gemv_q6_k_kernel<<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
-                                                                     static_cast<int>(cols));
+    const size_t units = cols / 64;  // 64-element units per row
+    const bool half = (units + 31) / 32 * 32 < (units + 63) / 64 * 64;  // fewer idle lanes at 32 per row
+    const size_t rpw = half ? 8 : 4;                                    // rows per workgroup
+    const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw), static_cast<unsigned>(batch));
+    if (half)
+        gemv_q6_k_kernel<32><<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
+                                                                             static_cast<int>(cols));
+    else
+        gemv_q6_k_kernel<64><<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
+                                                                             static_cast<int>(cols));
     return hipGetLastError();
 }
 
