@@ -1127,14 +1127,18 @@ __global__ __launch_bounds__(256) void gemv_q6_k_batch_kernel(const uint8_t* __r
                 double wv[4][4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
+                    // the 6-bit codes u = q + 32 of the four columns as bytes
+                    // (nibble of ql, bits 2l..2l+1 of qh above it); each
+                    // weight (d*sc)*(u - 32) by one fma from its exact value
                     const uint32_t lw = (l & 1) ? qb[r][jq] : qa[r][jq];
                     const uint32_t hw = qh[r][jq];
+                    const uint32_t lo4 = (l >> 1) ? (lw >> 4) & 0x0f0f0f0fu : lw & 0x0f0f0f0fu;
+                    const uint32_t hi2 = (2 * l <= 4 ? hw << (4 - 2 * l) : hw >> (2 * l - 4)) & 0x30303030u;
+                    const uint32_t u = lo4 | hi2;
+                    const float off = -32.0f * dsc[r][l];  // exact (a power-of-two multiple)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int lo = static_cast<int>((lw >> (8 * e + 4 * (l >> 1))) & 15u);
-                        const int hi = static_cast<int>((hw >> (8 * e + 2 * l)) & 3u);
-                        wv[r][e] = static_cast<double>(dsc[r][l] * static_cast<float>((lo | (hi << 4)) - 32));
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        wv[r][e] = static_cast<double>(fmaf(static_cast<float>((u >> (8 * e)) & 0xffu), dsc[r][l], off));
                 }
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
