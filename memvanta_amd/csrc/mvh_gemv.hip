@@ -714,8 +714,8 @@ __global__ __launch_bounds__(256) void batch_f32act_lanes_kernel(const uint8_t* 
 // activation reads from LDS per fma.
 //
 // BS = true: dot_q4_0_fp32 / dot_q8_0_fp32 numerics (src/gguf_kernels.cpp:
-// 93-120, tensor_matmul_batch_v06 with MEMVANTA_FORCE_Q8_ACT for Q8_0
-// weights, and the per-token remainders): per block, lane j's t_j over
+// 93-120; tensor_matmul_batch, and tensor_matmul_batch_v06 with
+// MEMVANTA_FORCE_Q8_ACT for Q8_0 weights): per block, lane j's t_j over
 // elements j, j+8, j+16, j+24 from zero, s = t0 + ... + t7 in order, then
 // sum = fma(d, s, sum) over the blocks in order.  The same tile and staging;
 // thread (block jb, row pair, token group) owns block jb of each unit for two
