@@ -7,16 +7,20 @@ Q4_0, output Q6_K; weights N(0, 0.02), drawn and quantized on the device),
 ctx 768, batch 32, paged F16 KV (128-token pages) -- the protocol of the
 reference's real_model_bench (benchmarks/real_model_bench.cpp:20-27):
 
-* tg: reset, prefill a 128-token seed, then greedy decode from token 17.
-  One step = one decode token; the K timed steps run as the device-resident
-  greedy loop (one captured HIP graph per token, argmax on the device).
-  `value` = K / time (tok/s).  The per-call API rate (forward() + host argmax,
-  as the reference's loop does) is reported beside it.
+* tg128: reset, prefill a 128-token seed (untimed), then 128 greedy decode
+  tokens from token 17, timed -- the reference's tg rep.  One step = one whole
+  tg128 rep; the 128 tokens run as the device-resident greedy loop (one
+  captured HIP graph per token, argmax on the device) at positions 128..255.
+  `value` = 128 * K / (the K reps' decode seconds) (tok/s); `ms_per_step` =
+  the mean decode time of one rep.  The per-call API rate (forward() + host
+  argmax, as the reference's loop does) is reported beside it.
 * pp512: reset, prefill 512 prompt ids in chunks of 32 with last-token
   logits (tensor_matmul_batch_v06 numerics, MEMVANTA_FORCE_Q8_ACT=1 mode), and
   the same with the default prefill numerics (no MEMVANTA_FORCE_Q8_ACT), the
   numerics of the reference's published pp512.
-* prompt ids follow the reference bench's fixed_tokens: (i*1543+17) % vocab.
+* prompt and seed ids are seeded uniform in [0, vocab) (the 7B config's
+  protocol); one more tg128 rep seeded with the reference bench's
+  fixed_tokens ((i*1543+17) % vocab) is reported beside it.
 * the same tg and pp512 are timed beside it with F32 and Q8 KV pages
   (LlamaModel's kv_type) and reported under config.other_kv_cache_types.
 
@@ -65,6 +69,8 @@ sys.path.insert(0, ROOT)
 METRIC = "tg128 tok/s + achieved HBM GB/s (7B-shape Q4_0); pp512 prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 CTX, BATCH, PAGE, SEED_TOKENS, PROMPT_TOKENS, FIRST_TOKEN = 768, 32, 128, 128, 512, 17
+TG_TOKENS = 128          # decode tokens of one tg rep (tg128)
+PROMPT_SEED_7B = 2026    # seed of the 7B model's uniform prompt / seed ids
 # per-layer decode GEMV launches of the 7B shape (K, N, launches per layer)
 DECODE_GEMVS = [(4096, 12288, 1), (4096, 4096, 1), (4096, 22016, 1), (11008, 4096, 1)]
 GEMV_CONFIG = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]  # the isolated-GEMV config (K, N)
@@ -371,28 +377,60 @@ def pp_whole_prompt(m, prompt, reps: int):
     return rates, bool(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))
 
 
-def time_tg(m, seed, steps: int, warmup: int):
-    """Greedy decode rate after the seed prefill: (tok/s, ids), device-resident loop."""
+def tg_reps(m, seed, gen: int, reps: int, warmup: int):
+    """The reference bench's tg rep (benchmarks/real_model_bench.cpp:22):
+    reset, untimed prefill of `seed` in chunks of BATCH, then `gen` greedy
+    tokens from token 17 timed, here as the device-resident loop.  `warmup`
+    untimed reps first (the first captures the decode graph), then `reps`
+    timed ones.  Returns the per-rep wall seconds (between device
+    synchronizations), the per-rep device seconds (HIP events on the model's
+    stream around the decode), the ids of the last rep and whether every rep
+    produced the same ids."""
     import torch
 
-    m.reset()
-    m.prefill(seed, BATCH, logits=False)
-    if warmup:
-        m.generate_greedy(FIRST_TOKEN, warmup)
-    m.reset()
-    m.prefill(seed, BATCH, logits=False)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ids = m.generate_greedy(FIRST_TOKEN, steps)
-    torch.cuda.synchronize()
-    return steps / (time.perf_counter() - t0), [int(i) for i in ids]
+    stream = torch.cuda.ExternalStream(m.stream)
+    wall, dev, first = [], [], None
+    same = True
+    ids = []
+    for r in range(warmup + reps):
+        m.reset()
+        m.prefill(seed, BATCH, logits=False)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+        ids = [int(i) for i in m.generate_greedy(FIRST_TOKEN, gen)]
+        with torch.cuda.stream(stream):
+            e1.record(stream)
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+        if first is None:
+            first = ids
+        same = same and ids == first
+        if r >= warmup:
+            wall.append(t)
+            dev.append(e0.elapsed_time(e1) * 1e-3)
+    return wall, dev, ids, same
 
 
-def default_numerics_run(path: str, prompt, ctx_len: int, seed, n_ids: int):
+def time_tg(m, seed, gen: int, reps: int, warmup: int):
+    """tg<gen> rate over `reps` timed reps: (tok/s, ids of the last rep)."""
+    wall, _, ids, _ = tg_reps(m, seed, gen, reps, warmup)
+    return gen * len(wall) / sum(wall), ids
+
+
+def default_numerics_run(path: str, prompt, ctx_len: int, seed, n_ids: int, logits_path: str | None = None):
     """pp with tensor_matmul_batch_v06's default numerics (no
     MEMVANTA_FORCE_Q8_ACT: fp32 activations, batch8 / batch4 accumulators),
     and the greedy ids of n_ids decode steps after a default-numerics prefill
-    of seed (the CPU leg's protocol, for the id comparison)."""
+    of seed (the CPU leg's protocol, for the id comparison): forward() with the
+    host argmax, each step's logits saved to logits_path (.npy, [n_ids][vocab])
+    for the CPU leg's logits comparison; then the device-resident loop from the
+    same state, whose ids must equal those.  Returns (pp tok/s, ids, pp as one
+    batch tok/s, its logits equal to chunks of 32, graph ids equal)."""
+    import numpy as np
+
     from memvanta_amd import capi
 
     m = capi.Model(path, ctx=ctx_len, page_tokens=PAGE, act_mode=capi.MVH_ACT_REF, max_batch=len(prompt))
@@ -401,13 +439,24 @@ def default_numerics_run(path: str, prompt, ctx_len: int, seed, n_ids: int):
         whole, same = pp_whole_prompt(m, prompt, 1)
         m.reset()
         m.prefill(seed, BATCH, logits=False)
-        return pp, [int(i) for i in m.generate_greedy(FIRST_TOKEN, n_ids)], whole[0], same
+        ids, lgs, cur = [], [], FIRST_TOKEN
+        for _ in range(n_ids):
+            lg = np.array(m.forward(cur), dtype=np.float32, copy=True)
+            cur = int(np.argmax(lg))
+            ids.append(cur)
+            lgs.append(lg)
+        if logits_path:
+            np.save(logits_path, np.stack(lgs))
+        m.reset()
+        m.prefill(seed, BATCH, logits=False)
+        graph_same = [int(i) for i in m.generate_greedy(FIRST_TOKEN, n_ids)] == ids
+        return pp, ids, whole[0], same, graph_same
     finally:
         m.close()
 
 
-def time_kv_types(path: str, steps: int, warmup: int):
-    """tg and pp512 of the same model with the F32 and Q8 KV cache types
+def time_kv_types(path: str, seed, prompt, reps: int, warmup: int):
+    """tg128 and pp512 of the same model with the F32 and Q8 KV cache types
     (LlamaModel's kv_type; decode attention then runs as RoPE + KV write +
     scores + softmax-V launches instead of the fused F16 kernel)."""
     from memvanta_amd import capi
@@ -415,17 +464,16 @@ def time_kv_types(path: str, steps: int, warmup: int):
     out = []
     for kt in (capi.MVH_KV_F32, capi.MVH_KV_Q8):
         m = capi.Model(path, ctx=CTX, page_tokens=PAGE, act_mode=capi.MVH_ACT_Q8, max_batch=BATCH, kv_type=kt)
-        seed, prompt = fixed_tokens(SEED_TOKENS, m.vocab), fixed_tokens(PROMPT_TOKENS, m.vocab)
         pp = time_pp(m, prompt)[0]
-        tg, ids = time_tg(m, seed, steps, warmup)
-        out.append({"kv": capi.kv_type_name(kt), "tg_tok_s": round(tg, 2), "pp512_tok_s": round(pp, 1),
-                    "kv_bytes_after_tg": m.kv_bytes(), "greedy_ids_head": ids[:4]})
+        tg, ids = time_tg(m, seed, TG_TOKENS, reps, warmup)
+        out.append({"kv": capi.kv_type_name(kt), "tg128_tok_s": round(tg, 2), "tg128_reps": reps,
+                    "pp512_tok_s": round(pp, 1), "kv_bytes_after_tg": m.kv_bytes(), "greedy_ids_head": ids[:4]})
         m.close()
     return out
 
 
 def time_other_model(tmpdir: str, label: str, cfg_name: str, ctx_len: int, pp_n: int, seed_n: int, tg_n: int,
-                     prompt_seed: int, cpu_run, warmup: int):
+                     prompt_seed: int, cpu_run, reps: int, warmup: int):
     """pp / tg of one of the other model configs (random-init, written on the device)."""
     import torch
 
@@ -440,19 +488,22 @@ def time_other_model(tmpdir: str, label: str, cfg_name: str, ctx_len: int, pp_n:
     m = capi.Model(path, ctx=ctx_len, page_tokens=PAGE, act_mode=capi.MVH_ACT_Q8, max_batch=BATCH)
     try:
         pp = time_pp(m, prompt, reps=3)
-        tg, ids = time_tg(m, seed, tg_n, warmup)
+        tg, ids = time_tg(m, seed, tg_n, reps, warmup)
     finally:
         m.close()
     cpu_seed, cpu_tg = cpu_run
-    pp_default, ref_ids, _, _ = default_numerics_run(path, prompt, ctx_len, prompt[:cpu_seed], cpu_tg)
+    lg_path = os.path.join(tmpdir, f"{cfg_name}_gpu_logits.npy")
+    pp_default, ref_ids, _, _, graph_same = default_numerics_run(path, prompt, ctx_len, prompt[:cpu_seed], cpu_tg,
+                                                                 lg_path)
     res = {"workload": f"{label}: {cfg.name} (dim {cfg.dim}, FFN {cfg.ffn}, {cfg.layers} layers, "
                        f"{cfg.heads}/{cfg.kv_heads} heads, vocab {cfg.vocab}), ctx {ctx_len}, batch {BATCH}, "
                        f"paged F16 KV, prompt ids uniform from seed {prompt_seed}",
            "pp_tokens": pp_n, "pp_tok_s": round(sum(pp) / len(pp), 1), "pp_tok_s_reps": [round(v, 1) for v in pp],
            "pp_default_numerics_tok_s": round(pp_default, 1),
-           "tg_tokens": tg_n, "tg_after_seed_tokens": seed_n, "tg_tok_s": round(tg, 2),
-           "greedy_ids_head": ids[:8]}
-    spec = {"path": path, "ctx": ctx_len, "seed_ids": [int(t) for t in prompt[:cpu_seed]], "tg_tokens": cpu_tg}
+           "tg_tokens": tg_n, "tg_after_seed_tokens": seed_n, "tg_reps": reps, "tg_tok_s": round(tg, 2),
+           "greedy_ids_head": ids[:8], "graph_ids_equal_forward_ids": graph_same}
+    spec = {"path": path, "ctx": ctx_len, "seed_ids": [int(t) for t in prompt[:cpu_seed]], "tg_tokens": cpu_tg,
+            "gpu_logits": lg_path}
     return res, spec, ref_ids
 
 
@@ -478,12 +529,33 @@ def _lscpu() -> dict:
     return out
 
 
-def _cpu_model_run(lib, path, ctx_len, threads, seed_ids, n_tg, force_q8=False, warm_chunk=True):
+def _logits_vs_gpu(cpu_logits, gpu_path):
+    """Per-step logits of the CPU run against the GPU's saved ones: the largest
+    relative L2 difference and the smallest bit-identical fraction over the
+    steps both ran."""
+    import numpy as np
+
+    g = np.load(gpu_path, allow_pickle=False)
+    n = min(len(cpu_logits), len(g))
+    rels, fracs = [], []
+    for c, x in zip(cpu_logits[:n], g[:n]):
+        c64 = np.asarray(c, np.float64)
+        rels.append(float(np.linalg.norm(np.asarray(x, np.float64) - c64) / np.linalg.norm(c64)))
+        fracs.append(float((np.asarray(c, np.float32).view(np.uint32) == np.asarray(x, np.float32).view(np.uint32))
+                           .mean()))
+    return {"logits_steps_compared": n, "logits_max_rel_l2": max(rels) if rels else None,
+            "logits_min_bit_identical_frac": round(min(fracs), 6) if fracs else None}
+
+
+def _cpu_model_run(lib, path, ctx_len, threads, seed_ids, n_tg, force_q8=False, warm_chunk=True, gpu_logits=None):
     """Seed prefill + greedy decode on the CPU model: pp tok/s, tg tok/s, ids.
-    One untimed chunk first touches every weight page."""
+    One untimed chunk first touches every weight page.  With gpu_logits (a
+    .npy of the GPU's per-step decode logits from the same state), every
+    step's logits are compared with the GPU's after the timing."""
     import numpy as np
 
     m = lib.model(path, ctx=ctx_len, page=PAGE, threads=threads, force_q8=force_q8)
+    keep = []
     try:
         if warm_chunk:
             m.prefill(seed_ids[:BATCH], BATCH, logits=False)
@@ -492,17 +564,26 @@ def _cpu_model_run(lib, path, ctx_len, threads, seed_ids, n_tg, force_q8=False, 
         m.prefill(seed_ids, BATCH, logits=False)
         pp_s = time.perf_counter() - t0
         ids, cur = [], FIRST_TOKEN
-        cur = int(np.argmax(m.forward(cur)))  # first decode step: untimed
+        lg = m.forward(cur)  # first decode step: untimed
+        cur = int(np.argmax(lg))
         ids.append(cur)
+        if gpu_logits:
+            keep.append(np.array(lg, np.float32, copy=True))
         t0 = time.perf_counter()
         for _ in range(n_tg - 1):
-            cur = int(np.argmax(m.forward(cur)))
+            lg = m.forward(cur)
+            cur = int(np.argmax(lg))
             ids.append(cur)
+            if gpu_logits:
+                keep.append(np.array(lg, np.float32, copy=True))
         tg_s = time.perf_counter() - t0
     finally:
         m.close()
-    return {"pp_tok_s": round(len(seed_ids) / pp_s, 3), "pp_tokens": len(seed_ids), "pp_s": round(pp_s, 2),
-            "tg_tok_s": round((n_tg - 1) / tg_s, 3), "tg_tokens_timed": n_tg - 1, "tg_s": round(tg_s, 2)}, ids
+    res = {"pp_tok_s": round(len(seed_ids) / pp_s, 3), "pp_tokens": len(seed_ids), "pp_s": round(pp_s, 2),
+           "tg_tok_s": round((n_tg - 1) / tg_s, 3), "tg_tokens_timed": n_tg - 1, "tg_s": round(tg_s, 2)}
+    if gpu_logits:
+        res.update(_logits_vs_gpu(keep, gpu_logits))
+    return res, ids
 
 
 def _cpu_pp_only(lib, path, ctx_len, threads, ids, force_q8):
@@ -584,7 +665,8 @@ def cpu_leg(spec: dict) -> dict:
     res = {"kind": kind, "library": note, "threads": t_all, "lscpu": _lscpu(),
            "omp": {k: os.environ.get(k) for k in ("OMP_PROC_BIND", "OMP_PLACES", "OMP_NUM_THREADS")}}
     t0 = time.perf_counter()
-    run, ids = _cpu_model_run(lib, s["path"], CTX, t_all, s["seed_ids"], s["tg_tokens"])
+    run, ids = _cpu_model_run(lib, s["path"], CTX, t_all, s["seed_ids"], s["tg_tokens"],
+                              gpu_logits=s.get("gpu_logits"))
     res["llama7b"] = dict(run, greedy_ids=ids)
     log(f"cpu leg: 7B seed prefill + {s['tg_tokens']} decode tokens on {t_all} threads "
         f"({time.perf_counter() - t0:.1f} s)")
@@ -601,7 +683,8 @@ def cpu_leg(spec: dict) -> dict:
     log("cpu leg: isolated kernels done")
     res["other_models"] = []
     for o in spec["other_models"]:
-        r, oids = _cpu_model_run(lib, o["path"], o["ctx"], t_all, o["seed_ids"], o["tg_tokens"])
+        r, oids = _cpu_model_run(lib, o["path"], o["ctx"], t_all, o["seed_ids"], o["tg_tokens"],
+                                 gpu_logits=o.get("gpu_logits"))
         res["other_models"].append(dict(r, greedy_ids=oids))
     log("cpu leg: other models done")
     return res
@@ -636,8 +719,11 @@ def run_cpu_leg(spec: dict, timeout_s: float):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128, help="timed decode tokens (tg128)")
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--steps", type=int, default=10,
+                    help="timed tg128 reps (each: reset, untimed 128-token seed prefill, 128 timed decode tokens)")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed tg128 reps before them")
+    ap.add_argument("--side-reps", type=int, default=3,
+                    help="timed tg reps of the KV-type and other-model runs")
     ap.add_argument("--pp-reps", type=int, default=3)
     ap.add_argument("--api-tokens", type=int, default=32, help="decode tokens timed through forward()")
     ap.add_argument("--kernel-launches", type=int, default=96)
@@ -652,6 +738,8 @@ def main():
     ap.add_argument("--model", default=None, help="existing GGUF to use instead of the synthetic 7B shape")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the isolated kernel timings plus the read probe and a 256 MiB copy (counter runs)")
+    ap.add_argument("--tg-only", action="store_true",
+                    help="only the 7B tg128 reps (no pp512, kernel timings, other runs or CPU baseline)")
     ap.add_argument("--cpu-leg", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_leg:
@@ -665,8 +753,8 @@ def main():
         print("bench.py measures one MI355X: this build runs on a single GPU (no multi-GPU path); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    if SEED_TOKENS + args.warmup + args.steps > CTX or PROMPT_TOKENS > CTX:
-        print(f"--warmup + --steps must fit ctx {CTX} after the {SEED_TOKENS}-token seed", file=sys.stderr)
+    if args.steps < 1 or args.warmup < 0 or args.side_reps < 1:
+        print("--steps and --side-reps must be >= 1, --warmup >= 0", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -711,33 +799,34 @@ def main():
         t_load = time.perf_counter() - t0
         stream = torch.cuda.ExternalStream(m.stream)
         vocab = m.vocab
-        seed, prompt = fixed_tokens(SEED_TOKENS, vocab), fixed_tokens(PROMPT_TOKENS, vocab)
+        prompt = synth.prompt_tokens(PROMPT_SEED_7B, PROMPT_TOKENS, vocab)
+        seed = prompt[:SEED_TOKENS]
+
+        if args.tg_only:
+            tg_wall, tg_dev, ids, ids_same = tg_reps(m, seed, TG_TOKENS, args.steps, args.warmup)
+            m.close()
+            print(json.dumps({"tg128_tok_s": round(TG_TOKENS * args.steps / sum(tg_wall), 2),
+                              "tg128_tok_s_per_rep": [round(TG_TOKENS / t, 2) for t in tg_wall],
+                              "gpu_ms_per_token": round(sum(tg_dev) / (TG_TOKENS * args.steps) * 1e3, 4),
+                              "ids_head": ids[:8], "ids_identical_across_reps": ids_same,
+                              "attn_ns": os.environ.get("MVH_ATTN_NS")}), flush=True)
+            return
 
         # pp512 (host-driven chunks of 32, last-token logits), after one untimed run
         pp = time_pp(m, prompt, args.pp_reps)
         pp_whole, pp_whole_same = pp_whole_prompt(m, prompt, args.pp_reps)
 
-        # tg: warm-up (captures the decode graph), then the K timed tokens
-        m.reset()
-        m.prefill(seed, BATCH, logits=False)
-        if args.warmup:
-            m.generate_greedy(FIRST_TOKEN, args.warmup)
-        m.reset()
-        m.prefill(seed, BATCH, logits=False)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        w0 = time.perf_counter()
-        with torch.cuda.stream(stream):
-            e0.record(stream)
-        ids = [int(i) for i in m.generate_greedy(FIRST_TOKEN, args.steps)]
-        with torch.cuda.stream(stream):
-            e1.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - w0
-        gpu_s = e0.elapsed_time(e1) * 1e-3
-        tg = args.steps / wall
-        tok_bytes = model_weight_bytes(cfg, synth) * args.steps + kv_read_bytes(cfg, SEED_TOKENS, args.steps)
-        tg_gbs = tok_bytes / wall / 1e9
+        # tg128: W untimed reps (the first captures the decode graph), then K timed reps
+        tg_wall, tg_dev, ids, ids_same = tg_reps(m, seed, TG_TOKENS, args.steps, args.warmup)
+        wall = sum(tg_wall)
+        gpu_s = sum(tg_dev)
+        n_tok = TG_TOKENS * args.steps
+        tg = n_tok / wall
+        tg_rep_rates = [TG_TOKENS / t for t in tg_wall]
+        tok_bytes = model_weight_bytes(cfg, synth) * TG_TOKENS + kv_read_bytes(cfg, SEED_TOKENS, TG_TOKENS)
+        tg_gbs = tok_bytes * args.steps / wall / 1e9
+        # one more rep seeded with the reference bench's fixed_tokens
+        fx_wall, _, fx_ids, _ = tg_reps(m, fixed_tokens(SEED_TOKENS, vocab), TG_TOKENS, 1, 0)
 
         # the same decode through the per-call API: forward() + host argmax
         m.reset()
@@ -750,11 +839,12 @@ def main():
             cur = int(np.argmax(m.forward(cur)))
         api_tg = args.api_tokens / (time.perf_counter() - t0)
         m.close()
-        log(f"7B pp512 / tg{args.steps} done")
+        log(f"7B pp512 / {args.steps} x tg{TG_TOKENS} done")
 
         n_cpu_tg = args.cpu_tg_tokens
-        pp_default, ref_ids, pp_default_whole, pp_default_whole_same = default_numerics_run(
-            path, prompt, CTX, seed, n_cpu_tg)
+        gpu_logits_7b = os.path.join(tmpdir, "openllama-7b_gpu_logits.npy")
+        pp_default, ref_ids, pp_default_whole, pp_default_whole_same, graph_ids_same = default_numerics_run(
+            path, prompt, CTX, seed, n_cpu_tg, gpu_logits_7b)
 
         # dominant kernel alone: Q4_0 x Q8 GEMV; prefill GEMM; measured ceilings
         ctx = capi.Context(0)
@@ -777,13 +867,14 @@ def main():
             with open(pmc) as f:
                 traffic = json.load(f).get("hbm_bytes_per_launch")
 
-        kv_types = None if args.no_kv_types else time_kv_types(path, args.steps, args.warmup)
+        kv_types = None if args.no_kv_types else time_kv_types(path, seed, prompt, args.side_reps,
+                                                               min(args.warmup, 1))
 
         others, other_specs, other_ids = [], [], []
         if not args.no_other_models:
             for label, name, ctx_len, pp_n, seed_n, tg_n, pseed, cpu_run in OTHER_MODELS:
                 r, s, oids = time_other_model(tmpdir, label, name, ctx_len, pp_n, seed_n, tg_n, pseed, cpu_run,
-                                              min(args.warmup, ctx_len - seed_n))
+                                              args.side_reps, min(args.warmup, 1))
                 others.append(r)
                 other_specs.append(s)
                 other_ids.append(oids)
@@ -807,6 +898,7 @@ def main():
             del mats
             spec = {"threads": len(os.sched_getaffinity(0)),
                     "llama7b": {"path": path, "seed_ids": [int(t) for t in seed], "tg_tokens": n_cpu_tg,
+                                "gpu_logits": gpu_logits_7b,
                                 "pp_force_q8_tokens": CPU_PP_FORCE_Q8_TOKENS, "seed_4": CPU_SEED_4_THREADS,
                                 "tg_tokens_4": CPU_TG_4_THREADS},
                     "matrices": {"path": mpath, "shapes": GEMV_CONFIG, "npy": npys,
@@ -847,6 +939,11 @@ def main():
             "greedy_ids_compared": n_cmp,
             "greedy_ids_basis": "GPU ids after a default-numerics seed prefill (the CPU leg's); decode numerics "
                                 "do not depend on the prefill mode, the seed's KV entries do",
+            "logits_steps_compared": c7.get("logits_steps_compared"),
+            "logits_max_rel_l2": c7.get("logits_max_rel_l2"),
+            "logits_min_bit_identical_frac": c7.get("logits_min_bit_identical_frac"),
+            "logits_basis": "every decode step's logits of the CPU run against the GPU's forward() logits at the "
+                            "same step (same seed prefill, same ids); tolerance 1e-3 relative L2",
             "pp_sample_default_numerics_tok_s": c7["pp_tok_s"],
             "pp_sample_default_numerics_tokens": c7["pp_tokens"],
             "pp_sample_force_q8_tok_s": c7["pp_force_q8_tok_s"],
@@ -870,6 +967,9 @@ def main():
                         "tg_tok_s": c["tg_tok_s"], "tg_tokens_timed": c["tg_tokens_timed"],
                         "tg_after_seed_tokens": c["pp_tokens"],
                         "greedy_ids_match_gpu": c["greedy_ids"] == g[:n], "greedy_ids_compared": n,
+                        "logits_steps_compared": c.get("logits_steps_compared"),
+                        "logits_max_rel_l2": c.get("logits_max_rel_l2"),
+                        "logits_min_bit_identical_frac": c.get("logits_min_bit_identical_frac"),
                         "greedy_ids_basis": "GPU ids after a default-numerics prefill of the same seed"}
 
     pp_mean = float(np.mean(pp))
@@ -880,7 +980,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "ms_per_step": round(wall / args.steps * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(tg / REF_TG128_TOKS, 1),
@@ -889,12 +989,26 @@ def main():
         "config": {
             "workload": "tg128 + pp512, OpenLLaMA-7B-v2-shape random-init Q4_0 model (dim 4096, FFN 11008, "
                         "32 layers, 32 heads MHA, vocab 32000, output Q6_K), ctx 768, batch 32, paged F16 KV "
-                        "(128-token pages), greedy",
+                        "(128-token pages), greedy, seeded uniform prompt ids",
+            "step": f"one tg128 rep: reset, untimed prefill of a {SEED_TOKENS}-token seed (chunks of {BATCH}), "
+                    f"then {TG_TOKENS} greedy decode tokens from token {FIRST_TOKEN} timed (positions "
+                    f"{SEED_TOKENS}..{SEED_TOKENS + TG_TOKENS - 1}); value = {TG_TOKENS} x steps / the steps' "
+                    f"decode seconds; ms_per_step = decode ms of one rep",
+            "prompt_ids": f"uniform in [0, {vocab}) from seed {PROMPT_SEED_7B} (numpy default_rng); the tg seed "
+                          f"is the prompt's first {SEED_TOKENS} ids",
             "tg_tok_s": round(tg, 2),
+            "tg_tok_s_per_rep": [round(v, 2) for v in tg_rep_rates],
+            "tg_tokens_timed": n_tok,
+            "tg_ids_identical_across_reps": ids_same,
             "tg_hbm_gbs": round(tg_gbs, 1),
             "tg_hbm_frac": round(tg_gbs / HBM_PEAK_GBS, 4),
-            "tg_bytes_per_token": tok_bytes // args.steps,
-            "tg_gpu_ms_per_token": round(gpu_s / args.steps * 1e3, 4),
+            "tg_bytes_per_token": tok_bytes // TG_TOKENS,
+            "tg_bytes_basis": f"weights + F16 K and V read at positions {SEED_TOKENS}..{SEED_TOKENS + TG_TOKENS - 1}, "
+                              f"averaged over the {TG_TOKENS} tokens",
+            "tg_gpu_ms_per_token": round(gpu_s / n_tok * 1e3, 4),
+            "tg128_fixed_tokens_seed_tok_s": round(TG_TOKENS / fx_wall[0], 2),
+            "tg128_fixed_tokens_seed_ids_head": fx_ids[:8],
+            "graph_ids_equal_forward_ids": graph_ids_same,
             "tg_api_tok_s": round(api_tg, 2),
             "pp512_tok_s": round(pp_mean, 1),
             "pp512_tok_s_reps": [round(v, 1) for v in pp],

@@ -32,9 +32,21 @@ def spec(tmp_path_factory):
         np.save(npys[-1], data)
     mp = str(d / "mats.gguf")
     w.write(mp)
+    # the logits the GPU side would save: here the restatement's own run of the protocol
+    seed_ids = synth.prompt_tokens(5, 40)
+    o = pyoracle.Oracle().model(big, ctx=bench.CTX, page=bench.PAGE, threads=4)
+    o.prefill(seed_ids, bench.BATCH, logits=False)
+    lgs, cur = [], bench.FIRST_TOKEN
+    for _ in range(5):
+        lg = np.array(o.forward(cur), np.float32, copy=True)
+        cur = int(np.argmax(lg))
+        lgs.append(lg)
+    o.close()
+    lpath = str(d / "gpu_logits.npy")
+    np.save(lpath, np.stack(lgs))
     return {"threads": 4,
-            "llama7b": {"path": big, "seed_ids": bench.fixed_tokens(40, 32000).tolist(), "tg_tokens": 5,
-                        "pp_force_q8_tokens": 32, "seed_4": 32, "tg_tokens_4": 3},
+            "llama7b": {"path": big, "seed_ids": seed_ids.tolist(), "tg_tokens": 5,
+                        "pp_force_q8_tokens": 32, "seed_4": 32, "tg_tokens_4": 3, "gpu_logits": lpath},
             "matrices": {"path": mp, "shapes": shapes, "npy": npys, "names": names, "gemm_shapes": [shapes[0]]},
             "other_models": [{"path": tiny, "ctx": 256, "seed_ids": synth.prompt_tokens(2024, 40).tolist(),
                               "tg_tokens": 4}]}
@@ -50,6 +62,11 @@ def _check(res, kind, spec):
     assert res["kernels_4_threads"]["tensor_matmul_batch_v06"] == []
     assert len(res["other_models"][0]["greedy_ids"]) == 4
     assert "CPU(s)" in res["lscpu"]
+    # every decode step's logits compared with the saved ones: the same numerics reproduce them exactly
+    assert res["llama7b"]["logits_steps_compared"] == 5
+    assert res["llama7b"]["logits_max_rel_l2"] == 0.0
+    assert res["llama7b"]["logits_min_bit_identical_frac"] == 1.0
+    assert "logits_steps_compared" not in res["other_models"][0]
 
 
 def test_cpu_leg_port_and_reference_agree(spec, monkeypatch):
@@ -71,6 +88,20 @@ def test_cpu_leg_child_process(spec):
     assert "error" not in res, res
     assert res["omp"]["OMP_PROC_BIND"] == "close" and res["omp"]["OMP_PLACES"] == "cores"
     json.dumps(res)
+
+
+def test_logits_vs_gpu_reports_the_worst_step(tmp_path):
+    rng = np.random.default_rng(3)
+    cpu = [rng.standard_normal(1000).astype(np.float32) for _ in range(3)]
+    gpu = np.stack(cpu).copy()
+    gpu[1, :10] += np.float32(0.5)  # one step differs
+    p = str(tmp_path / "g.npy")
+    np.save(p, gpu)
+    r = bench._logits_vs_gpu(cpu, p)
+    want = np.linalg.norm(gpu[1].astype(np.float64) - cpu[1]) / np.linalg.norm(cpu[1].astype(np.float64))
+    assert r["logits_steps_compared"] == 3
+    assert abs(r["logits_max_rel_l2"] - want) < 1e-12 and r["logits_max_rel_l2"] > 1e-3
+    assert r["logits_min_bit_identical_frac"] == 0.99
 
 
 def test_prefill_roofline_floor():
