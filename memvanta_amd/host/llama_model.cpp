@@ -589,34 +589,46 @@ const std::vector<float>& LlamaModel::prefill(const std::vector<int>& tokens, st
     const int lanes = profiling_ ? 1 : kLanes;
     int prev = -1;
     std::size_t chunk = 0;
-    auto drain = [&] {
-        for (Lane& l : lanes_) check(hipStreamSynchronize(l.st), "sync");
-        ln_ = &lanes_[0];
-    };
-    for (std::size_t i = 0; i < tokens.size(); i += batch_size, ++chunk) {
-        const std::size_t B = std::min(batch_size, tokens.size() - i);
-        const char* err = nullptr;
-        if (pos_ + B > c_.n_ctx) err = "context exhausted";
-        for (std::size_t b = 0; b < B && !err; ++b)
-            if (tokens[i + b] < 0 || static_cast<std::size_t>(tokens[i + b]) >= c_.vocab) err = "token id out of range";
-        if (err) {  // the chunks before this one complete, as in a chunk-by-chunk run
-            drain();
-            throw std::runtime_error(err);
+    // every lane drained and lane 0 current again before the call returns,
+    // also when it throws: a later forward / reset / generate on lane 0 must
+    // not race with chunks still writing the shared KV slab
+    auto drain = [&](bool quiet) {
+        hipError_t first = hipSuccess;
+        for (Lane& l : lanes_) {
+            const hipError_t e = hipStreamSynchronize(l.st);
+            if (first == hipSuccess) first = e;
         }
-        const bool last = compute_logits_last && i + B == tokens.size();
-        const int lane = static_cast<int>(chunk % lanes);
-        ln_ = &lanes_[lane];
-        std::memcpy(pin_ + i, tokens.data() + i, B * 4);
-        check(hipMemcpyAsync(d_prompt_ + i, pin_ + i, B * 4, hipMemcpyHostToDevice, ln_->st), "token upload");
-        batch_step(d_prompt_ + i, B, last, lanes > 1 ? prev : -1);
-        prof_flush();
-        prev = lane;
-        pos_ += B;
-        kv_hi_ = std::max(kv_hi_, pos_);
-        if (last) check(hipMemcpyAsync(logits_.data(), logits_d_, c_.vocab * 4, hipMemcpyDeviceToHost, ln_->st),
-                        "logits copy");
+        ln_ = &lanes_[0];
+        if (!quiet) check(first, "sync");
+    };
+    try {
+        for (std::size_t i = 0; i < tokens.size(); i += batch_size, ++chunk) {
+            const std::size_t B = std::min(batch_size, tokens.size() - i);
+            const char* err = nullptr;
+            if (pos_ + B > c_.n_ctx) err = "context exhausted";
+            for (std::size_t b = 0; b < B && !err; ++b)
+                if (tokens[i + b] < 0 || static_cast<std::size_t>(tokens[i + b]) >= c_.vocab)
+                    err = "token id out of range";
+            if (err) throw std::runtime_error(err);  // the chunks before this one complete (drained below)
+            const bool last = compute_logits_last && i + B == tokens.size();
+            const int lane = static_cast<int>(chunk % lanes);
+            ln_ = &lanes_[lane];
+            std::memcpy(pin_ + i, tokens.data() + i, B * 4);
+            check(hipMemcpyAsync(d_prompt_ + i, pin_ + i, B * 4, hipMemcpyHostToDevice, ln_->st), "token upload");
+            batch_step(d_prompt_ + i, B, last, lanes > 1 ? prev : -1);
+            prof_flush();
+            prev = lane;
+            pos_ += B;
+            kv_hi_ = std::max(kv_hi_, pos_);
+            if (last)
+                check(hipMemcpyAsync(logits_.data(), logits_d_, c_.vocab * 4, hipMemcpyDeviceToHost, ln_->st),
+                      "logits copy");
+        }
+    } catch (...) {
+        drain(true);  // secondary errors ignored: the first one is what the caller sees
+        throw;
     }
-    drain();
+    drain(false);
     return logits_;
 }
 
@@ -644,7 +656,12 @@ std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
         // every step
         hipGraph_t g{};
         check(hipStreamBeginCapture(ln_->st, hipStreamCaptureModeThreadLocal), "begin capture");
-        decode_step(d_tok_, true, true);
+        try {
+            decode_step(d_tok_, true, true);
+        } catch (...) {  // leave the stream out of capture mode for the calls that follow
+            if (hipStreamEndCapture(ln_->st, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+            throw;
+        }
         check(hipStreamEndCapture(ln_->st, &g), "end capture");
         check(hipGraphInstantiate(&graph_, g, nullptr, nullptr, 0), "graph instantiate");
         (void)hipGraphDestroy(g);

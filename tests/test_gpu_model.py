@@ -153,19 +153,27 @@ def test_whole_prompt_batch_equals_chunks_of_32(tmp_path, mode):
     assert (kb_a, ids_a) == (kb_b, ids_b)
 
 
-def test_pipelined_prefill_error_completes_earlier_chunks(tiny):
-    """A bad token id in the third chunk: the two chunks before it complete (as
-    in a chunk-by-chunk run), the position stops after them, and decoding from
-    there equals decoding after a prefill of just those two chunks."""
+@pytest.mark.parametrize("kind", ["token", "context"])
+def test_pipelined_prefill_error_completes_earlier_chunks(tiny, kind):
+    """An error raised in the third chunk while the first two still run on
+    their streams (a bad token id, or the context running out): the call
+    drains every stream before it raises, the two chunks before it complete
+    (as in a chunk-by-chunk run), the position stops after them, and decoding
+    from there on lane 0 equals decoding after a prefill of just those two
+    chunks."""
     prompt = synth.prompt_tokens(4, 96)
     bad = prompt.copy()
-    bad[70] = 32000
-    m = capi.Model(tiny, ctx=256, max_batch=32)
-    with pytest.raises(capi.MvhError, match="token id out of range"):
+    ctx = 256
+    if kind == "token":
+        bad[70] = 32000
+    else:
+        ctx = 80  # chunk 3 (positions 64..95) does not fit
+    m = capi.Model(tiny, ctx=ctx, max_batch=32)
+    with pytest.raises(capi.MvhError, match="token id out of range" if kind == "token" else "context exhausted"):
         m.prefill(bad, 32)
     assert m.position == 64
     got = m.forward(5)
-    ref = capi.Model(tiny, ctx=256, max_batch=32)
+    ref = capi.Model(tiny, ctx=ctx, max_batch=32)
     ref.prefill(prompt[:64], 32, logits=False)
     want = ref.forward(5)
     assert (bits(got) == bits(want)).all()
