@@ -11,7 +11,10 @@
  * Q8_0 34-byte, Q6_K 210-byte blocks; GGML order ne0 = cols, ne1 = rows) and
  * are never repacked.  Activation/result pointers are host memory
  * (MVH_HOST: the call stages, launches and synchronises) or device memory
- * (MVH_DEVICE: the call only enqueues on the context's stream).
+ * (MVH_DEVICE: the call only enqueues on the context's stream).  Device fp32
+ * activation inputs (the x of the matvec / matmul / quantize entry points)
+ * must be 16-byte aligned: the kernels read them as 16-byte vectors, and a
+ * misaligned pointer fails with MVH_E_INVALID.
  *
  * Reference interfaces replaced (MemVanta file:line):
  *   mvh_matvec            tensor_matvec            include/memvanta/gguf_kernels.hpp:26,

@@ -148,6 +148,14 @@ int stage_in(mvh_context* c, mvh_context::Buf& b, const void* src, size_t bytes,
     return MVH_OK;
 }
 
+// fp32 activations: the kernels read them as 16-byte vectors, so a device
+// pointer must be 16-byte aligned (host buffers are staged into aligned ones)
+int stage_in_act(mvh_context* c, mvh_context::Buf& b, const float* x, size_t bytes, int kind, const void** out) {
+    if (kind == MVH_DEVICE && (reinterpret_cast<uintptr_t>(x) & 15))
+        return fail(MVH_E_INVALID, "device activations must be 16-byte aligned");
+    return stage_in(c, b, x, bytes, kind, out);
+}
+
 int finish_out(mvh_context* c, void* host_dst, const void* dev_src, size_t bytes, int kind) {
     if (kind == MVH_DEVICE) return MVH_OK;
     MVH_HIP(hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost, c->stream));
@@ -445,7 +453,7 @@ int mvh_quantize_q8(mvh_context* c, const float* x, size_t batch, size_t cols, i
     if (!batch || !cols) return MVH_OK;
     if (!x || !q || !d) return fail(MVH_E_INVALID, "null argument");
     const void* xd = nullptr;
-    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
+    if (int rc = stage_in_act(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
     ActView a;
     if (int rc = act_buffers(c, batch, cols, &a)) return rc;
     int8_t* qd = kind == MVH_DEVICE ? q : a.q;
@@ -472,7 +480,7 @@ int mvh_matvec(mvh_context* c, const mvh_tensor* w, const float* x, float* y, in
     const size_t cols = w->ne0, rows = w->ne1;
     if (!rows) return prof_empty(w, 1);
     const void* xd = nullptr;
-    if (int rc = stage_in(c, c->xin, x, cols * 4, kind, &xd)) return rc;
+    if (int rc = stage_in_act(c, c->xin, x, cols * 4, kind, &xd)) return rc;
     float* yd = y;
     if (kind == MVH_HOST) {
         if (int rc = grow(c, c->yout, rows * 4)) return rc;
@@ -549,7 +557,7 @@ int mvh_matmul_batch(mvh_context* c, const mvh_tensor* w, const float* x, float*
     if (!batch || !rows) return prof_empty(w, batch);
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
     const void* xd = nullptr;
-    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
+    if (int rc = stage_in_act(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
     float* yd = y;
     if (kind == MVH_HOST) {
         if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;
@@ -607,7 +615,7 @@ int mvh_matmul_batch_v06(mvh_context* c, const mvh_tensor* w, const float* x, fl
     if (!rows) return prof_empty(w, batch);
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
     const void* xv = nullptr;
-    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xv)) return rc;
+    if (int rc = stage_in_act(c, c->xin, x, batch * cols * 4, kind, &xv)) return rc;
     const auto* xd = static_cast<const float*>(xv);
     float* yd = y;
     if (kind == MVH_HOST) {
@@ -633,6 +641,7 @@ int mvh_matmul_batch_v06_noalloc(mvh_context* c, const mvh_tensor* w, const floa
     const size_t cols = w->ne0, rows = w->ne1;
     if (!batch || !rows) return MVH_OK;
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
+    if (reinterpret_cast<uintptr_t>(x) & 15) return fail(MVH_E_INVALID, "device activations must be 16-byte aligned");
     // fallback conditions of src/gguf_kernels.cpp:263: tensor_matmul_batch's per-(token, row) dots
     if (batch < 2 || (w->type != MVH_TYPE_Q4_0 && w->type != MVH_TYPE_Q8_0) || cols % 32)
         return fp32_rows(c, w, x, y, batch, "batch matrix");
@@ -735,7 +744,7 @@ static int quantize_native(mvh_context* c, uint32_t type, const float* x, size_t
     if (!x || !blocks) return fail(MVH_E_INVALID, "null argument");
     const size_t out_bytes = n / 32 * (q4 ? 20 : 36);
     const void* xd = nullptr;
-    if (int rc = stage_in(c, c->xin, x, n * 4, kind, &xd)) return rc;
+    if (int rc = stage_in_act(c, c->xin, x, n * 4, kind, &xd)) return rc;
     void* od = blocks;
     if (kind == MVH_HOST) {
         if (int rc = grow(c, c->yout, out_bytes)) return rc;
@@ -793,7 +802,7 @@ static int native_f32act(mvh_context* c, const mvh_tensor* w, uint32_t type, con
     if (!rows || !batch) return MVH_OK;
     if (!x || !y) return fail(MVH_E_INVALID, "null x/y");
     const void* xd = nullptr;
-    if (int rc = stage_in(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
+    if (int rc = stage_in_act(c, c->xin, x, batch * cols * 4, kind, &xd)) return rc;
     float* yd = y;
     if (kind == MVH_HOST) {
         if (int rc = grow(c, c->yout, batch * rows * 4)) return rc;

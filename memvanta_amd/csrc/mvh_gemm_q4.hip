@@ -386,19 +386,15 @@ hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const fl
     // From 256 tokens the workgroup kernel (64 rows x 32 tokens per workgroup)
     // is a few percent faster (M = 512: 68-69 against 70-71 us at 4096^2,
     // 160 against 165-172 us at the other two shapes); at M = 128 it is slower.
-    // Tuning override: MVH_GEMM_WG=0 never, 1 always (16-token tiles at M <= 32).
+    // Tuning override: MVH_GEMM_WG=0 never, 1 at every batch size.
     static const int wg_mode = [] {
         const char* e = getenv("MVH_GEMM_WG");
         return e ? atoi(e) : -1;
     }();
     const size_t gw = (rows + 63) / 64;
     if (wg_mode == 1 || (wg_mode != 0 && batch >= 256)) {
-        if (wg_mode == 1 && batch <= 32)
-            gemm_q4_0_q8_mfma_wg_kernel<1><<<dim3(static_cast<unsigned>(gw), static_cast<unsigned>(g16)), 256, 0, st>>>(
-                W, aq, ad, y, N, nb, Bn);
-        else
-            gemm_q4_0_q8_mfma_wg_kernel<2><<<dim3(static_cast<unsigned>(gw), static_cast<unsigned>(g32)), 256, 0, st>>>(
-                W, aq, ad, y, N, nb, Bn);
+        gemm_q4_0_q8_mfma_wg_kernel<2><<<dim3(static_cast<unsigned>(gw), static_cast<unsigned>(g32)), 256, 0, st>>>(
+            W, aq, ad, y, N, nb, Bn);
         return hipGetLastError();
     }
     if ((batch <= 32 && gx < tg2_min) || gx * g32 <= 1024) {

@@ -87,10 +87,18 @@ __global__ __launch_bounds__(64 * kRowWaves) void q4q8_native_rows_kernel(const 
             }
             s_pair[w][lane] = make_float2(static_cast<float>(s) * __uint_as_float(wb[0]), __uint_as_float(ab[0]));
         }
+        // the wave's LDS slots: every lane's store visible to lane 0 before it
+        // reads them, and lane 0's reads done before the next chunk's stores
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (lane == 0) {
             const int n = min(64, nb - b0);
             for (int j = 0; j < n; ++j) sum = fmaf(s_pair[w][j].x, s_pair[w][j].y, sum);
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     if (lane == 0) y[row] = sum;
 }

@@ -538,3 +538,45 @@ def test_gemv_f16(ctx, oracle, k, n):
     wb = oracle.matmul_batch(w, synth.F16, n, k, xb)
     assert ulp_diff(gb, wb).max() <= 2
     t.free()
+
+
+_WG_CHILD = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from memvanta_amd import capi, synth
+from oracle.pyoracle import Oracle
+o, ctx = Oracle(), capi.Context(0)
+for batch, k, n in [(3, 512, 17), (33, 256, 100), (40, 4096, 70), (300, 4096, 1000)]:
+    rng = np.random.default_rng(batch + k + n)
+    w = synth.quantize(synth.Q4_0, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    t = ctx.upload("blk.0.ffn_gate.weight", synth.Q4_0, k, n, w)
+    x = synth.activations(rng, batch, k)
+    got = ctx.matmul_batch_v06(t, x, capi.MVH_ACT_Q8)
+    want = o.matmul_batch_v06(w, synth.Q4_0, n, k, x, is_ffn=True, force_q8=True)
+    bad = int((got.view(np.uint32) != want.view(np.uint32)).sum())
+    print(f"M={batch} K={k} N={n} differing={bad}", flush=True)
+    assert bad == 0
+    t.free()
+ctx.close()
+print("ok", flush=True)
+"""
+
+
+@pytest.mark.parametrize("wg", ["1", "0"])
+def test_prefill_gemm_kernel_override_bitexact(wg):
+    """MVH_GEMM_WG (read once per process) forces the workgroup int8-MFMA GEMM
+    at every batch size (1) or never (0): both selections against the
+    FORCE_Q8 reference chain in a child process that sets it before any GPU
+    call -- small and ragged token counts on the workgroup kernel, 300 tokens
+    on the wave-private kernel."""
+    import os
+    import subprocess
+    import sys
+
+    from conftest import ROOT
+
+    env = dict(os.environ, MVH_GEMM_WG=wg)
+    p = subprocess.run([sys.executable, "-u", "-c", _WG_CHILD, ROOT], env=env, capture_output=True, text=True,
+                       timeout=110)
+    assert p.returncode == 0 and p.stdout.strip().endswith("ok"), p.stdout + p.stderr

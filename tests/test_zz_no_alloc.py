@@ -78,3 +78,40 @@ def test_noalloc_rejects_batches_beyond_the_scratch(ctx):
     ctx.synchronize()
     assert bool((y == 7.0).all())
     t.free()
+
+
+@pytest.mark.parametrize("mode,b", [(capi.MVH_ACT_Q8, 40), (capi.MVH_ACT_REF, 40), (capi.MVH_ACT_REF, 37)])
+def test_noalloc_under_graph_capture(ctx, mode, b):
+    """The entry point captured into a HIP graph on the context's stream (the
+    callers it exists for) and replayed three times, with an eager call of a
+    different input between the replays (it overwrites the static scratch):
+    every replay equals the eager result bit for bit.  40 tokens in default
+    numerics are five 8-token groups; 37 leaves a 5-token tail of per-token dots."""
+    import torch
+
+    rng = np.random.default_rng(77 + b + mode)
+    t, x = _case(ctx, rng, synth.Q4_0, 4096, 512, b)
+    _, x_other = _case(ctx, rng, synth.Q4_0, 4096, 8, 2 * b)
+    y_other = torch.empty((2 * b, 512), dtype=torch.float32, device="cuda:0")
+    want = torch.full((b, 512), float("nan"), dtype=torch.float32, device="cuda:0")
+    y = torch.full_like(want, float("nan"))
+    torch.cuda.synchronize()
+    ctx.matmul_batch_v06_noalloc(t, x, want, mode)
+    ctx.synchronize()
+    want = want.cpu().numpy()
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        ctx.matmul_batch_v06_noalloc(t, x, y, mode)
+    ctx.synchronize()
+    for r in range(3):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            g.replay()
+        ctx.synchronize()
+        assert_bitexact(y.cpu().numpy(), want, f"replay {r}")
+        ctx.matmul_batch_v06_noalloc(t, x_other, y_other, mode)  # eager work between the replays
+        ctx.synchronize()
+    del g
+    t.free()
