@@ -378,6 +378,43 @@ def normal_quantized_torch(ty: int, rows: int, cols: int, gen, std: float = 0.02
     return produce
 
 
+def random_blocks(ty: int, rows: int, cols: int, rng: np.random.Generator, chunk_rows: int = 4096):
+    """Producer of valid blocks drawn directly as bytes (no float weights to
+    quantize, so a 7B-shape model takes seconds on any host and the bytes are
+    the same on every machine): uniform random quant codes with scales of the
+    magnitude N(0, 0.02) weights quantize to --
+    Q4_0: d = +-U(0.004, 0.009), nibbles uniform;
+    Q8_0: d = U(3e-4, 7e-4), int8 codes uniform in [-127, 127];
+    Q6_K: d = U(2.5e-5, 5e-5) (fp16 subnormals), 6-bit codes uniform, int8
+    sub-block scales uniform in [-64, 63]."""
+    if ty not in (Q4_0, Q8_0, Q6_K):
+        raise ValueError(f"random blocks: unsupported type {TYPE_NAMES.get(ty, ty)}")
+    _, bs = BLOCK[ty]
+
+    def f16(v):
+        return v.astype(np.float16).view(np.uint8).reshape(-1, 2)
+
+    def produce():
+        for r0 in range(0, rows, chunk_rows):
+            n = min(chunk_rows, rows - r0)
+            raw = rng.integers(0, 256, n * row_bytes(ty, cols), dtype=np.uint8)
+            b = raw.reshape(-1, bs)
+            nb = b.shape[0]
+            if ty == Q4_0:
+                sign = np.where(rng.integers(0, 256, nb, dtype=np.uint8) & 1, -1.0, 1.0)
+                b[:, 0:2] = f16(rng.uniform(0.004, 0.009, nb) * sign)
+            elif ty == Q8_0:
+                b[:, 0:2] = f16(rng.uniform(3e-4, 7e-4, nb))
+                q = b[:, 2:].view(np.int8)
+                np.maximum(q, -127, out=q)
+            else:
+                b[:, 192:208] = rng.integers(-64, 64, (nb, 16), dtype=np.int8).view(np.uint8)
+                b[:, 208:210] = f16(rng.uniform(2.5e-5, 5e-5, nb))
+            yield raw.tobytes()
+
+    return produce
+
+
 # --------------------------------------------------------------------------
 # model + matrix configurations
 # --------------------------------------------------------------------------
@@ -412,14 +449,18 @@ CONFIGS = {c.name: c for c in (TINY, TINYLLAMA_MIXED, LLAMA7B, TINYLLAMA_MIXED_2
 
 
 def write_model(cfg: ModelConfig, path: str, seed: int = 1234, std: float = 0.02, device: str | None = None,
-                digest: bool = True) -> str | None:
+                digest: bool = True, blocks: str = "normal") -> str | None:
     """Random-init llama GGUF; returns the sha256 of the file (None when
     digest=False).  With `device` (e.g. "cuda"), weights are drawn and
     quantized there by torch: seconds for a 7B shape instead of minutes, but a
-    different random stream from the default numpy one."""
+    different random stream from the default numpy one.  blocks="random":
+    every matrix from random_blocks (seconds on the host, the same bytes
+    everywhere; `device` and `std` are then unused)."""
+    if blocks not in ("normal", "random"):
+        raise ValueError(f"blocks must be 'normal' or 'random', got {blocks!r}")
     rng = np.random.default_rng(seed)
     gen = None
-    if device is not None:
+    if device is not None and blocks == "normal":
         import torch
 
         gen = torch.Generator(device=device)
@@ -441,8 +482,12 @@ def write_model(cfg: ModelConfig, path: str, seed: int = 1234, std: float = 0.02
     D, F, kv = cfg.dim, cfg.ffn, cfg.kv_heads * cfg.head_dim
 
     def mat(name, rows, cols, ty):
-        prod = (normal_quantized(ty, rows, cols, rng, std) if gen is None
-                else normal_quantized_torch(ty, rows, cols, gen, std))
+        if blocks == "random":
+            prod = random_blocks(ty, rows, cols, rng)
+        elif gen is None:
+            prod = normal_quantized(ty, rows, cols, rng, std)
+        else:
+            prod = normal_quantized_torch(ty, rows, cols, gen, std)
         w.add_tensor(name, (cols, rows), ty, rows * row_bytes(ty, cols), prod)
 
     def ones(name, n):

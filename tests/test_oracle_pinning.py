@@ -504,6 +504,12 @@ MUTATIONS = {
                             "size_t kb = (h % n_head_kv) * hd, qb = h * hd;"),
     "gqa_head_map_prefill": ("kb = (h / group) * hd, qb = h * hd, upto = start + b;",
                              "kb = (h % m->n_head_kv) * hd, qb = h * hd, upto = start + b;"),
+    # the score scale: a division by sqrtf(hd), not a product with its reciprocal
+    # (src/llama_model.cpp:248,256), in the decode and in the prefill attention
+    "attn_scale_reciprocal_decode": ("float sf = mvo_kv_dot_key(kv, t, kb, q + qb, hd) / sq;",
+                                     "float sf = mvo_kv_dot_key(kv, t, kb, q + qb, hd) * (1.0f / sq);"),
+    "attn_scale_reciprocal_prefill": ("float sf = mvo_kv_dot_key(m->kv[li], t, kb, Q + b * D + qb, hd) / sq;",
+                                      "float sf = mvo_kv_dot_key(m->kv[li], t, kb, Q + b * D + qb, hd) * (1.0f / sq);"),
     # native blocks: the weight scale must multiply isum before the fused add of x.d
     "nq_q4q8_unfused": ("        sum = fmaf(p, nq_d(xb), sum);", "        sum = sum + p * nq_d(xb);"),
     "nq_q4q8_scale_order": ("float p = (float)isum * nq_d(wa);\n        sum = fmaf(p, nq_d(xb), sum);",
@@ -552,8 +558,18 @@ def _golden_ok(o, mats, tiny_model, gqa_model):
         assert np.array_equal(o.fp32_to_fp16(f16["bits"].view(np.float32)), f16["half"])
         gm = golden("model_tiny.npz")
         m = o.model(tiny_model, ctx=256)
-        assert_bitexact(m.prefill(gm["prompt"], 32), gm["prefill_logits_m0"])
-        m.close()
+        try:
+            assert_bitexact(m.prefill(gm["prompt"], 32), gm["prefill_logits_m0"])
+            # the decode sites too (head_dim 48: sqrtf(48) is not a power of two, unlike the GQA model's 64)
+            ids, cur = [], 17
+            for _ in range(12):
+                lg = m.forward(cur)
+                cur = int(np.argmax(lg))
+                ids.append(cur)
+            assert ids == gm["decode_ids_m0"].tolist()
+            assert_bitexact(lg, gm["decode_last_logits_m0"])
+        finally:
+            m.close()
         for tname in KV_TYPES:
             _kv_types_check(o, tname)
         _gqa_check(o, gqa_model, "f16", 0)

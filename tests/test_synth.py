@@ -37,3 +37,48 @@ def test_write_model_device_path(tmp_path):
     sha1 = synth.write_model(cfg, p, seed=3, device="cpu")
     sha2 = synth.write_model(cfg, p, seed=3, device="cpu")
     assert sha1 == sha2
+
+
+@pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0, synth.Q6_K])
+def test_random_blocks_are_valid_and_reproducible(ty):
+    """blocks="random" models: every scale a finite fp16 in its stated range,
+    Q8_0 codes in [-127, 127], Q6_K sub-block scales in [-64, 63]; the same
+    seed gives the same bytes, and the dequantized weights have the spread of
+    N(0, 0.02) weights (std within a factor 2)."""
+    rows, cols = 33, 512
+    a = b"".join(synth.random_blocks(ty, rows, cols, np.random.default_rng(9), chunk_rows=8)())
+    b = b"".join(synth.random_blocks(ty, rows, cols, np.random.default_rng(9), chunk_rows=8)())
+    assert a == b and len(a) == rows * synth.row_bytes(ty, cols)
+    raw = np.frombuffer(a, np.uint8)
+    qk, bs = synth.BLOCK[ty]
+    blk = raw.reshape(-1, bs)
+    if ty == synth.Q6_K:
+        d = blk[:, 208:210].copy().view(np.float16).astype(np.float64).ravel()
+        sc = blk[:, 192:208].view(np.int8)
+        assert sc.min() >= -64 and sc.max() <= 63
+        assert (d >= 2.4e-5).all() and (d <= 5.1e-5).all()
+    else:
+        d = blk[:, 0:2].copy().view(np.float16).astype(np.float64).ravel()
+        if ty == synth.Q8_0:
+            assert blk[:, 2:].view(np.int8).min() >= -127
+            assert (d >= 2.9e-4).all() and (d <= 7.1e-4).all()
+        else:
+            assert (np.abs(d) >= 0.0039).all() and (np.abs(d) <= 0.0091).all()
+            assert (d < 0).any() and (d > 0).any()
+    w = synth.dequantize(ty, raw.reshape(rows, -1), rows, cols)
+    assert np.isfinite(w).all() and 0.01 <= float(w.std()) <= 0.04
+
+
+def test_random_block_model_runs_on_the_oracle(tmp_path, oracle):
+    """A blocks="random" model is a valid GGUF for the host restatement: a
+    short prefill and decode give finite logits, and a second write of the
+    same seed is byte-identical."""
+    cfg = synth.dataclasses.replace(synth.TINYLLAMA_MIXED_2L, name="tl-random")
+    p = str(tmp_path / "r.gguf")
+    sha = synth.write_model(cfg, p, seed=4, blocks="random")
+    assert synth.write_model(cfg, str(tmp_path / "r2.gguf"), seed=4, blocks="random") == sha
+    m = oracle.model(p, ctx=64, threads=4)
+    lg = m.prefill(synth.prompt_tokens(1, 9), 32)
+    assert np.isfinite(lg).all() and lg.std() > 0
+    assert np.isfinite(m.forward(int(np.argmax(lg)))).all()
+    m.close()
