@@ -514,6 +514,287 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     }
 }
 
+// ---- fused decode attention, K and V staged through LDS ----------------------
+//
+// The same step as attn_decode_fused_kernel (RoPE of q and k at position
+// p = *d_pos, the F16 K/V row of p written through fp32_to_fp16, scores
+// dot_key / sqrtf(hd), mx, e = expf(s - mx), den in double, a_t = e_t *
+// float(1/den), out[d] = fma(a_t, V_t[d], out[d]) for t = 0..p in order, Q8
+// of each 32-element block of the output), arranged so that every K and V
+// byte crosses the memory system once per workgroup in full 16-byte pieces of
+// whole rows:
+//  * workgroup (head h, slice s of NS) owns output elements [s*SW, (s+1)*SW),
+//    SW = HD / NS; the NS slices of a head run on one XCD (consecutive
+//    blockIdx modulo the eight XCDs), so their K rows come from one L2;
+//  * K rows are staged in rounds of kHR rows: thread t loads 16-byte pieces
+//    t, t + 256, ... of the round (CPR = HD/8 pieces per row, so a wave's
+//    load covers whole rows), stores them to an LDS tile of pitch
+//    2*HD + 16 bytes, and after one barrier computes the score of row t of
+//    the round from the tile with the reference's eight-lane fma order;
+//  * V rows of the slice are staged the same way into a second tile, and the
+//    value chain runs in wave 0, lane l owning DPL = SW/64 (or 1) output
+//    elements, one ds_read per row;
+//  * round 0 of K and of V (rows 0..kHR-1, whatever the position: rows past
+//    it are read and ignored) is issued with q/k/v and the RoPE row, so the
+//    kernel has one memory round trip below kHR positions; the row of the
+//    position itself is taken from the RoPE'd k and v (the cache row is
+//    written by this launch), the staged copy of that row skipped.
+constexpr int kHT = 256;        // threads
+constexpr int kHR = 256;        // rows per staging round
+constexpr int kHMaxCtx = 2048;  // positions the LDS score array holds
+
+template <int HD, int NS>
+struct HeadCfg {
+    static constexpr int SW = HD / NS;                   // output elements per workgroup
+    static constexpr int CPR = HD / 8;                   // 16-byte K pieces per row
+    static constexpr int KPT = kHR * CPR / kHT;          // K pieces per thread per round
+    static constexpr int CV = SW / 8;                    // 16-byte V pieces per row of the slice
+    static constexpr int VPT = (kHR * CV + kHT - 1) / kHT;
+    static constexpr int KP = 2 * HD + 16;               // K tile pitch (bytes)
+    static constexpr int VP = 2 * SW + 16;               // V tile pitch (bytes)
+    static constexpr int DPL = SW >= 128 ? SW / 64 : 1;  // output elements per chain lane
+    static constexpr int LANES = SW / DPL;               // chain lanes (<= 64: wave 0)
+    static_assert(kHR * CPR % kHT == 0 && LANES <= 64 && DPL <= 2, "head attention shape");
+};
+
+template <int HD, int NS>
+__global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ rope, const int* __restrict__ d_pos, uint16_t* kbase, uint16_t* vbase,
+    int page_tokens, size_t page_stride, int rows_alloc, float* __restrict__ out, int8_t* __restrict__ q8,
+    float* __restrict__ q8d, int group, int kv_dim) {
+    using C = HeadCfg<HD, NS>;
+    constexpr int SW = C::SW, CPR = C::CPR, KPT = C::KPT, CV = C::CV, VPT = C::VPT, KP = C::KP, VP = C::VP,
+                  DPL = C::DPL, half = HD / 2;
+    __shared__ __align__(16) uint8_t s_kt[kHR * KP];
+    __shared__ __align__(16) uint8_t s_vt[kHR * VP];
+    __shared__ __align__(16) float s_q[HD];
+    __shared__ __align__(16) float s_a[kHMaxCtx];
+    __shared__ float red_f[kHT / 64];
+    __shared__ double red_d[kHT / 64];
+    __shared__ uint64_t s_tab[32];
+
+    // blockIdx -> (head, slice): the slices of a head on one XCD
+    const int G = gridDim.x, b = blockIdx.x;
+    const int hs = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
+    const int h = hs / NS, slice = hs - h * NS;
+    const int kh = h / group, t = threadIdx.x, dbase = slice * SW;
+    auto row_off = [&](int tt) {
+        return static_cast<size_t>(tt / page_tokens) * page_stride + static_cast<size_t>(tt % page_tokens) * kv_dim +
+               kh * HD;
+    };
+
+    // the one round trip: position, q/k/v, the RoPE row, K and V round 0
+    const int pos = *d_pos;
+    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    const int th = t < half ? t : 0;
+    const float* qh = q + static_cast<size_t>(h) * HD;
+    const float* kk = k + static_cast<size_t>(kh) * HD;
+    const float* vv = v + static_cast<size_t>(kh) * HD;
+    const float q0 = qh[th], q1 = qh[th + half], k0 = kk[th], k1 = kk[th + half], v0 = vv[th], v1 = vv[th + half];
+    const float cs = rope[th];
+    const float sn = rope[half + th];
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 kr[KPT], vr[VPT];
+    auto load_k = [&](int r0) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int pc = i * kHT + t, row = min(r0 + pc / CPR, rows_alloc - 1);
+            kr[i] = ld_global16(kbase + row_off(row) + (pc % CPR) * 8);
+        }
+    };
+    auto load_v = [&](int r0) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pc = min(i * kHT + t, kHR * CV - 1), row = min(r0 + pc / CV, rows_alloc - 1);
+            vr[i] = ld_global16(vbase + row_off(row) + dbase + (pc % CV) * 8);
+        }
+    };
+    load_k(0);
+    load_v(0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // RoPE (every thread computes it so the loads are used outside a branch)
+    const float rq0 = fmaf(q0, cs, -(q1 * sn)), rq1 = fmaf(q0, sn, q1 * cs);
+    const uint16_t hk0 = f2h_ref(fmaf(k0, cs, -(k1 * sn))), hk1 = f2h_ref(fmaf(k0, sn, k1 * cs));
+    const uint16_t hv0 = f2h_ref(v0), hv1 = f2h_ref(v1);
+    if (t < half) {
+        s_q[t] = rq0;
+        s_q[t + half] = rq1;
+        if (slice == 0 && h % group == 0) {  // one writer of the cache row per kv head
+            uint16_t* kc = kbase + row_off(pos);
+            uint16_t* vc = vbase + row_off(pos);
+            kc[t] = hk0;
+            kc[t + half] = hk1;
+            vc[t] = hv0;
+            vc[t + half] = hv1;
+        }
+    }
+    // stores of the staged registers, the position's row replaced by the RoPE'd values
+    auto store_k = [&](int r0) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int pc = i * kHT + t, row = pc / CPR;
+            if (r0 + row != pos) *reinterpret_cast<uint4*>(s_kt + row * KP + (pc % CPR) * 16) = kr[i];
+        }
+        if (pos >= r0 && pos < r0 + kHR && t < half) {
+            uint16_t* kt = reinterpret_cast<uint16_t*>(s_kt + (pos - r0) * KP);
+            kt[t] = hk0;
+            kt[t + half] = hk1;
+        }
+    };
+    auto store_v = [&](int r0) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pc = i * kHT + t, row = pc / CV;
+            if (pc < kHR * CV && r0 + row != pos)
+                *reinterpret_cast<uint4*>(s_vt + row * VP + (pc % CV) * 16) = vr[i];
+        }
+        if (pos >= r0 && pos < r0 + kHR && t < half) {  // the slice's elements of the position's v
+            uint16_t* vt = reinterpret_cast<uint16_t*>(s_vt + (pos - r0) * VP);
+            if (t >= dbase && t < dbase + SW) vt[t - dbase] = hv0;
+            if (t + half >= dbase && t + half < dbase + SW) vt[t + half - dbase] = hv1;
+        }
+    };
+
+    // scores, round by round; the next round's K loads in flight meanwhile
+    const float scale = sqrt_rn(static_cast<float>(HD));
+    float mx = -INFINITY;
+    for (int r0 = 0; r0 <= pos; r0 += kHR) {
+        if (r0) __syncthreads();  // the previous round's tile reads are done
+        store_k(r0);
+        if (r0 == 0) store_v(0);
+        if (r0 + kHR <= pos) load_k(r0 + kHR);
+        __syncthreads();
+        const int tt = r0 + t;
+        if (tt <= pos) {
+            float acc[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+            const uint8_t* kt = s_kt + t * KP;
+#pragma unroll
+            for (int c = 0; c < CPR; ++c) {
+                const half8 hk = as_half8(*reinterpret_cast<const uint4*>(kt + 16 * c));
+                const float4 qa = *reinterpret_cast<const float4*>(s_q + 8 * c);
+                const float4 qb = *reinterpret_cast<const float4*>(s_q + 8 * c + 4);
+                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] = fmaf(qv[e], static_cast<float>(hk[e]), acc[e]);
+            }
+            float sum = acc[0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) sum = sum + acc[e];
+            const float sc = __fdiv_rn(sum, scale);
+            s_a[tt] = sc;
+            mx = fmaxf(mx, sc);
+        }
+    }
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red_f[t >> 6] = mx;
+    __syncthreads();
+    mx = red_f[0];
+#pragma unroll
+    for (int w = 1; w < kHT / 64; ++w) mx = fmaxf(mx, red_f[w]);
+
+    // softmax weights
+    double den = 0.0;
+    for (int tt = t; tt <= pos; tt += kHT) {
+        const float e = mvh_expf_tabbed(s_a[tt] - mx, s_tab);
+        s_a[tt] = e;
+        den += static_cast<double>(e);
+    }
+    den = wave_sum(den);
+    if ((t & 63) == 0) red_d[t >> 6] = den;
+    __syncthreads();
+    den = red_d[0];
+#pragma unroll
+    for (int w = 1; w < kHT / 64; ++w) den += red_d[w];
+    const float inv = static_cast<float>(1.0 / den);
+    for (int tt = t; tt <= pos; tt += kHT) s_a[tt] = s_a[tt] * inv;
+
+    // value chain over t = 0..pos in order, round by round
+    float acc[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
+    const int lane = t;  // wave 0
+    for (int r0 = 0; r0 <= pos; r0 += kHR) {
+        if (r0) {
+            __syncthreads();  // the previous round's chain is done
+            store_v(r0);
+        }
+        if (r0 + kHR <= pos) load_v(r0 + kHR);
+        __syncthreads();  // the tile (and, in round 0, the weights) written
+        if (t < C::LANES) {
+            const int rows = min(kHR, pos + 1 - r0);
+            const uint8_t* vl = s_vt + lane * DPL * 2;
+            const float* al = s_a + r0;
+            // 8-row steps with two register sets used in turn; every read is
+            // unconditional (a step past the last one re-reads the last), so
+            // the wait counts cover only the set being summed
+            const int nsteps = rows >> 3;
+            auto ld = [&](int st, uint32_t (&vw)[8], float4 (&a)[2]) {
+                const int j0 = min(st, max(nsteps - 1, 0)) << 3;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if constexpr (DPL == 2)
+                        vw[j] = *reinterpret_cast<const uint32_t*>(vl + (j0 + j) * VP);
+                    else
+                        vw[j] = *reinterpret_cast<const uint16_t*>(vl + (j0 + j) * VP);
+                }
+                a[0] = *reinterpret_cast<const float4*>(al + j0);
+                a[1] = *reinterpret_cast<const float4*>(al + j0 + 4);
+            };
+            auto step = [&](const uint32_t (&vw)[8], const float4 (&a)[2]) {
+                const float av[8] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    acc[0] = fmaf(av[j], h2f(vw[j] & 0xffffu), acc[0]);
+                    if constexpr (DPL == 2) acc[1] = fmaf(av[j], h2f(vw[j] >> 16), acc[1]);
+                }
+            };
+            if (nsteps > 0) {
+                uint32_t va[8], vb[8];
+                float4 aa[2], ab[2];
+                ld(0, va, aa);
+                for (int st = 0; st < nsteps; st += 2) {
+                    ld(st + 1, vb, ab);
+                    __builtin_amdgcn_sched_barrier(0);
+                    step(va, aa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    ld(st + 2, va, aa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (st + 1 < nsteps) step(vb, ab);
+                }
+            }
+            for (int j = nsteps << 3; j < rows; ++j) {
+                const uint32_t w = DPL == 2 ? *reinterpret_cast<const uint32_t*>(vl + j * VP)
+                                            : *reinterpret_cast<const uint16_t*>(vl + j * VP);
+                acc[0] = fmaf(al[j], h2f(w & 0xffffu), acc[0]);
+                if constexpr (DPL == 2) acc[1] = fmaf(al[j], h2f(w >> 16), acc[1]);
+            }
+        }
+    }
+    if (t < C::LANES) {
+        const size_t o = static_cast<size_t>(h) * HD + dbase + lane * DPL;
+        if constexpr (DPL == 2) {
+            *reinterpret_cast<float2*>(out + o) = make_float2(acc[0], acc[1]);
+        } else {
+            out[o] = acc[0];
+        }
+        if (q8) {  // quantize_q8 of each 32-element block of the output (32 / DPL lanes)
+            constexpr int L = 32 / DPL;
+            float m = fabsf(acc[0]);
+            if constexpr (DPL == 2) m = fmaxf(m, fabsf(acc[1]));
+            m = group_max<L>(m);
+            const float d = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+            const float id = __fdiv_rn(1.0f, d);
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) q8[o + i] = static_cast<int8_t>(q_round_away(acc[i] * id, 127.0f));
+            if ((lane & (L - 1)) == 0) q8d[o / 32] = d;
+        }
+    }
+}
+
 // ---- prefill chunk attention: scores + softmax once, values shared ----------
 //
 // Scores and softmax weights of query token b (grid y) and head h (grid x)
@@ -865,6 +1146,28 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
                                     size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st) {
     if (!attn_decode_fused_ok(hd, max_ctx, page_tokens)) return hipErrorInvalidValue;
     const int rows_alloc = static_cast<int>((max_ctx + page_tokens - 1) / page_tokens * page_tokens);
+    // head dims 64 and 128 up to kHMaxCtx positions: the LDS-staged kernel,
+    // NS slices per head.  Tuning override MVH_ATTN_NS: 1, 2 or 4 slices, 0 =
+    // the register-staged kernel below.
+    static const int ns_env = [] {
+        const char* e = getenv("MVH_ATTN_NS");
+        return e ? atoi(e) : -1;
+    }();
+    const int ns = ns_env < 0 ? 2 : ns_env;
+    if ((hd == 128 || hd == 64) && max_ctx <= static_cast<size_t>(kHMaxCtx) && ns > 0) {
+        const int group = static_cast<int>(n_head / n_head_kv), kvd = static_cast<int>(n_head_kv * hd);
+#define MVH_ATTN_HEAD(HD_, NS_)                                                                                   \
+    attn_decode_head_kernel<HD_, NS_><<<dim3(static_cast<unsigned>(n_head * NS_)), kHT, 0, st>>>(                \
+        q, k, v, rope, d_pos, kbase, vbase, static_cast<int>(page_tokens), page_stride, rows_alloc, out, q8, q8d, \
+        group, kvd)
+        if (hd == 128 && ns == 1) MVH_ATTN_HEAD(128, 1);
+        else if (hd == 128 && ns == 4) MVH_ATTN_HEAD(128, 4);
+        else if (hd == 128) MVH_ATTN_HEAD(128, 2);
+        else if (ns == 1) MVH_ATTN_HEAD(64, 1);
+        else MVH_ATTN_HEAD(64, 2);
+#undef MVH_ATTN_HEAD
+        return hipGetLastError();
+    }
     const int sw = hd % 32 == 0 ? 32 : hd % 16 == 0 ? 16 : 8;
     const int nslice = static_cast<int>(hd) / sw;
     const int ctx_pad = static_cast<int>((max_ctx + 3) / 4 * 4);

@@ -381,11 +381,13 @@ def normal_quantized_torch(ty: int, rows: int, cols: int, gen, std: float = 0.02
 def random_blocks(ty: int, rows: int, cols: int, rng: np.random.Generator, chunk_rows: int = 4096):
     """Producer of valid blocks drawn directly as bytes (no float weights to
     quantize, so a 7B-shape model takes seconds on any host and the bytes are
-    the same on every machine): uniform random quant codes with scales of the
-    magnitude N(0, 0.02) weights quantize to --
-    Q4_0: d = +-U(0.004, 0.009), nibbles uniform;
-    Q8_0: d = U(3e-4, 7e-4), int8 codes uniform in [-127, 127];
-    Q6_K: d = U(2.5e-5, 5e-5) (fp16 subnormals), 6-bit codes uniform, int8
+    the same on every machine): uniform random quant codes with scales that
+    give the weights a standard deviation of about 0.02, as N(0, 0.02)
+    weights have (larger weights make a deep random model amplify a
+    one-ulp difference of a double sum's rounding layer after layer) --
+    Q4_0: d = +-U(0.003, 0.006), nibbles uniform;
+    Q8_0: d = U(1.5e-4, 3.5e-4), int8 codes uniform in [-127, 127];
+    Q6_K: d = U(1.8e-5, 3.6e-5) (fp16 subnormals), 6-bit codes uniform, int8
     sub-block scales uniform in [-64, 63]."""
     if ty not in (Q4_0, Q8_0, Q6_K):
         raise ValueError(f"random blocks: unsupported type {TYPE_NAMES.get(ty, ty)}")
@@ -402,14 +404,14 @@ def random_blocks(ty: int, rows: int, cols: int, rng: np.random.Generator, chunk
             nb = b.shape[0]
             if ty == Q4_0:
                 sign = np.where(rng.integers(0, 256, nb, dtype=np.uint8) & 1, -1.0, 1.0)
-                b[:, 0:2] = f16(rng.uniform(0.004, 0.009, nb) * sign)
+                b[:, 0:2] = f16(rng.uniform(0.003, 0.006, nb) * sign)
             elif ty == Q8_0:
-                b[:, 0:2] = f16(rng.uniform(3e-4, 7e-4, nb))
+                b[:, 0:2] = f16(rng.uniform(1.5e-4, 3.5e-4, nb))
                 q = b[:, 2:].view(np.int8)
                 np.maximum(q, -127, out=q)
             else:
                 b[:, 192:208] = rng.integers(-64, 64, (nb, 16), dtype=np.int8).view(np.uint8)
-                b[:, 208:210] = f16(rng.uniform(2.5e-5, 5e-5, nb))
+                b[:, 208:210] = f16(rng.uniform(1.8e-5, 3.6e-5, nb))
             yield raw.tobytes()
 
     return produce

@@ -403,3 +403,54 @@ def test_f16_f32_weights_vs_oracle(tmp_path, oracle, mode):
         cur = int(np.argmax(want))
         assert int(np.argmax(got)) == cur
     m.close()
+
+
+_ATTN_CHILD = r"""
+import sys, dataclasses
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from memvanta_amd import capi, synth
+from oracle.pyoracle import Oracle
+o = Oracle()
+for base, n_prompt in ((synth.LLAMA7B_1L, 300), (synth.TINYLLAMA_MIXED_2L, 270)):
+    cfg = dataclasses.replace(base, name=base.name + "-ns", ctx=512)
+    path = sys.argv[2] + "/" + cfg.name + ".gguf"
+    synth.write_model(cfg, path, seed=29, digest=False)
+    prompt = synth.prompt_tokens(6, n_prompt)
+    mo = o.model(path, ctx=512, force_q8=True, threads=16)
+    m = capi.Model(path, ctx=512, act_mode=1, max_batch=32)
+    mo.prefill(prompt, 32, logits=False)
+    m.prefill(prompt, 32, logits=False)
+    cur = 3
+    for i in range(3):
+        want = mo.forward(cur)
+        got = m.forward(cur)
+        rel = float(np.linalg.norm(got.astype(np.float64) - want) / np.linalg.norm(want.astype(np.float64)))
+        same = float((got.view(np.uint32) == want.view(np.uint32)).mean())
+        print(f"{cfg.name} pos {n_prompt + i}: rel {rel:.2e} bit-identical {same:.4f}", flush=True)
+        assert rel <= 1e-3 and same >= 0.999 and int(np.argmax(got)) == int(np.argmax(want))
+        cur = int(np.argmax(want))
+    m.close()
+    mo.close()
+print("ok", flush=True)
+"""
+
+
+@pytest.mark.parametrize("ns", ["1", "4", "0"])
+def test_decode_attention_variants_vs_oracle(tmp_path, ns):
+    """The fused F16 decode attention with every slice count the MVH_ATTN_NS
+    override selects (1 or 4 slices per head for the LDS-staged kernel, 0 for
+    the register-staged one; the default 2 runs in every other model test), in
+    a child process that sets it before any GPU call: head dims 128 (MHA) and
+    64 (GQA 32/4), positions past 256 (a second staging round), against the
+    oracle."""
+    import os
+    import subprocess
+    import sys
+
+    from conftest import ROOT
+
+    env = dict(os.environ, MVH_ATTN_NS=ns)
+    p = subprocess.run([sys.executable, "-u", "-c", _ATTN_CHILD, ROOT, str(tmp_path)], env=env, capture_output=True,
+                       text=True, timeout=110)
+    assert p.returncode == 0 and p.stdout.strip().endswith("ok"), p.stdout + p.stderr
