@@ -65,37 +65,61 @@ __device__ __forceinline__ double swz_xor(double v) {
     return __hiloint2double(swz_xor<XOR>(hi), swz_xor<XOR>(lo));
 }
 
-// Reductions over aligned groups of N lanes (N = 2..32), result in every lane.
+// DPP lane moves (VALU operand modifiers, no LDS round trip): quad_perm
+// [1,0,3,2] = 0xb1 and [2,3,0,1] = 0x4e, row_half_mirror = 0x141 (lane i of
+// each 8 reads lane 7 - i), row_mirror = 0x140 (lane i of each 16 reads 15 - i).
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(dpp_mov<CTRL>(__float_as_int(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov(double v) {
+    return __hiloint2double(dpp_mov<CTRL>(__double2hiint(v)), dpp_mov<CTRL>(__double2loint(v)));
+}
+
+// Reductions over aligned groups of N lanes (N = 2..32), result in every lane
+// of the group (every lane of it must be active): the quad steps, then the
+// half-row and row mirrors pair lanes holding the reductions of disjoint
+// halves; across 16-lane rows a swizzle.
 template <int N>
 __device__ __forceinline__ float group_max(float v) {
+    if constexpr (N >= 2) v = fmaxf(v, dpp_mov<0xb1>(v));
+    if constexpr (N >= 4) v = fmaxf(v, dpp_mov<0x4e>(v));
+    if constexpr (N >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
     if constexpr (N >= 32) v = fmaxf(v, swz_xor<16>(v));
-    if constexpr (N >= 16) v = fmaxf(v, swz_xor<8>(v));
-    if constexpr (N >= 8) v = fmaxf(v, swz_xor<4>(v));
-    if constexpr (N >= 4) v = fmaxf(v, swz_xor<2>(v));
-    if constexpr (N >= 2) v = fmaxf(v, swz_xor<1>(v));
     return v;
 }
 template <int N>
 __device__ __forceinline__ int group_sum(int v) {
+    if constexpr (N >= 2) v += dpp_mov<0xb1>(v);
+    if constexpr (N >= 4) v += dpp_mov<0x4e>(v);
+    if constexpr (N >= 8) v += dpp_mov<0x141>(v);
+    if constexpr (N >= 16) v += dpp_mov<0x140>(v);
     if constexpr (N >= 32) v += swz_xor<16>(v);
-    if constexpr (N >= 16) v += swz_xor<8>(v);
-    if constexpr (N >= 8) v += swz_xor<4>(v);
-    if constexpr (N >= 4) v += swz_xor<2>(v);
-    if constexpr (N >= 2) v += swz_xor<1>(v);
     return v;
 }
-// Double sum over the full wave (xor butterfly inside 32-lane halves, then the
-// two halves through a DPP row broadcast-free readlane pair).
+// Double sum over the full wave, the same value in every lane: DPP within each
+// 16-lane row (the lanes of a row then hold equal sums), then the four rows
+// read and added in row order.
 __device__ __forceinline__ double wave_sum(double v) {
-    v += swz_xor<16>(v);
-    v += swz_xor<8>(v);
-    v += swz_xor<4>(v);
-    v += swz_xor<2>(v);
-    v += swz_xor<1>(v);
-    int lo = __double2loint(v), hi = __double2hiint(v);
-    double other = __hiloint2double(__builtin_amdgcn_readlane(hi, 32), __builtin_amdgcn_readlane(lo, 32));
-    double mine = __hiloint2double(__builtin_amdgcn_readlane(hi, 0), __builtin_amdgcn_readlane(lo, 0));
-    return mine + other;
+    v += dpp_mov<0xb1>(v);
+    v += dpp_mov<0x4e>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    const int lo = __double2loint(v), hi = __double2hiint(v);
+    auto rd = [&](int l) { return __hiloint2double(__builtin_amdgcn_readlane(hi, l), __builtin_amdgcn_readlane(lo, l)); };
+    return ((rd(0) + rd(16)) + rd(32)) + rd(48);
+}
+// Max over the full wave, in every lane.
+__device__ __forceinline__ float wave_max_all(float v) {
+    v = group_max<16>(v);
+    auto rd = [&](int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); };
+    return fmaxf(fmaxf(rd(0), rd(16)), fmaxf(rd(32), rd(48)));
 }
 
 // clamp(lround(v), -lim, lim) as the reference's x86 build evaluates it: a
