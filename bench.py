@@ -740,6 +740,8 @@ def main():
                     help="only the isolated kernel timings plus the read probe and a 256 MiB copy (counter runs)")
     ap.add_argument("--tg-only", action="store_true",
                     help="only the 7B tg128 reps (no pp512, kernel timings, other runs or CPU baseline)")
+    ap.add_argument("--tg-api", action="store_true",
+                    help="with --tg-only: decode through forward() + host argmax (no HIP graph; counter runs)")
     ap.add_argument("--cpu-leg", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_leg:
@@ -802,6 +804,22 @@ def main():
         prompt = synth.prompt_tokens(PROMPT_SEED_7B, PROMPT_TOKENS, vocab)
         seed = prompt[:SEED_TOKENS]
 
+        if args.tg_only and args.tg_api:
+            walls, ids = [], []
+            for _ in range(args.warmup + args.steps):
+                m.reset()
+                m.prefill(seed, BATCH, logits=False)
+                torch.cuda.synchronize()
+                t0, cur, ids = time.perf_counter(), FIRST_TOKEN, []
+                for _ in range(TG_TOKENS):
+                    cur = int(np.argmax(m.forward(cur)))
+                    ids.append(cur)
+                walls.append(time.perf_counter() - t0)
+            m.close()
+            walls = walls[args.warmup:]
+            print(json.dumps({"tg128_api_tok_s": round(TG_TOKENS * len(walls) / sum(walls), 2) if walls else None,
+                              "ids_head": ids[:8]}), flush=True)
+            return
         if args.tg_only:
             tg_wall, tg_dev, ids, ids_same = tg_reps(m, seed, TG_TOKENS, args.steps, args.warmup)
             m.close()

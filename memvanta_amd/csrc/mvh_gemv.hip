@@ -935,18 +935,15 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
 }
 
 // Q6_K with fp32 activations (dot_q6_k_fp32, src/gguf_kernels.cpp:138-146):
-// w = (d*sc[i/16])*q in f32, exact products summed in double.  One wave per
-// row; each lane owns 64 elements of one half super-block and keeps its own
-// double partial, the wave adds the partials as a tree and rounds to f32 once.
-// The double sum order differs from the reference's element order, so a row
-// can differ from it only when the exact sum lies within ~1e-13 (relative) of
-// an f32 rounding boundary.
+// w = (d*sc[i/16])*q in f32, exact products summed in double.  LPR lanes per
+// row (64: one row per wave; 32: two; the launch picks by K); each lane sums
+// 64-element units (a half super-block's sixteen-column group) into its own
+// double partial, the row's lanes add the partials as a tree and round to f32
+// once.  The double sum order differs from the reference's element order, so
+// a row can differ from it only when the exact sum lies within ~1e-13
+// (relative) of an f32 rounding boundary.
 constexpr int kQ6Threads = 256;
 
-// LPR lanes per row (64: one row per wave; 32: two), chosen per K so that
-// the rows' 64-element units fill the lanes (K = 2048: 32 units; K = 5632: 88
-// units in three rounds of 32 rather than two of 64 with 40 lanes idle in
-// the second).
 template <int LPR>
 __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __restrict__ W,
                                                                const float* __restrict__ x, float* __restrict__ y,
@@ -1020,30 +1017,18 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
             }
         }
     };
-    // up to three units per lane: every unit's bytes are loaded before the
-    // activation is staged and before any unit is summed (one memory round
-    // trip per lane rather than one per unit); a lane without a third (or
-    // second) unit reloads its first and skips it
-    const bool pre = units <= 3 * LPR;
-    Raw w[3];
-    if (pre) {
-#pragma unroll
-        for (int i = 0; i < 3; ++i) load_unit(l + i * LPR < units ? l + i * LPR : l, w[i]);
-    }
+    // the activation staged first, then each lane's units loaded and summed in
+    // turn (loading every unit before the staging, which keeps three units'
+    // bytes in registers, measured slower at every shape: 4096->32000 61 against
+    // 39 us, 2048->32000 29 against 21 us, 5632->2048 10 against 8 us)
     const float* xt = x + static_cast<size_t>(blockIdx.y) * K;
     for (int c = threadIdx.x; c < K / 4; c += blockDim.x)
         reinterpret_cast<float4*>(s_x)[c] = reinterpret_cast<const float4*>(xt)[c];
     __syncthreads();
-    if (pre) {
-#pragma unroll
-        for (int i = 0; i < 3; ++i)
-            if (l + i * LPR < units) sum_unit(l + i * LPR, w[i]);
-    } else {
-        for (int u = l; u < units; u += LPR) {
-            Raw w;
-            load_unit(u, w);
-            sum_unit(u, w);
-        }
+    for (int u = l; u < units; u += LPR) {
+        Raw w;
+        load_unit(u, w);
+        sum_unit(u, w);
     }
     double tot;
     if constexpr (LPR == 64) {
@@ -1450,9 +1435,11 @@ hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t r
         y += done * rows;
         batch -= done;
     }
+    // 32 lanes per row up to 64 units (4096->32000 39 against 40 us, 2048->32000
+    // 21 against 29 us), 64 beyond (5632->2048 7.7 against 8.0 us)
     const size_t units = cols / 64;  // 64-element units per row
-    const bool half = (units + 31) / 32 * 32 < (units + 63) / 64 * 64;  // fewer idle lanes at 32 per row
-    const size_t rpw = half ? 8 : 4;                                    // rows per workgroup
+    const bool half = units <= 64;
+    const size_t rpw = half ? 8 : 4;  // rows per workgroup
     const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw), static_cast<unsigned>(batch));
     if (half)
         gemv_q6_k_kernel<32><<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
