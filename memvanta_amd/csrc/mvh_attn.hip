@@ -896,6 +896,111 @@ __global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const void* co
     }
 }
 
+// Scores of a prefill chunk for F16 pages, K read once per head and row
+// block: workgroup (head h, block of kTR positions), every query token of the
+// chunk (B <= 32).  The block's K rows come in with 16-byte loads (a wave's
+// load covers whole rows) into an LDS tile; the chunk's q rows are staged
+// beside it; thread t scores tile row t % kTR for tokens t / kTR + 4k
+// (k = 0..7), with kv_dot_row's order (eight-lane fma over the elements,
+// t0 + .. + t7) and the division by sqrtf(hd).  Writes the raw score of every
+// (token b, position p <= pos0 + b) to s[(b*n_head + h)*pitch + p]; the
+// softmax then runs per (head, token) on those rows (attn_softmax_rows_kernel).
+// Against one workgroup per (head, token) reading its K rows itself, K crosses
+// the caches once per head instead of once per token.
+constexpr int kTR = 64;
+template <int HD>
+__global__ __launch_bounds__(256) void attn_scores_tile_kernel(const void* const* __restrict__ pt_k,
+                                                               const float* __restrict__ q, int q_pitch,
+                                                               float* __restrict__ s_out, int pos0, int B,
+                                                               int n_head, int group, int kv_dim, int page_tokens,
+                                                               int pitch) {
+    constexpr int CPR = HD / 8, KP = 2 * HD + 16;
+    __shared__ __align__(16) uint8_t s_kt[kTR * KP];
+    __shared__ __align__(16) float s_q[32 * HD];
+    const int h = blockIdx.x, r0 = blockIdx.y * kTR, t = threadIdx.x, kh = h / group;
+    const int nmax = pos0 + B;  // rows 0..nmax-1 hold keys (this chunk's included)
+#pragma unroll
+    for (int i = 0; i < kTR * CPR / 256; ++i) {
+        const int pc = i * 256 + t, row = min(r0 + pc / CPR, nmax - 1);
+        const uint16_t* src = static_cast<const uint16_t*>(pt_k[row / page_tokens]) +
+                              static_cast<size_t>(row % page_tokens) * kv_dim + kh * HD + (pc % CPR) * 8;
+        *reinterpret_cast<uint4*>(s_kt + (pc / CPR) * KP + (pc % CPR) * 16) = ld_global16(src);
+    }
+    for (int i = t; i < B * (HD / 4); i += 256) {
+        const int b = i / (HD / 4), c = i % (HD / 4);
+        reinterpret_cast<float4*>(s_q)[i] =
+            *reinterpret_cast<const float4*>(q + static_cast<size_t>(b) * q_pitch + static_cast<size_t>(h) * HD + 4 * c);
+    }
+    __syncthreads();
+    const int rr = t % kTR, tb = t / kTR, r = r0 + rr;
+    float acc[8][8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[k][e] = 0.0f;
+    const uint8_t* kt = s_kt + rr * KP;
+#pragma unroll 4
+    for (int c = 0; c < CPR; ++c) {
+        const half8 hk = as_half8(*reinterpret_cast<const uint4*>(kt + 16 * c));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int b = min(tb + 4 * k, B - 1);  // the waves' tokens: one per wave and k (LDS broadcast)
+            const float4 qa = *reinterpret_cast<const float4*>(s_q + b * HD + 8 * c);
+            const float4 qb = *reinterpret_cast<const float4*>(s_q + b * HD + 8 * c + 4);
+            const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[k][e] = fmaf(qv[e], static_cast<float>(hk[e]), acc[k][e]);
+        }
+    }
+    const float scale = sqrt_rn(static_cast<float>(HD));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int b = tb + 4 * k;
+        float sum = acc[k][0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) sum = sum + acc[k][e];
+        if (b < B && r <= pos0 + b)
+            s_out[(static_cast<size_t>(b) * n_head + h) * pitch + r] = __fdiv_rn(sum, scale);
+    }
+}
+
+// Softmax of the raw scores attn_scores_tile_kernel wrote, in place, one
+// workgroup per (head h, token b) over positions 0..pos0+b: the arithmetic
+// and thread mapping of attn_scores_softmax_kernel's second half (mx,
+// e = expf(s - mx), den in double as the same tree, a = e * float(1/den)).
+__global__ __launch_bounds__(kSM) void attn_softmax_rows_kernel(float* __restrict__ s_io, int pos0, int n_head,
+                                                                int pitch) {
+    __shared__ float red_f[kSM / 64];
+    __shared__ double red_d[kSM / 64];
+    __shared__ uint64_t s_tab[32];
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const int n = pos0 + b + 1;
+    float* sr = s_io + (static_cast<size_t>(b) * n_head + h) * pitch;
+    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    float mx = -INFINITY;
+    for (int tt = t; tt < n; tt += kSM) mx = fmaxf(mx, sr[tt]);
+    mx = wave_max_all(mx);
+    if ((t & 63) == 0) red_f[t >> 6] = mx;
+    __syncthreads();
+    mx = red_f[0];
+#pragma unroll
+    for (int w = 1; w < kSM / 64; ++w) mx = fmaxf(mx, red_f[w]);
+    double den = 0.0;
+    for (int tt = t; tt < n; tt += kSM) {
+        const float e = mvh_expf_tabbed(sr[tt] - mx, s_tab);
+        sr[tt] = e;
+        den += static_cast<double>(e);
+    }
+    den = wave_sum(den);
+    if ((t & 63) == 0) red_d[t >> 6] = den;
+    __syncthreads();
+    den = red_d[0];
+#pragma unroll
+    for (int w = 1; w < kSM / 64; ++w) den += red_d[w];
+    const float inv = static_cast<float>(1.0 / den);
+    for (int tt = t; tt < n; tt += kSM) sr[tt] = sr[tt] * inv;
+}
+
 // Value chains of a prefill chunk: workgroup (head h, 32-element slice of
 // head_dim, group of 32 query tokens); thread = (token b, 4 consecutive
 // elements), out[d] = fma(w_t, V_t[d], out[d]) over t = 0..pos0+b in order,
@@ -1097,6 +1202,12 @@ hipError_t attn_typed(const void* const* pt_k, const void* const* pt_v, const fl
     return hipGetLastError();
 }
 
+// Tuning override MVH_ATTN_SCORES_TILE=0: the per-(head, token) scores kernel for every chunk.
+const bool kScoresTile = [] {
+    const char* e = getenv("MVH_ATTN_SCORES_TILE");
+    return !(e && atoi(e) == 0);
+}();
+
 template <int KT>
 hipError_t attn_prefill_typed(const void* const* pt_k, const void* const* pt_v, const float* q, size_t q_pitch,
                               float* a_scratch, float* out, int8_t* q8, float* q8d, bool q8_op, const int* d_pos,
@@ -1104,6 +1215,24 @@ hipError_t attn_prefill_typed(const void* const* pt_k, const void* const* pt_v, 
                               size_t kv_dim, size_t page_tokens, hipStream_t st) {
     const int group = static_cast<int>(n_head / n_head_kv);
     const int pitch = static_cast<int>(max_pos);  // weight row pitch >= last position + 1
+    if (kScoresTile && KT == kKvF16 && !d_pos && B >= 8 && B <= 32 && (hd == 128 || hd == 64) && q_pitch % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
+        // F16 chunks of 8..32 tokens, q rows 16-byte aligned: K staged once per (head, 64-row block)
+        const dim3 gs(static_cast<unsigned>(n_head), static_cast<unsigned>((pos + B + kTR - 1) / kTR));
+        if (hd == 128)
+            attn_scores_tile_kernel<128><<<gs, 256, 0, st>>>(pt_k, q, static_cast<int>(q_pitch), a_scratch,
+                                                             static_cast<int>(pos), static_cast<int>(B),
+                                                             static_cast<int>(n_head), group, static_cast<int>(kv_dim),
+                                                             static_cast<int>(page_tokens), pitch);
+        else
+            attn_scores_tile_kernel<64><<<gs, 256, 0, st>>>(pt_k, q, static_cast<int>(q_pitch), a_scratch,
+                                                            static_cast<int>(pos), static_cast<int>(B),
+                                                            static_cast<int>(n_head), group, static_cast<int>(kv_dim),
+                                                            static_cast<int>(page_tokens), pitch);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+        attn_softmax_rows_kernel<<<dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(B)), kSM, 0, st>>>(
+            a_scratch, static_cast<int>(pos), static_cast<int>(n_head), pitch);
+    } else {
     // one workgroup per (head, token): all of a chunk's workgroups resident
     // at once (a 128-wide compile-time head_dim that hoists the K loads, or
     // several tokens per workgroup sharing them, need more registers and run
@@ -1112,6 +1241,7 @@ hipError_t attn_prefill_typed(const void* const* pt_k, const void* const* pt_v, 
                                      (hd + max_pos) * sizeof(float), st>>>(
         pt_k, pt_v, q, static_cast<int>(q_pitch), a_scratch, d_pos, static_cast<int>(pos), static_cast<int>(n_head),
         group, static_cast<int>(hd), static_cast<int>(kv_dim), static_cast<int>(page_tokens), pitch);
+    }
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     const dim3 g(static_cast<unsigned>(n_head), static_cast<unsigned>(hd / 32), static_cast<unsigned>((B + 31) / 32));
     attn_pv_chunk_kernel<KT><<<g, kPV, 0, st>>>(pt_v, a_scratch, out, q8, q8d, q8_op, d_pos, static_cast<int>(pos),

@@ -419,15 +419,16 @@ for base, n_prompt in ((synth.LLAMA7B_1L, 300), (synth.TINYLLAMA_MIXED_2L, 270))
     prompt = synth.prompt_tokens(6, n_prompt)
     mo = o.model(path, ctx=512, force_q8=True, threads=16)
     m = capi.Model(path, ctx=512, act_mode=1, max_batch=32)
-    mo.prefill(prompt, 32, logits=False)
-    m.prefill(prompt, 32, logits=False)
+    steps = [("prefill", lambda mm: mm.prefill(prompt, 32))] + [("decode", None)] * 3
     cur = 3
-    for i in range(3):
-        want = mo.forward(cur)
-        got = m.forward(cur)
+    for i, (what, fn) in enumerate(steps):
+        if fn:
+            want, got = fn(mo), fn(m)
+        else:
+            want, got = mo.forward(cur), m.forward(cur)
         rel = float(np.linalg.norm(got.astype(np.float64) - want) / np.linalg.norm(want.astype(np.float64)))
         same = float((got.view(np.uint32) == want.view(np.uint32)).mean())
-        print(f"{cfg.name} pos {n_prompt + i}: rel {rel:.2e} bit-identical {same:.4f}", flush=True)
+        print(f"{cfg.name} {what} pos {n_prompt + i - 1}: rel {rel:.2e} bit-identical {same:.4f}", flush=True)
         assert rel <= 1e-3 and same >= 0.999 and int(np.argmax(got)) == int(np.argmax(want))
         cur = int(np.argmax(want))
     m.close()
@@ -436,22 +437,25 @@ print("ok", flush=True)
 """
 
 
-@pytest.mark.parametrize("ns", ["1", "2", "0"])
-def test_decode_attention_variants_vs_oracle(tmp_path, ns):
-    """The fused F16 decode attention with every slice count the MVH_ATTN_NS
-    override selects (1 or 2 slices per head for the LDS-staged kernel, 0 for
-    the register-staged one; the default -- 4 at head_dim 128, 2 at 64 -- runs
-    in every other model test), in
-    a child process that sets it before any GPU call: head dims 128 (MHA) and
-    64 (GQA 32/4), positions past 256 (a second staging round), against the
-    oracle."""
+@pytest.mark.parametrize("override", ["MVH_ATTN_NS=1", "MVH_ATTN_NS=2", "MVH_ATTN_NS=0", "MVH_ATTN_SCORES_TILE=0"])
+def test_attention_variants_vs_oracle(tmp_path, override):
+    """The attention kernels the tuning overrides select, in a child process
+    that sets the override before any GPU call: the fused F16 decode attention
+    with 1 or 2 slices per head (LDS-staged kernel) or 0 (the register-staged
+    one) -- the default, 4 at head_dim 128 and 2 at 64, runs in every other
+    model test -- and the per-(head, token) prefill scores kernel in place of
+    the K-tile one for F16 chunks of 8..32 tokens.  Head dims 128 (MHA) and 64
+    (GQA 32/4), prefill chunks of 32 ending in ragged ones (12 and 14 tokens),
+    decode positions past 256 (a second staging round); the prefill's last
+    logits and three decode steps against the oracle."""
     import os
     import subprocess
     import sys
 
     from conftest import ROOT
 
-    env = dict(os.environ, MVH_ATTN_NS=ns)
+    key, val = override.split("=")
+    env = dict(os.environ, **{key: val})
     p = subprocess.run([sys.executable, "-u", "-c", _ATTN_CHILD, ROOT, str(tmp_path)], env=env, capture_output=True,
                        text=True, timeout=110)
     assert p.returncode == 0 and p.stdout.strip().endswith("ok"), p.stdout + p.stderr
