@@ -564,7 +564,7 @@ __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ rope, const int* __restrict__ d_pos, uint16_t* kbase, uint16_t* vbase,
     int page_tokens, size_t page_stride, int rows_alloc, float* __restrict__ out, int8_t* __restrict__ q8,
-    float* __restrict__ q8d, int group, int kv_dim) {
+    float* __restrict__ q8d, int group, int kv_dim, int nwg, L2Warm warm, L2Warm warm2) {
     using C = HeadCfg<HD, NS>;
     constexpr int SW = C::SW, CPR = C::CPR, KPT = C::KPT, CV = C::CV, VPT = C::VPT, KP = C::KP, VPP = C::VPP,
                   DPL = C::DPL, half = HD / 2;
@@ -576,8 +576,15 @@ __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
     __shared__ double red_d[kHT / 64];
     __shared__ uint64_t s_tab[32];
 
-    // blockIdx -> (head, slice): the slices of a head on one XCD
-    const int G = gridDim.x, b = blockIdx.x;
+    // blockIdx -> (head, slice): the slices of a head on one XCD; workgroups
+    // from nwg on warm the weights of the GEMVs after it instead (l2_warm;
+    // the o projection's, then a share of the next one's)
+    const int G = nwg, b = blockIdx.x;
+    if (b >= G) {
+        l2_warm<kHT>(warm, b, G, static_cast<int>(gridDim.x) - G);
+        l2_warm<kHT>(warm2, b, G, static_cast<int>(gridDim.x) - G);
+        return;
+    }
     const int hs = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
     const int h = hs / NS, slice = hs - h * NS;
     const int kh = h / group, t = threadIdx.x, dbase = slice * SW;
@@ -1305,7 +1312,8 @@ hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* 
 hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* rope,
                                     const int* d_pos, uint16_t* kbase, uint16_t* vbase, size_t page_tokens,
                                     size_t page_stride, float* out, int8_t* q8, float* q8d, size_t n_head,
-                                    size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st) {
+                                    size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st, const L2Warm& warm,
+                                    const L2Warm& warm2) {
     if (!attn_decode_fused_ok(hd, max_ctx, page_tokens)) return hipErrorInvalidValue;
     const int rows_alloc = static_cast<int>((max_ctx + page_tokens - 1) / page_tokens * page_tokens);
     // head dims 64 and 128 up to kHMaxCtx positions: the LDS-staged kernel,
@@ -1320,10 +1328,14 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
     const int ns = ns_env >= 0 ? ns_env : hd == 128 ? 4 : 2;
     if ((hd == 128 || hd == 64) && max_ctx <= static_cast<size_t>(kHMaxCtx) && ns > 0) {
         const int group = static_cast<int>(n_head / n_head_kv), kvd = static_cast<int>(n_head_kv * hd);
+        auto warm_wgs = [&](size_t g) {
+            return (warm.c1 > warm.c0 || warm2.c1 > warm2.c0) && g < kWarmWgs ? kWarmWgs - static_cast<unsigned>(g) : 0u;
+        };
 #define MVH_ATTN_HEAD(HD_, NS_)                                                                                   \
-    attn_decode_head_kernel<HD_, NS_><<<dim3(static_cast<unsigned>(n_head * NS_)), kHT, 0, st>>>(                \
-        q, k, v, rope, d_pos, kbase, vbase, static_cast<int>(page_tokens), page_stride, rows_alloc, out, q8, q8d, \
-        group, kvd)
+    attn_decode_head_kernel<HD_, NS_>                                                                             \
+        <<<dim3(static_cast<unsigned>(n_head * NS_) + warm_wgs(n_head * NS_)), kHT, 0, st>>>(                     \
+            q, k, v, rope, d_pos, kbase, vbase, static_cast<int>(page_tokens), page_stride, rows_alloc, out, q8, q8d, \
+            group, kvd, static_cast<int>(n_head * NS_), warm, warm2)
         if (hd == 128 && ns == 1) MVH_ATTN_HEAD(128, 1);
         else if (hd == 128 && ns == 4) MVH_ATTN_HEAD(128, 4);
         else if (hd == 128) MVH_ATTN_HEAD(128, 2);

@@ -185,6 +185,45 @@ __device__ __forceinline__ uint4 ld_stream16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// L2 warm-up of a coming decode GEMV's weights by spare workgroups of a
+// launch before it (a norm or the attention, which leave most CUs and HBM
+// idle).  The GEMV's workgroup c reads the contiguous chunk [c*chunk,
+// (c+1)*chunk) of base and runs on XCD c % 8 (a launch's workgroups go to the
+// eight XCDs in turn, each XCD with its own L2), so the warm-up workgroup `id`
+// (of `count` such workgroups starting at grid index `first`, 1-D grid) reads
+// the chunks c in [c0, c1) with c % 8 == id % 8 that fall to it: each chunk
+// lands in the L2 its reader looks in.  Loads only; their values are consumed
+// by an empty asm statement.  c0 == c1: nothing to warm.
+struct L2Warm {
+    const uint8_t* base = nullptr;
+    unsigned chunk = 0;  // bytes, a multiple of 16
+    unsigned c0 = 0, c1 = 0;
+};
+
+template <int NT>
+__device__ __forceinline__ void l2_warm(const L2Warm& w, int id, int first, int count) {
+    const int x = id & 7;
+    const int fx = first + ((x - first) & 7);  // first warm-up workgroup on XCD x
+    const int nx = (first + count - 1 - fx) / 8 + 1;
+    const int c16 = static_cast<int>(w.chunk / 16);
+    const unsigned c_x = w.c0 + ((static_cast<unsigned>(x) - w.c0) & 7u);  // first chunk of [c0, c1) on XCD x
+    for (unsigned c = c_x + 8u * static_cast<unsigned>((id - fx) >> 3); c < w.c1; c += 8u * static_cast<unsigned>(nx)) {
+        const uint4* src = reinterpret_cast<const uint4*>(w.base + static_cast<size_t>(c) * w.chunk);
+        for (int i0 = static_cast<int>(threadIdx.x); i0 < c16; i0 += 8 * NT) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + u * NT;
+                v[u] = i < c16 ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+            }
+            uint32_t acc = 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+            asm volatile("" ::"v"(acc));
+        }
+    }
+}
+
 // Bytes [2*sel, 2*sel+4) of the 8-byte value hi:lo (v_alignbyte_b32).
 __device__ __forceinline__ uint32_t align16(uint32_t hi, uint32_t lo) {
     return __builtin_amdgcn_alignbyte(hi, lo, 2);

@@ -11,6 +11,10 @@ namespace mvh {
 // element 2i = low nibble of qs[i]) and BlockQ8_0 {float d; int8 qs[32]} (36 bytes).
 enum : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ6_K = 14, kNQ4_0 = 0x1002, kNQ8_0 = 0x1008 };
 
+// Grid of the launches that carry L2 warm-up workgroups (warm.c1 > warm.c0): their
+// own workgroups and the warm-up ones fill kWarmWgs (one per CU of the 256)
+constexpr unsigned kWarmWgs = 256;
+
 // ---- activation quantization / conversions (mvh_quant.hip) ----
 // q_op: q in the prefill GEMM's operand order (q8_op_offset; cols % 256 == 0,
 // q8_op_bytes(rows, cols) bytes), else row-major
@@ -105,7 +109,8 @@ bool attn_decode_fused_ok(size_t hd, size_t max_ctx, size_t page_tokens);  // LD
 hipError_t launch_attn_decode_fused(const float* q, const float* k, const float* v, const float* rope,
                                     const int* d_pos, uint16_t* kbase, uint16_t* vbase, size_t page_tokens,
                                     size_t page_stride, float* out, int8_t* q8, float* q8d, size_t n_head,
-                                    size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st);
+                                    size_t n_head_kv, size_t hd, size_t max_ctx, hipStream_t st,
+                                    const L2Warm& warm = {}, const L2Warm& warm2 = {});
 // scores needs n_head * (pos+1) floats of scratch
 hipError_t launch_attn_decode(int kv_type, const void* const* pt_k, const void* const* pt_v, const float* q,
                               float* scores, float* out, size_t pos, size_t n_head, size_t n_head_kv, size_t hd,
@@ -122,9 +127,10 @@ hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, siz
 hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int* tokens, size_t B, float* out,
                         hipStream_t st, const int* d_pos = nullptr, const float* cos_t = nullptr,
                         const float* sin_t = nullptr, size_t half = 0, float* rope_cur = nullptr);
-// x += add (if add), n = rmsnorm(x)*w, and q/qd = Q8 of n (if q); B rows of D
+// x += add (if add), n = rmsnorm(x)*w, and q/qd = Q8 of n (if q); B rows of D;
+// warm.c1 > warm.c0: the launch also warms the next GEMV's weights in L2 (L2Warm)
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
-                          size_t D, float eps, hipStream_t st, bool q_op = false);
+                          size_t D, float eps, hipStream_t st, bool q_op = false, const L2Warm& warm = {});
 // q/k/v of token b at q + b*q_pitch, k + b*kv_pitch, v + b*kv_pitch; the
 // rotated k and v go to the pages when pt_k != null, F16 or F32 (kv_type;
 // Q8 pages are written by launch_kv_write), k is rotated in place either way
@@ -134,7 +140,7 @@ hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, si
                           hipStream_t st);
 // B rows: g/u row b at g + b*pitch, u + b*pitch; ff/q rows of F
 hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff, int8_t* q, float* qd, size_t B,
-                         size_t F, hipStream_t st, bool q_op = false);
+                         size_t F, hipStream_t st, bool q_op = false, const L2Warm& warm = {});
 hipError_t launch_argmax(const float* logits, size_t V, size_t B, int* out, int* d_pos, int* hist, hipStream_t st);
 
 }  // namespace mvh

@@ -53,15 +53,19 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t
 
 // x += add (when add != null), then LlamaModel::rmsnorm (src/llama_model.cpp:237)
 // of each row and optionally its Q8 activation: rmsnorm_row, one workgroup
-// per row.
+// per row; workgroups past the rows warm the next GEMV's weights (l2_warm).
 constexpr int kNormT = 1024;
 constexpr int kNormV = 4;  // float4s per thread: D <= 16384, all held in registers
 __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                          const float* __restrict__ w, float* __restrict__ n,
                                                          int8_t* __restrict__ q, float* __restrict__ qd, int D,
-                                                         float eps, bool q_op) {
+                                                         float eps, bool q_op, int rows, L2Warm warm) {
     __shared__ double red[kNormT / 64];
     const size_t row = blockIdx.x;
+    if (static_cast<int>(blockIdx.x) >= rows) {
+        l2_warm<kNormT>(warm, static_cast<int>(blockIdx.x), rows, static_cast<int>(gridDim.x) - rows);
+        return;
+    }
     rmsnorm_row<kNormT, kNormV>(x + row * D, add ? add + row * D : nullptr, w, n + row * D, q, qd, row, D, eps, q_op,
                                 red);
 }
@@ -119,11 +123,16 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int
 // the C library computes it; optionally the Q8 activation of ff (row-major,
 // or in the prefill GEMM's operand order when q_op).  Row b of g/u at
 // g + b*pitch, u + b*pitch; ff and q rows are F long.  F % 32 == 0
-// (F % 256 == 0 with q_op).
+// (F % 256 == 0 with q_op).  One row (gridDim.y == 1): workgroups from
+// nblk on warm the next GEMV's weights (l2_warm).
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                      int pitch, float* __restrict__ ff, int8_t* __restrict__ q,
-                                                     float* __restrict__ qd, int F, bool q_op) {
+                                                     float* __restrict__ qd, int F, bool q_op, int nblk, L2Warm warm) {
     __shared__ uint64_t s_tab[32];
+    if (static_cast<int>(blockIdx.x) >= nblk) {
+        l2_warm<256>(warm, static_cast<int>(blockIdx.x), nblk, static_cast<int>(gridDim.x) - nblk);
+        return;
+    }
     const int i = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
     const int n4 = F / 4;
     const bool live = i < n4;  // n4 % 8 == 0: 8-lane groups are whole blocks
@@ -222,11 +231,12 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
 }
 
 hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, int8_t* q, float* qd, size_t B,
-                          size_t D, float eps, hipStream_t st, bool q_op) {
+                          size_t D, float eps, hipStream_t st, bool q_op, const L2Warm& warm) {
     if (!B) return hipSuccess;
     if (D % 32 || D > static_cast<size_t>(4 * kNormT * kNormV) || (q_op && D % 256)) return hipErrorInvalidValue;
-    rmsnorm_kernel<<<static_cast<unsigned>(B), kNormT, 0, st>>>(x, add, w, n, q, qd, static_cast<int>(D), eps,
-                                                                q && q_op);
+    const unsigned extra = warm.c1 > warm.c0 && B < kWarmWgs ? kWarmWgs - static_cast<unsigned>(B) : 0u;
+    rmsnorm_kernel<<<static_cast<unsigned>(B) + extra, kNormT, 0, st>>>(x, add, w, n, q, qd, static_cast<int>(D), eps,
+                                                                        q && q_op, static_cast<int>(B), warm);
     return hipGetLastError();
 }
 
@@ -244,12 +254,14 @@ hipError_t launch_rope_kv(float* q, size_t q_pitch, float* k, const float* v, si
 }
 
 hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff, int8_t* q, float* qd, size_t B,
-                         size_t F, hipStream_t st, bool q_op) {
+                         size_t F, hipStream_t st, bool q_op, const L2Warm& warm) {
     const size_t n4 = F / 4;
     if (!n4 || !B) return hipSuccess;
     if (q_op && F % 256) return hipErrorInvalidValue;
-    swiglu_kernel<<<dim3(static_cast<unsigned>((n4 + 255) / 256), static_cast<unsigned>(B)), 256, 0, st>>>(
-        g, u, static_cast<int>(pitch), ff, q, qd, static_cast<int>(F), q && q_op);
+    const unsigned nblk = static_cast<unsigned>((n4 + 255) / 256);
+    const unsigned extra = warm.c1 > warm.c0 && B == 1 && nblk < kWarmWgs ? kWarmWgs - nblk : 0u;
+    swiglu_kernel<<<dim3(nblk + extra, static_cast<unsigned>(B)), 256, 0, st>>>(
+        g, u, static_cast<int>(pitch), ff, q, qd, static_cast<int>(F), q && q_op, static_cast<int>(nblk), warm);
     return hipGetLastError();
 }
 

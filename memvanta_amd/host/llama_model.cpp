@@ -6,6 +6,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 
@@ -189,6 +191,17 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
           "hipHostMalloc");
     logits_.resize(c_.vocab);
     fused_attn_ = kv_type_ == mvh::kKvF16 && mvh::attn_decode_fused_ok(c_.head_dim(), c_.n_ctx, page_tokens_);
+    // default shares: what the RMSNorm and attention launches can fetch while
+    // their own work runs (the SwiGLU launch warming ffn_down measured slower);
+    // MVH_L2_WARM=0 turns the warm-up off, "a,b,c,d,e" sets the five shares
+    const float defaults[kWarmSites] = {0.5f, 1.0f, 0.3f, 0.0f, 0.15f};
+    std::copy(defaults, defaults + kWarmSites, warm_frac_);
+    if (const char* e = getenv("MVH_L2_WARM")) {
+        float f[kWarmSites] = {};
+        const int n = std::sscanf(e, "%f,%f,%f,%f,%f", &f[0], &f[1], &f[2], &f[3], &f[4]);
+        if (n == kWarmSites || (n == 1 && f[0] == 0.0f))
+            for (int i = 0; i < kWarmSites; ++i) warm_frac_[i] = std::clamp(f[i], 0.0f, 1.0f);
+    }
     reset();
 }
 
@@ -369,6 +382,24 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
     prof_stop(w, B);
 }
 
+// The L2 warm-up of a decode GEMV's weights (mvh::l2_warm): a Q4_0 GEMV on
+// the one-token kernel (gemv_q4_rows16: workgroup c reads rows 16c..16c+15,
+// one contiguous chunk) has its chunks from the fraction `from` to from +
+// share pulled into the L2 of the XCD that will read them; other GEMVs get
+// none.
+static mvh::L2Warm l2_warm_for(std::uint32_t type, std::size_t rows, std::size_t cols, const void* d, float from,
+                               float share) {
+    mvh::L2Warm r;
+    if (type != 2 || !mvh::gemv_q4_0_rows16_ok(cols) || share <= 0.0f) return r;
+    const float chunks = static_cast<float>((rows + 15) / 16);
+    const unsigned whole = static_cast<unsigned>(rows / 16);  // a partial last chunk is left cold
+    r.base = static_cast<const uint8_t*>(d);
+    r.chunk = static_cast<unsigned>(16 * (cols / 32) * 18);  // cols % 256 == 0: a multiple of 16
+    r.c0 = std::min(whole, static_cast<unsigned>(from * chunks));
+    r.c1 = std::min(whole, static_cast<unsigned>((from + share) * chunks));
+    return r;
+}
+
 // One decode step (LlamaModel::forward, src/llama_model.cpp:253-259) for the
 // token in *d_token at position *d_pos_.
 void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
@@ -378,12 +409,16 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
     check(mvh::launch_embed(embd_.type, static_cast<const uint8_t*>(embd_.d), D, d_token, 1, a.x, a.st, d_pos_,
                             rope_cos_, rope_sin_, hd / 2, fused_attn_ ? rope_cur_ : nullptr),
           "embed");
+    auto warm = [&](const Tensor& w, float from, float share) {
+        return l2_warm_for(w.type, w.rows, w.cols, w.d, from, share);
+    };
     for (std::size_t li = 0; li < c_.n_layer; ++li) {
         auto& L = layers_[li];
         const auto lay = qkv_layout(L, 1);
         const bool q8_in = L.fused_qkv ? L.qkv.type == 2 : (L.q.type == 2 || L.k.type == 2 || L.v.type == 2);
         check(mvh::launch_rmsnorm(a.x, li ? a.ffo : nullptr, L.attn_norm, a.n, q8_in ? a.q8 : nullptr, a.q8d, 1, D,
-                                  c_.rms_eps, a.st),
+                                  c_.rms_eps, a.st, false,
+                                  warm(L.fused_qkv ? L.qkv : L.q, 0.0f, warm_frac_[0])),
               "rmsnorm");
         if (L.fused_qkv) {
             gemv(L.qkv, a.n, L.qkv.type == 2 ? a.q8 : nullptr, a.q8d, a.qkv);
@@ -403,7 +438,8 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
                                                 reinterpret_cast<uint16_t*>(vslab_ + layer_off), page_tokens_,
                                                 kv_stride_ / 2, a.att,
                                                 o_q8 ? a.q8 : nullptr, a.q8d, c_.n_head, c_.n_head_kv, hd, c_.n_ctx,
-                                                a.st),
+                                                a.st, warm(L.o, 0.0f, warm_frac_[1]),
+                                                warm(L.fused_gu ? L.gate_up : L.gate, 0.0f, warm_frac_[4])),
                   "attention");
         } else if (hd % 32 == 0) {  // F32 / Q8 pages: the chunk kernels with one query token
             store_kv(lay, pk, pv, d_pos_, 0, 1);
@@ -420,7 +456,9 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
         }
         gemv(L.o, a.att, o_q8 ? a.q8 : nullptr, a.q8d, a.proj);
         const bool q8_ffn = L.fused_gu ? L.gate_up.type == 2 : (L.gate.type == 2 || L.up.type == 2);
-        check(mvh::launch_rmsnorm(a.x, a.proj, L.ffn_norm, a.n, q8_ffn ? a.q8 : nullptr, a.q8d, 1, D, c_.rms_eps, a.st),
+        check(mvh::launch_rmsnorm(a.x, a.proj, L.ffn_norm, a.n, q8_ffn ? a.q8 : nullptr, a.q8d, 1, D, c_.rms_eps, a.st,
+                                  false,
+                                  warm(L.fused_gu ? L.gate_up : L.gate, warm_frac_[4], warm_frac_[2])),
               "rmsnorm");
         float* g = a.gu;
         float* u = a.gu + F;  // one token: the fused and the separate layouts coincide
@@ -430,7 +468,9 @@ void LlamaModel::decode_step(const int* d_token, bool logits, bool argmax) {
             gemv(L.gate, a.n, L.gate.type == 2 ? a.q8 : nullptr, a.q8d, g);
             gemv(L.up, a.n, L.up.type == 2 ? a.q8 : nullptr, a.q8d, u);
         }
-        check(mvh::launch_swiglu(g, u, 2 * F, a.ff, L.down.type == 2 ? a.q8 : nullptr, a.q8d, 1, F, a.st), "swiglu");
+        check(mvh::launch_swiglu(g, u, 2 * F, a.ff, L.down.type == 2 ? a.q8 : nullptr, a.q8d, 1, F, a.st, false,
+                                 warm(L.down, 0.0f, warm_frac_[3])),
+              "swiglu");
         gemv(L.down, a.ff, L.down.type == 2 ? a.q8 : nullptr, a.q8d, a.ffo);
     }
     if (logits || argmax) {

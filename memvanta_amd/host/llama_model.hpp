@@ -138,6 +138,12 @@ private:
     std::vector<float> logits_;
     hipGraphExec_t graph_{};
     bool fused_attn_{};  // decode attention in one launch (launch_attn_decode_fused; F16 pages)
+    // L2 warm-up during a decode step (l2_warm), as shares of a GEMV's
+    // weights: q|k|v by the RMSNorm before it, o by the attention, gate|up by
+    // the RMSNorm before it, down by the SwiGLU, and a first share of gate|up
+    // by the attention (the RMSNorm's share then follows it)
+    static constexpr int kWarmSites = 5;
+    float warm_frac_[kWarmSites]{};
     // kernel profiler: GEMV / GEMM launches of a step are timed while it is on
     std::unique_ptr<prof::Recorder> rec_;
     bool profiling_{};

@@ -437,17 +437,21 @@ print("ok", flush=True)
 """
 
 
-@pytest.mark.parametrize("override", ["MVH_ATTN_NS=1", "MVH_ATTN_NS=2", "MVH_ATTN_NS=0", "MVH_ATTN_SCORES_TILE=0"])
+@pytest.mark.parametrize("override", ["MVH_ATTN_NS=1", "MVH_ATTN_NS=2", "MVH_ATTN_NS=0", "MVH_ATTN_SCORES_TILE=0",
+                                      "MVH_L2_WARM=0", "MVH_L2_WARM=1,1,1,1,1"])
 def test_attention_variants_vs_oracle(tmp_path, override):
-    """The attention kernels the tuning overrides select, in a child process
-    that sets the override before any GPU call: the fused F16 decode attention
-    with 1 or 2 slices per head (LDS-staged kernel) or 0 (the register-staged
-    one) -- the default, 4 at head_dim 128 and 2 at 64, runs in every other
-    model test -- and the per-(head, token) prefill scores kernel in place of
-    the K-tile one for F16 chunks of 8..32 tokens.  Head dims 128 (MHA) and 64
-    (GQA 32/4), prefill chunks of 32 ending in ragged ones (12 and 14 tokens),
-    decode positions past 256 (a second staging round); the prefill's last
-    logits and three decode steps against the oracle."""
+    """The kernels the tuning overrides select, in a child process that sets
+    the override before any GPU call: the fused F16 decode attention with 1 or
+    2 slices per head (LDS-staged kernel) or 0 (the register-staged one) --
+    the default, 4 at head_dim 128 and 2 at 64, runs in every other model
+    test --, the per-(head, token) prefill scores kernel in place of the
+    K-tile one for F16 chunks of 8..32 tokens, and the decode step's L2
+    warm-up of the Q4_0 GEMV weights off or at every site in full (the norm,
+    attention and SwiGLU launches then carry warm-up workgroups over whole
+    tensors).  Head dims 128 (MHA) and 64 (GQA 32/4), prefill chunks of 32
+    ending in ragged ones (12 and 14 tokens), decode positions past 256 (a
+    second staging round); the prefill's last logits and three decode steps
+    against the oracle."""
     import os
     import subprocess
     import sys
