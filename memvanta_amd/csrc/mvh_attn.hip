@@ -7,6 +7,7 @@
 // layout of src/llama_model.cpp:18-22.
 #include "mvh_kernels.hpp"
 #define MVH_EXPF_QUAL __device__ __forceinline__
+#define MVH_EXPF_TABLE static __constant__ const
 #include "mvh_expf.h"
 
 namespace mvh {
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
                                                             float* __restrict__ q8d, bool q8_op) {
     extern __shared__ float s_a[];  // [score_pitch] weights; Q8: then [score_pitch] V row scales
     __shared__ uint64_t s_tab[32];
-    if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
+    const uint64_t tab_v = mvh_expf_tab(threadIdx.x);  // the expf table, stored to LDS after the other loads
     const int h = blockIdx.x, b = blockIdx.z;
     const int n = (d_pos ? *d_pos : pos_arg) + b + 1;
     if constexpr (KT == kKvQ8) {  // V row scales: loads issued before the softmax, in flight meanwhile
@@ -183,6 +184,7 @@ __global__ __launch_bounds__(64) void attn_softmax_v_kernel(const void* const* _
         for (int t = threadIdx.x; t < n; t += 64)
             s_vs[t] = kv_row_scale<KT>(pt_v[t / page_tokens], t % page_tokens, page_tokens, kv_dim);
     }
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = tab_v;
     __syncthreads();
     const float* sc = scores + (static_cast<size_t>(b) * n_head + h) * score_pitch;
     float mx = -INFINITY;
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
     // for q/k/v and the RoPE row alone while the K rows and V are in flight (a
     // load under a branch makes the compiler's wait cover all of them).
     const int pos = *d_pos;
-    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    const uint64_t tab_v = mvh_expf_tab(t);  // the expf table, stored to LDS after the other loads
     const int th = t < half ? t : 0;
     const float* qh = q + static_cast<size_t>(h) * hd;
     const float* kk = k + static_cast<size_t>(kh) * hd;
@@ -363,6 +365,7 @@ __global__ __launch_bounds__(kAT) void attn_decode_fused_kernel(
             vc[t + half] = hv1;
         }
     }
+    if (t < 32) s_tab[t] = tab_v;
     __syncthreads();
 
     // 2. scores
@@ -559,12 +562,14 @@ struct HeadCfg {
     static_assert(kHR * CPR % kHT == 0 && kHR * CV % kHT == 0 && LANES <= 64 && DPL <= 2, "head attention shape");
 };
 
+// The arguments the first instructions need come first: the 14 dwords the
+// dispatch preloads into SGPRs hold nwg .. kbase (q, k and v are one buffer:
+// k at q + n_head * HD, v at k + kv_dim).
 template <int HD, int NS>
 __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    int nwg, int group, int page_tokens, int kv_dim, int rows_alloc, int page_stride, const float* __restrict__ q,
     const float* __restrict__ rope, const int* __restrict__ d_pos, uint16_t* kbase, uint16_t* vbase,
-    int page_tokens, size_t page_stride, int rows_alloc, float* __restrict__ out, int8_t* __restrict__ q8,
-    float* __restrict__ q8d, int group, int kv_dim, int nwg, L2Warm warm, L2Warm warm2) {
+    float* __restrict__ out, int8_t* __restrict__ q8, float* __restrict__ q8d, L2Warm warm, L2Warm warm2) {
     using C = HeadCfg<HD, NS>;
     constexpr int SW = C::SW, CPR = C::CPR, KPT = C::KPT, CV = C::CV, VPT = C::VPT, KP = C::KP, VPP = C::VPP,
                   DPL = C::DPL, half = HD / 2;
@@ -588,6 +593,8 @@ __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
     const int hs = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
     const int h = hs / NS, slice = hs - h * NS;
     const int kh = h / group, t = threadIdx.x, dbase = slice * SW;
+    const float* k = q + static_cast<size_t>(G / NS) * HD;
+    const float* v = k + kv_dim;
     auto row_off = [&](int tt) {
         return static_cast<size_t>(tt / page_tokens) * page_stride + static_cast<size_t>(tt % page_tokens) * kv_dim +
                kh * HD;
@@ -596,9 +603,12 @@ __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
     const int vi = t & 7, vc = (t >> 3) % CV;
 
     // the one round trip: position, q/k/v, the RoPE row, K round 0 and this
-    // thread's chunk of the position's v
-    const int pos = *d_pos;
-    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    // thread's chunk of the position's v (the position by a vector load, made
+    // uniform only after the K loads are issued: a scalar load of it would
+    // hold up the K loads, whose addresses wait for the kernel's argument
+    // loads on the same counter)
+    const int pos_v = ld_global_lanes(d_pos);
+    const uint64_t tab_v = mvh_expf_tab(t);  // the expf table, stored to LDS after the RoPE
     const int th = t < half ? t : 0;
     const float* qh = q + static_cast<size_t>(h) * HD;
     const float* kk = k + static_cast<size_t>(kh) * HD;
@@ -626,6 +636,7 @@ __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
     };
     load_k(0);
     __builtin_amdgcn_sched_barrier(0);
+    const int pos = __builtin_amdgcn_readfirstlane(pos_v);
 
     // RoPE (every thread computes it so the loads are used outside a branch)
     const float rq0 = fmaf(q0, cs, -(q1 * sn)), rq1 = fmaf(q0, sn, q1 * cs);
@@ -647,6 +658,7 @@ __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
             vc_[t + half] = hv1;
         }
     }
+    if (t < 32) s_tab[t] = tab_v;
     // stores of the staged registers, the position's row replaced by the RoPE'd k
     auto store_k = [&](int r0) {
 #pragma unroll
@@ -862,8 +874,9 @@ __global__ __launch_bounds__(kSM) void attn_scores_softmax_kernel(const void* co
     const int n = (d_pos ? *d_pos : pos_arg) + b + 1;
     const int kh = h / group;
     const float* qh = q + static_cast<size_t>(b) * q_pitch + static_cast<size_t>(h) * hd;
+    const uint64_t tab_v = mvh_expf_tab(t);
     for (int i = t; i < hd; i += kSM) s_q[i] = qh[i];
-    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    if (t < 32) s_tab[t] = tab_v;
     __syncthreads();
     const float scale = sqrt_rn(static_cast<float>(hd));
     float mx = -INFINITY;
@@ -983,11 +996,12 @@ __global__ __launch_bounds__(kSM) void attn_softmax_rows_kernel(float* __restric
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
     const int n = pos0 + b + 1;
     float* sr = s_io + (static_cast<size_t>(b) * n_head + h) * pitch;
-    if (t < 32) s_tab[t] = mvh_expf_tab(t);
+    const uint64_t tab_v = mvh_expf_tab(t);
     float mx = -INFINITY;
     for (int tt = t; tt < n; tt += kSM) mx = fmaxf(mx, sr[tt]);
     mx = wave_max_all(mx);
     if ((t & 63) == 0) red_f[t >> 6] = mx;
+    if (t < 32) s_tab[t] = tab_v;
     __syncthreads();
     mx = red_f[0];
 #pragma unroll
@@ -1326,7 +1340,9 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
     // default: four slices per head at head_dim 128 (tg128 562.9 against
     // 561.8 tok/s with two, 543 with one), two at 64
     const int ns = ns_env >= 0 ? ns_env : hd == 128 ? 4 : 2;
-    if ((hd == 128 || hd == 64) && max_ctx <= static_cast<size_t>(kHMaxCtx) && ns > 0) {
+    // the LDS-staged kernel takes q, k and v as one buffer (the decode step's q|k|v)
+    const bool qkv_one = k == q + n_head * hd && v == k + n_head_kv * hd && page_stride <= INT32_MAX;
+    if ((hd == 128 || hd == 64) && max_ctx <= static_cast<size_t>(kHMaxCtx) && ns > 0 && qkv_one) {
         const int group = static_cast<int>(n_head / n_head_kv), kvd = static_cast<int>(n_head_kv * hd);
         auto warm_wgs = [&](size_t g) {
             return (warm.c1 > warm.c0 || warm2.c1 > warm2.c0) && g < kWarmWgs ? kWarmWgs - static_cast<unsigned>(g) : 0u;
@@ -1334,8 +1350,8 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
 #define MVH_ATTN_HEAD(HD_, NS_)                                                                                   \
     attn_decode_head_kernel<HD_, NS_>                                                                             \
         <<<dim3(static_cast<unsigned>(n_head * NS_) + warm_wgs(n_head * NS_)), kHT, 0, st>>>(                     \
-            q, k, v, rope, d_pos, kbase, vbase, static_cast<int>(page_tokens), page_stride, rows_alloc, out, q8, q8d, \
-            group, kvd, static_cast<int>(n_head * NS_), warm, warm2)
+            static_cast<int>(n_head * NS_), group, static_cast<int>(page_tokens), kvd, rows_alloc,                \
+            static_cast<int>(page_stride), q, rope, d_pos, kbase, vbase, out, q8, q8d, warm, warm2)
         if (hd == 128 && ns == 1) MVH_ATTN_HEAD(128, 1);
         else if (hd == 128 && ns == 4) MVH_ATTN_HEAD(128, 4);
         else if (hd == 128) MVH_ATTN_HEAD(128, 2);

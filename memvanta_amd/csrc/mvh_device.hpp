@@ -172,6 +172,17 @@ __device__ __forceinline__ uint4 ld_global16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// A uniform int read by a vector load in every lane (the address offset by a
+// zero the compiler cannot see through), where a scalar load would share its
+// wait counter with the kernel's argument loads: the first wait for an
+// argument would then also wait for this load's trip to memory.  Vector
+// loads complete in issue order, so its value is waited for where it is used.
+__device__ __forceinline__ int ld_global_lanes(const int* p) {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return *(const __attribute__((address_space(1))) int*)(reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(z));
+}
+
 // 8-byte form of ld_global16.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint2 ld_global8(const void* p) {

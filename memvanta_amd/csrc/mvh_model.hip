@@ -4,6 +4,7 @@
 // from device memory, so one captured HIP graph serves every decode step.
 #include "mvh_kernels.hpp"
 #define MVH_EXPF_QUAL __device__ __forceinline__
+#define MVH_EXPF_TABLE static __constant__ const
 #include "mvh_expf.h"
 
 namespace mvh {
@@ -56,10 +57,10 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t
 // per row; workgroups past the rows warm the next GEMV's weights (l2_warm).
 constexpr int kNormT = 1024;
 constexpr int kNormV = 4;  // float4s per thread: D <= 16384, all held in registers
-__global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ add,
+__global__ __launch_bounds__(kNormT) void rmsnorm_kernel(int rows, float* __restrict__ x, const float* __restrict__ add,
                                                          const float* __restrict__ w, float* __restrict__ n,
                                                          int8_t* __restrict__ q, float* __restrict__ qd, int D,
-                                                         float eps, bool q_op, int rows, L2Warm warm) {
+                                                         float eps, bool q_op, L2Warm warm) {
     __shared__ double red[kNormT / 64];
     const size_t row = blockIdx.x;
     if (static_cast<int>(blockIdx.x) >= rows) {
@@ -125,9 +126,10 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, int
 // g + b*pitch, u + b*pitch; ff and q rows are F long.  F % 32 == 0
 // (F % 256 == 0 with q_op).  One row (gridDim.y == 1): workgroups from
 // nblk on warm the next GEMV's weights (l2_warm).
-__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
-                                                     int pitch, float* __restrict__ ff, int8_t* __restrict__ q,
-                                                     float* __restrict__ qd, int F, bool q_op, int nblk, L2Warm warm) {
+__global__ __launch_bounds__(256) void swiglu_kernel(int nblk, int pitch, const float* __restrict__ g,
+                                                     const float* __restrict__ u, float* __restrict__ ff,
+                                                     int8_t* __restrict__ q, float* __restrict__ qd, int F, bool q_op,
+                                                     L2Warm warm) {
     __shared__ uint64_t s_tab[32];
     if (static_cast<int>(blockIdx.x) >= nblk) {
         l2_warm<256>(warm, static_cast<int>(blockIdx.x), nblk, static_cast<int>(gridDim.x) - nblk);
@@ -141,7 +143,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
         a = reinterpret_cast<const float4*>(g + static_cast<size_t>(b) * pitch)[i];
         c = reinterpret_cast<const float4*>(u + static_cast<size_t>(b) * pitch)[i];
     }
-    if (threadIdx.x < 32) s_tab[threadIdx.x] = mvh_expf_tab(threadIdx.x);
+    const uint64_t tab_v = mvh_expf_tab(threadIdx.x);
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = tab_v;
     __syncthreads();
     if (live) {
         auto f = [&](float z, float up) { return __fdiv_rn(z, 1.0f + mvh_expf_tabbed(-z, s_tab)) * up; };
@@ -235,8 +238,8 @@ hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, 
     if (!B) return hipSuccess;
     if (D % 32 || D > static_cast<size_t>(4 * kNormT * kNormV) || (q_op && D % 256)) return hipErrorInvalidValue;
     const unsigned extra = warm.c1 > warm.c0 && B < kWarmWgs ? kWarmWgs - static_cast<unsigned>(B) : 0u;
-    rmsnorm_kernel<<<static_cast<unsigned>(B) + extra, kNormT, 0, st>>>(x, add, w, n, q, qd, static_cast<int>(D), eps,
-                                                                        q && q_op, static_cast<int>(B), warm);
+    rmsnorm_kernel<<<static_cast<unsigned>(B) + extra, kNormT, 0, st>>>(static_cast<int>(B), x, add, w, n, q, qd,
+                                                                        static_cast<int>(D), eps, q && q_op, warm);
     return hipGetLastError();
 }
 
@@ -261,7 +264,7 @@ hipError_t launch_swiglu(const float* g, const float* u, size_t pitch, float* ff
     const unsigned nblk = static_cast<unsigned>((n4 + 255) / 256);
     const unsigned extra = warm.c1 > warm.c0 && B == 1 && nblk < kWarmWgs ? kWarmWgs - nblk : 0u;
     swiglu_kernel<<<dim3(nblk + extra, static_cast<unsigned>(B)), 256, 0, st>>>(
-        g, u, static_cast<int>(pitch), ff, q, qd, static_cast<int>(F), q && q_op, static_cast<int>(nblk), warm);
+        static_cast<int>(nblk), static_cast<int>(pitch), g, u, ff, q, qd, static_cast<int>(F), q && q_op, warm);
     return hipGetLastError();
 }
 
