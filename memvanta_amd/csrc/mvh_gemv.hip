@@ -1022,7 +1022,7 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
     // bytes in registers, measured slower at every shape: 4096->32000 61 against
     // 39 us, 2048->32000 29 against 21 us, 5632->2048 10 against 8 us)
     const float* xt = x + static_cast<size_t>(blockIdx.y) * K;
-    for (int c = threadIdx.x; c < K / 4; c += blockDim.x)
+    for (int c = threadIdx.x; c < K / 4; c += kQ6Threads)
         reinterpret_cast<float4*>(s_x)[c] = reinterpret_cast<const float4*>(xt)[c];
     __syncthreads();
     for (int u = l; u < units; u += LPR) {

@@ -37,12 +37,11 @@ __device__ __forceinline__ float dequant_elem(uint32_t type, const uint8_t* W, i
 namespace {
 
 // Embedding rows of B tokens (token ids in device memory).
-__global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t* __restrict__ W, int cols,
+__global__ __launch_bounds__(256) void embed_kernel(uint32_t type, int cols, int half, const uint8_t* __restrict__ W,
                                                     const int* __restrict__ tokens, float* __restrict__ out,
                                                     const int* __restrict__ d_pos, const float* __restrict__ cos_t,
-                                                    const float* __restrict__ sin_t, int half,
-                                                    float* __restrict__ rope_cur) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+                                                    const float* __restrict__ sin_t, float* __restrict__ rope_cur) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= cols) return;
     out[static_cast<size_t>(blockIdx.y) * cols + i] = dequant_elem(type, W, cols, static_cast<size_t>(tokens[blockIdx.y]), i);
     if (rope_cur && i < half) {  // the decode attention's RoPE row, read without waiting for the position
@@ -57,10 +56,10 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type, const uint8_t
 // per row; workgroups past the rows warm the next GEMV's weights (l2_warm).
 constexpr int kNormT = 1024;
 constexpr int kNormV = 4;  // float4s per thread: D <= 16384, all held in registers
-__global__ __launch_bounds__(kNormT) void rmsnorm_kernel(int rows, float* __restrict__ x, const float* __restrict__ add,
-                                                         const float* __restrict__ w, float* __restrict__ n,
-                                                         int8_t* __restrict__ q, float* __restrict__ qd, int D,
-                                                         float eps, bool q_op, L2Warm warm) {
+__global__ __launch_bounds__(kNormT) void rmsnorm_kernel(int rows, int D, float eps, bool q_op, float* __restrict__ x,
+                                                         const float* __restrict__ add, const float* __restrict__ w,
+                                                         float* __restrict__ n, int8_t* __restrict__ q,
+                                                         float* __restrict__ qd, L2Warm warm) {
     __shared__ double red[kNormT / 64];
     const size_t row = blockIdx.x;
     if (static_cast<int>(blockIdx.x) >= rows) {
@@ -135,7 +134,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(int nblk, int pitch, const 
         l2_warm<256>(warm, static_cast<int>(blockIdx.x), nblk, static_cast<int>(gridDim.x) - nblk);
         return;
     }
-    const int i = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
     const int n4 = F / 4;
     const bool live = i < n4;  // n4 % 8 == 0: 8-lane groups are whole blocks
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f), c = a, o = a;
@@ -229,7 +228,7 @@ hipError_t launch_embed(uint32_t type, const uint8_t* W, size_t cols, const int*
     if (!B) return hipSuccess;
     if (rope_cur && (B != 1 || !d_pos || !cos_t || !sin_t || half > cols)) return hipErrorInvalidValue;
     embed_kernel<<<dim3(static_cast<unsigned>((cols + 255) / 256), static_cast<unsigned>(B)), 256, 0, st>>>(
-        type, W, static_cast<int>(cols), tokens, out, d_pos, cos_t, sin_t, static_cast<int>(half), rope_cur);
+        type, static_cast<int>(cols), static_cast<int>(half), W, tokens, out, d_pos, cos_t, sin_t, rope_cur);
     return hipGetLastError();
 }
 
@@ -238,8 +237,8 @@ hipError_t launch_rmsnorm(float* x, const float* add, const float* w, float* n, 
     if (!B) return hipSuccess;
     if (D % 32 || D > static_cast<size_t>(4 * kNormT * kNormV) || (q_op && D % 256)) return hipErrorInvalidValue;
     const unsigned extra = warm.c1 > warm.c0 && B < kWarmWgs ? kWarmWgs - static_cast<unsigned>(B) : 0u;
-    rmsnorm_kernel<<<static_cast<unsigned>(B) + extra, kNormT, 0, st>>>(static_cast<int>(B), x, add, w, n, q, qd,
-                                                                        static_cast<int>(D), eps, q && q_op, warm);
+    rmsnorm_kernel<<<static_cast<unsigned>(B) + extra, kNormT, 0, st>>>(static_cast<int>(B), static_cast<int>(D), eps,
+                                                                        q && q_op, x, add, w, n, q, qd, warm);
     return hipGetLastError();
 }
 
