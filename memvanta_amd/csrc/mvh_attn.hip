@@ -1061,12 +1061,12 @@ struct PvRaw<kKvQ8> {
     }
 };
 template <int KT>
-__global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(const void* const* __restrict__ pt_v,
-                                                            const float* __restrict__ a, float* __restrict__ out,
-                                                            int8_t* __restrict__ q8, float* __restrict__ q8d,
-                                                            bool q8_op, const int* __restrict__ d_pos, int pos_arg,
-                                                            int B, int n_head, int group, int hd, int kv_dim,
-                                                            int page_tokens, int pitch) {
+__global__ __launch_bounds__(kPV) void attn_pv_chunk_kernel(int pos_arg, int B, int n_head, int group, int hd,
+                                                            int kv_dim, int page_tokens, int pitch,
+                                                            const void* const* __restrict__ pt_v,
+                                                            const float* __restrict__ a, const int* __restrict__ d_pos,
+                                                            float* __restrict__ out, int8_t* __restrict__ q8,
+                                                            float* __restrict__ q8d, bool q8_op) {
     typedef typename KvElem<KT>::T E;
     __shared__ __align__(16) E s_v[kPVRows][PvTile<KT>::kPitch];  // V tile: rows x the slice's 32 elements
     __shared__ __align__(16) float s_at[32][kPVRows + 4];       // weights: token x tile row
@@ -1265,10 +1265,10 @@ hipError_t attn_prefill_typed(const void* const* pt_k, const void* const* pt_v, 
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     const dim3 g(static_cast<unsigned>(n_head), static_cast<unsigned>(hd / 32), static_cast<unsigned>((B + 31) / 32));
-    attn_pv_chunk_kernel<KT><<<g, kPV, 0, st>>>(pt_v, a_scratch, out, q8, q8d, q8_op, d_pos, static_cast<int>(pos),
-                                                static_cast<int>(B), static_cast<int>(n_head), group,
-                                                static_cast<int>(hd), static_cast<int>(kv_dim),
-                                                static_cast<int>(page_tokens), pitch);
+    attn_pv_chunk_kernel<KT><<<g, kPV, 0, st>>>(static_cast<int>(pos), static_cast<int>(B), static_cast<int>(n_head),
+                                                group, static_cast<int>(hd), static_cast<int>(kv_dim),
+                                                static_cast<int>(page_tokens), pitch, pt_v, a_scratch, d_pos, out, q8,
+                                                q8d, q8_op);
     return hipGetLastError();
 }
 }  // namespace

@@ -25,17 +25,18 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 // ties away from zero, and a mantissa carry is OR-ed (not added) into the
 // exponent field.  The F16 KV cache must hold exactly these bits, so this is
 // integer code, not v_cvt_f16_f32.
+// The reference's branches are all evaluated and one is selected: as branches
+// every conversion costs a few exec-mask round trips even when all lanes
+// agree.
 __device__ __forceinline__ uint16_t f2h_ref(float f) {
-    uint32_t x = __float_as_uint(f);
-    uint32_t sign = (x >> 16) & 0x8000u, mant = x & 0x7fffffu;
-    int e = static_cast<int>((x >> 23) & 0xffu) - 112;  // -127 + 15
-    if (e <= 0) {
-        if (e < -10) return static_cast<uint16_t>(sign);
-        mant = (mant | 0x800000u) >> (1 - e);
-        return static_cast<uint16_t>(sign + ((mant + 0x1000u) >> 13));
-    }
-    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
-    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | ((mant + 0x1000u) >> 13));
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u, mant = x & 0x7fffffu;
+    const int e = static_cast<int>((x >> 23) & 0xffu) - 112;  // -127 + 15
+    const uint32_t sh = static_cast<uint32_t>(min(max(1 - e, 0), 31));  // 1..11 where used
+    const uint32_t sub = sign + ((((mant | 0x800000u) >> sh) + 0x1000u) >> 13);            // -10 <= e <= 0
+    const uint32_t nrm = sign | (static_cast<uint32_t>(e) << 10) | ((mant + 0x1000u) >> 13);  // 1 <= e <= 30
+    const uint32_t r = e <= 0 ? (e < -10 ? sign : sub) : (e >= 31 ? (sign | 0x7c00u) : nrm);
+    return static_cast<uint16_t>(r);
 }
 
 // ---- correctly rounded sqrt ---------------------------------------------------

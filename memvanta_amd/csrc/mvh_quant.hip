@@ -11,7 +11,7 @@ namespace mvh {
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float4* __restrict__ x, uint32_t* __restrict__ q,
                                                           float* __restrict__ d, int* __restrict__ s, size_t n4,
                                                           int op_cols) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
     const bool live = i < n4;  // n4 % 8 == 0, so an 8-lane group is all-live or all-dead
     const float4 v = live ? x[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     float dd;
