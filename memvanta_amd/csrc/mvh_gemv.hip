@@ -936,15 +936,16 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
 
 // Q6_K with fp32 activations (dot_q6_k_fp32, src/gguf_kernels.cpp:138-146):
 // w = (d*sc[i/16])*q in f32, exact products summed in double.  LPR lanes per
-// row (64: one row per wave; 32: two; the launch picks by K); each lane sums
+// row (64: one row per wave; 32: two; the launch picks by K), each lane
+// working on R rows at once (the launch picks by row count); each lane sums
 // 64-element units (a half super-block's sixteen-column group) into its own
-// double partial, the row's lanes add the partials as a tree and round to f32
-// once.  The double sum order differs from the reference's element order, so
+// double partial per row, the row's lanes add the partials as a tree and
+// round to f32 once.  The double sum order differs from the reference's element order, so
 // a row can differ from it only when the exact sum lies within ~1e-13
 // (relative) of an f32 rounding boundary.
 constexpr int kQ6Threads = 256;
 
-template <int LPR>
+template <int LPR, int R>
 __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __restrict__ W,
                                                                const float* __restrict__ x, float* __restrict__ y,
                                                                int N, int K) {
@@ -954,9 +955,13 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
     const int nsb = K / 256;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l = lane % LPR;
-    const int row = blockIdx.x * (kQ6Threads / 64) * kRpw + wave * kRpw + lane / LPR;
+    // a lane sums the same units of R consecutive rows (each activation value
+    // converted once for all R)
+    const int row = (blockIdx.x * (kQ6Threads / 64) * kRpw + wave * kRpw + lane / LPR) * R;
     // rows past N sum row N - 1 (the lane groups reduce together) and are not written
-    const uint8_t* rb = W + static_cast<size_t>(min(row, N - 1)) * nsb * 210;
+    const uint8_t* rb[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rb[r] = W + static_cast<size_t>(min(row + r, N - 1)) * nsb * 210;
     const int units = 4 * nsb;
     // unit u of the row: ql bytes g*64 + h*16 (elements j = 0, 2) and
     // g*64 + 32 + h*16 (j = 1, 3), qh bytes 128 + g*32 + h*16, scales
@@ -966,9 +971,9 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
         int sc[4];
         uint32_t d;
     };
-    auto load_unit = [&](int u, Raw& w) __attribute__((always_inline)) {
+    auto load_unit = [&](int u, const uint8_t* rbase, Raw& w) __attribute__((always_inline)) {
         const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
-        const uint8_t* b = rb + static_cast<size_t>(sb) * 210;
+        const uint8_t* b = rbase + static_cast<size_t>(sb) * 210;
         const uint16_t* pa = reinterpret_cast<const uint16_t*>(b + g * 64 + h * 16);
         const uint16_t* pb = reinterpret_cast<const uint16_t*>(b + g * 64 + 32 + h * 16);
         const uint16_t* ph = reinterpret_cast<const uint16_t*>(b + 128 + g * 32 + h * 16);
@@ -983,38 +988,67 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
         for (int j = 0; j < 4; ++j) w.sc[j] = sc[2 * j];
         w.d = *reinterpret_cast<const uint16_t*>(b + 208);
     };
-    double acc = 0.0;
-    auto sum_unit = [&](int u, const Raw& w) __attribute__((always_inline)) {
-        const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
-        const float d = h2f(w.d);
-        float dsc[4], off[4];
+    // Every weight w = (d*sc)*q is exact in f32 (d*sc has at most 18
+    // significant bits, |q| <= 32 at most 5), so w*x = (d*sc) * (q*x) with
+    // q*x exact in double: each 16-element group (one scale) sums q*x in
+    // double and adds (d*sc) times that sum -- the reference's exact terms,
+    // added in another order (as the partials and the lane tree already do)
+    double acc[R];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            dsc[j] = d * static_cast<float>(w.sc[j]);
-            off[j] = -32.0f * dsc[j];  // exact (a power-of-two multiple)
-        }
-        const float* xb = s_x + sb * 256 + g * 128 + h * 16;
+    for (int r = 0; r < R; ++r) acc[r] = 0.0;
+    auto sum_unit = [&](int u, const Raw (&w)[R]) __attribute__((always_inline)) {
+        const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
+        // float4 f of the activation sits at f ^ swz(f) (the staging below);
+        // here f = base + 8j + c, so bits 0..1 (c) and 3 (j's bit 0) move
+        const float4* xb = reinterpret_cast<const float4*>(s_x) + sb * 64 + g * 32 + h * 4;
+        const int kv = (u >> 1) & 7, klo = kv & 3, kb = kv >> 2;
+        double part[R][4];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part[r][j] = 0.0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {  // columns 4c .. 4c+3 of the group
-            // the 6-bit codes u = q + 32 of element group j as four bytes:
-            // low nibbles (j = 0, 1) or high nibbles (j = 2, 3) of ql, bits
-            // 2j..2j+1 of qh above them
-            const uint32_t qa = w.qa[c], qb = w.qb[c], qh = w.qh[c];
-            const uint32_t u[4] = {(qa & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u),
-                                   (qb & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u),
-                                   ((qa >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u),
-                                   ((qb >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u)};
+            // the 6-bit codes u = q + 32 of element group j as four bytes
+            // (low nibbles (j = 0, 1) or high nibbles (j = 2, 3) of ql, bits
+            // 2j..2j+1 of qh above them), bit 5 flipped: a byte's low six bits
+            // are then q in two's complement
+            // (bits 6..7 of a byte are left as they come: the six-bit field
+            // extraction ignores them; bit 5 is flipped in qh once for all four)
+            uint32_t u[R][4];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t qa = w[r].qa[c], qb = w[r].qb[c], hx = w[r].qh[c] ^ 0xaaaaaaaau;
+                constexpr uint32_t kLo = 0x0f0f0f0fu;
+                u[r][0] = (qa & kLo) | ((hx << 4) & ~kLo);  // v_bfi_b32
+                u[r][1] = (qb & kLo) | ((hx << 2) & ~kLo);
+                u[r][2] = ((qa >> 4) & kLo) | (hx & ~kLo);
+                u[r][3] = ((qb >> 4) & kLo) | ((hx >> 2) & ~kLo);
+            }
+            const float4* pc = xb + (c ^ klo);
+            const float4* pe = pc + 8 * kb;  // j = 0, 2
+            const float4* po = pc - 8 * kb;  // j = 1, 3
+            const float4 xv[4] = {pe[0], po[8], pe[16], po[24]};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    // (d*sc)*(u - 32) rounded once: fma(u, d*sc, -32*d*sc) is
-                    // the exact product before its one rounding
-                    const float uf = static_cast<float>((u[j] >> (8 * e)) & 0xffu);
-                    const float wv = fmaf(uf, dsc[j], off[j]);
-                    acc = fma(static_cast<double>(wv), static_cast<double>(xb[j * 32 + 4 * c + e]), acc);
+                    const float xe = e == 0 ? xv[j].x : e == 1 ? xv[j].y : e == 2 ? xv[j].z : xv[j].w;
+                    const double xd = static_cast<double>(xe);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const int q = static_cast<int>(u[r][j] << (26 - 8 * e)) >> 26;  // v_bfe_i32
+                        part[r][j] = fma(static_cast<double>(q), xd, part[r][j]);
+                    }
                 }
             }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float d = h2f(w[r].d);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[r] = fma(static_cast<double>(d * static_cast<float>(w[r].sc[j])), part[r][j], acc[r]);
         }
     };
     // the activation staged first, then each lane's units loaded and summed in
@@ -1022,26 +1056,36 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
     // bytes in registers, measured slower at every shape: 4096->32000 61 against
     // 39 us, 2048->32000 29 against 21 us, 5632->2048 10 against 8 us)
     const float* xt = x + static_cast<size_t>(blockIdx.y) * K;
-    for (int c = threadIdx.x; c < K / 4; c += kQ6Threads)
-        reinterpret_cast<float4*>(s_x)[c] = reinterpret_cast<const float4*>(xt)[c];
+    // stored swizzled: float4 f at f ^ swz(f), swz taking bits 5..7 of f to
+    // bits 0, 1 and 3, so the 32 units the lanes of a row read at once spread
+    // over all 64 banks instead of two sets of four
+    for (int c = threadIdx.x; c < K / 4; c += kQ6Threads) {
+        const int kv = (c >> 5) & 7;
+        reinterpret_cast<float4*>(s_x)[c ^ ((kv & 3) | ((kv & 4) << 1))] = reinterpret_cast<const float4*>(xt)[c];
+    }
     __syncthreads();
     for (int u = l; u < units; u += LPR) {
-        Raw w;
-        load_unit(u, w);
+        Raw w[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) load_unit(u, rb[r], w[r]);
         sum_unit(u, w);
     }
-    double tot;
-    if constexpr (LPR == 64) {
-        tot = wave_sum(acc);
-    } else {  // within each 32-lane half
-        acc += swz_xor<16>(acc);
-        acc += swz_xor<8>(acc);
-        acc += swz_xor<4>(acc);
-        acc += swz_xor<2>(acc);
-        acc += swz_xor<1>(acc);
-        tot = acc;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        double tot;
+        if constexpr (LPR == 64) {
+            tot = wave_sum(acc[r]);
+        } else {  // within each 32-lane half
+            double a = acc[r];
+            a += swz_xor<16>(a);
+            a += swz_xor<8>(a);
+            a += swz_xor<4>(a);
+            a += swz_xor<2>(a);
+            a += swz_xor<1>(a);
+            tot = a;
+        }
+        if (l == 0 && row + r < N) y[static_cast<size_t>(blockIdx.y) * N + row + r] = static_cast<float>(tot);
     }
-    if (l == 0 && row < N) y[static_cast<size_t>(blockIdx.y) * N + row] = static_cast<float>(tot);
 }
 
 // Q6_K for whole groups of 16 tokens (tensor_matmul_batch / the model's
@@ -1435,18 +1479,29 @@ hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t r
         y += done * rows;
         batch -= done;
     }
-    // 32 lanes per row up to 64 units (4096->32000 39 against 40 us, 2048->32000
-    // 21 against 29 us), 64 beyond (5632->2048 7.7 against 8.0 us)
+    // 32 lanes per row up to 64 units, 64 beyond; two rows per lane when that
+    // still leaves at least four workgroups per CU (4096->32000 34-36 against
+    // 38 us, 2048->32000 19 against 20 us; 5632->2048 stays at one row per
+    // lane: 7.0 against 8.0 us)
     const size_t units = cols / 64;  // 64-element units per row
     const bool half = units <= 64;
-    const size_t rpw = half ? 8 : 4;  // rows per workgroup
+    const size_t rpw1 = half ? 8 : 4;  // rows per workgroup at one row per lane
+    const bool two = rows >= 1024 * 2 * rpw1;
+    const size_t rpw = two ? 2 * rpw1 : rpw1;
     const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw), static_cast<unsigned>(batch));
-    if (half)
-        gemv_q6_k_kernel<32><<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
-                                                                             static_cast<int>(cols));
-    else
-        gemv_q6_k_kernel<64><<<grid, kQ6Threads, cols * sizeof(float), st>>>(W, x, y, static_cast<int>(rows),
-                                                                             static_cast<int>(cols));
+    const size_t lds = cols * sizeof(float);
+    const int n = static_cast<int>(rows), k = static_cast<int>(cols);
+    if (half) {
+        if (two)
+            gemv_q6_k_kernel<32, 2><<<grid, kQ6Threads, lds, st>>>(W, x, y, n, k);
+        else
+            gemv_q6_k_kernel<32, 1><<<grid, kQ6Threads, lds, st>>>(W, x, y, n, k);
+    } else {
+        if (two)
+            gemv_q6_k_kernel<64, 2><<<grid, kQ6Threads, lds, st>>>(W, x, y, n, k);
+        else
+            gemv_q6_k_kernel<64, 1><<<grid, kQ6Threads, lds, st>>>(W, x, y, n, k);
+    }
     return hipGetLastError();
 }
 

@@ -166,9 +166,11 @@ def test_q4_0_f32act_one_token_bitexact(ctx, oracle, k, n):
 
 
 # row counts that leave the last workgroup's waves partly or wholly idle, odd
-# and even super-block counts per row
+# and even super-block counts per row; one and two rows per lane (two from
+# 16384 rows at K <= 4096 and from 8192 rows beyond), with ragged last
+# workgroups in both
 @pytest.mark.parametrize("k,n", [(4096, 32000), (2048, 32000), (5632, 2048), (256, 64), (6144, 1000), (8192, 37),
-                                 (11008, 64)])
+                                 (11008, 64), (4096, 16390), (6144, 8203), (256, 16383)])
 def test_gemv_q6_k(ctx, oracle, k, n):
     rng = np.random.default_rng(3 * k + n)
     w = _w(rng, synth.Q6_K, n, k)
