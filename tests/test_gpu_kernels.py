@@ -184,6 +184,25 @@ def test_gemv_q6_k(ctx, oracle, k, n):
     t.free()
 
 
+@pytest.mark.parametrize("k,n", [(4096, 16400), (2048, 300)])
+def test_gemv_q6_k_nonfinite(ctx, oracle, k, n):
+    """An infinite or NaN activation: the rows' double sums give inf, -inf or
+    NaN (a zero weight times inf) exactly where the oracle's do, on both the
+    one- and the two-rows-per-lane paths."""
+    rng = np.random.default_rng(k + n)
+    w = _w(rng, synth.Q6_K, n, k)
+    t = ctx.upload("output.weight", synth.Q6_K, k, n, w)
+    for bad in (np.inf, -np.inf, np.nan):
+        x = synth.activations(rng, 1, k)[0]
+        x[k // 3] = bad
+        got = ctx.matvec(t, x)
+        want = oracle.matvec(w, synth.Q6_K, n, k, x)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        fin = ~np.isnan(want)
+        assert np.array_equal(got[fin], want[fin])
+    t.free()
+
+
 @pytest.mark.parametrize("k,n,batch", [(5632, 2048, 32), (2048, 300, 37), (11008, 17, 16), (256, 64, 20),
                                        (6144, 1, 48)])
 def test_q6_k_token_groups(ctx, oracle, k, n, batch):
