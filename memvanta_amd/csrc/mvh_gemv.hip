@@ -1088,110 +1088,125 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_kernel(const uint8_t* __
     }
 }
 
-// Q6_K for whole groups of 16 tokens (tensor_matmul_batch / the model's
-// prefill): the same exact f32 weights (d*sc)*q and double products as
-// gemv_q6_k_kernel, each weight dequantized once for eight tokens.  A
-// workgroup covers 16 rows x 16 tokens; thread (row quad, token half, unit
-// slot s) sums rows 4rq..4rq+3 x tokens 8th..8th+7 over the 64-element units
-// u = s, s + 32, .. of the rows (unit u: super-block u / 4, half g, sixteen-
-// column group h, as gemv_q6_k_kernel's), keeping 32 double partials; the
-// 32 slot partials of each (row, token) are then added in slot order.  The
-// four row-quad lanes of a unit read the same activations, so a wave's loads
-// touch 16 units.  Like gemv_q6_k_kernel the double sum runs in another
-// order than the reference's, with the same bound on the difference.
-constexpr int kQ6BRows = 16, kQ6BTok = 16, kQ6BSlots = 32;
+// Q6_K for whole groups of 16 tokens on the f64 matrix pipe
+// (v_mfma_f64_16x16x4f64): the same exact products ((d*sc)*q)*x in double
+// as dot_q6_k_fp32 (src/gguf_kernels.cpp:138-146), accumulated by the
+// MFMA in double.  A workgroup covers 16 rows x 16 tokens; its kQ6FWaves
+// waves take consecutive shares of the super-blocks and their partials are
+// added in wave order through LDS.  In a wave, lane (i = lane % 16, g =
+// lane / 16) gives the A operand (row i) and the B operand (token i) of
+// the 64-element unit g of each super-block (half g / 2, sixteen-column
+// group g % 2, as gemv_q6_k_kernel's units): step (j, c) of a super-block
+// is element 128*(g/2) + 32j + 16*(g%2) + c of both, so one MFMA adds four
+// elements' products for all 16 x 16 (row, token) pairs; each weight is
+// formed once for the 16 tokens (signed 6-bit extract, int -> double, times
+// d*sc: exact), each activation converted once for the 16 rows.  Four
+// accumulators take the steps in turn.  The MFMA's 16 x 16 result: lane L,
+// element r = row 4r + L/16, token L % 16.  The sum order differs from the
+// reference's element order, with the same bound on the difference as the
+// other Q6_K kernels.
+constexpr int kQ6FWaves = 8;  // 8 against 4: 5632->2048 at 32 tokens 23.8 against 27.4 us
+constexpr int kQ6FAcc = 4;    // accumulators taking the steps in turn
+typedef double v4f64 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void gemv_q6_k_batch_kernel(const uint8_t* __restrict__ W,
-                                                              const float* __restrict__ x, float* __restrict__ y,
-                                                              int N, int K) {
-    __shared__ double s_part[kQ6BSlots][kQ6BRows * kQ6BTok + 1];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int rq = lane & 3, th = wave & 1, slot = (lane >> 2) + 16 * (wave >> 1);
-    const int nsb = K / 256, nunits = 4 * nsb;
-    const int row0 = blockIdx.x * kQ6BRows + 4 * rq;
-    const int tok0 = blockIdx.y * kQ6BTok + 8 * th;
-    const size_t row_bytes = static_cast<size_t>(nsb) * 210;
-    const uint8_t* rbase[4];
+__global__ __launch_bounds__(64 * kQ6FWaves) void gemv_q6_k_batch_f64_kernel(const uint8_t* __restrict__ W,
+                                                                             const float* __restrict__ x,
+                                                                             float* __restrict__ y, int N, int K) {
+    __shared__ v4f64 s_red[kQ6FWaves][64];
+    const int nsb = K / 256;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, g = lane >> 4, half = g >> 1, hg = g & 1;
+    const int r0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
+    // rows past N use row N - 1 (not written)
+    const uint8_t* rb = W + static_cast<size_t>(min(r0 + li, N - 1)) * nsb * 210;
+    const float* xt = x + static_cast<size_t>(t0 + li) * K + 128 * half + 16 * hg;
+    const int s_beg = wave * nsb / kQ6FWaves, s_end = (wave + 1) * nsb / kQ6FWaves;
+    struct Raw {
+        uint32_t qa[4], qb[4], qh[4];
+        int sc[4];
+        uint32_t d;
+    };
+    // the unit's bytes: ql g/2*64 + hg*16 (j = 0, 2) and +32 (j = 1, 3), qh
+    // 128 + g/2*32 + hg*16, scales 192 + g/2*8 + hg + 2j, d at 208
+    auto load_unit = [&](int sb, Raw& w) __attribute__((always_inline)) {
+        const uint8_t* b = rb + static_cast<size_t>(sb) * 210;
+        const uint16_t* pa = reinterpret_cast<const uint16_t*>(b + half * 64 + hg * 16);
+        const uint16_t* pb = reinterpret_cast<const uint16_t*>(b + half * 64 + 32 + hg * 16);
+        const uint16_t* ph = reinterpret_cast<const uint16_t*>(b + 128 + half * 32 + hg * 16);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) rbase[r] = W + static_cast<size_t>(min(row0 + r, N - 1)) * row_bytes;
-
-    double acc[4][8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) acc[r][k] = 0.0;
-    for (int u = slot; u < nunits; u += kQ6BSlots) {
-        const int sb = u >> 2, g = (u >> 1) & 1, h = u & 1;
-        // the unit's bytes of each row: ql at g*64 + h*16 (l = 0, 2) and
-        // g*64 + 32 + h*16 (l = 1, 3), qh at 128 + g*32 + h*16, scales
-        // 192 + g*8 + h + 2l, d at 208 (2-byte aligned: 16-bit loads)
-        uint32_t qa[4][4], qb[4][4], qh[4][4];
-        float dsc[4][4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint8_t* b = rbase[r] + static_cast<size_t>(sb) * 210;
-            const uint16_t* pa = reinterpret_cast<const uint16_t*>(b + g * 64 + h * 16);
-            const uint16_t* pb = reinterpret_cast<const uint16_t*>(b + g * 64 + 32 + h * 16);
-            const uint16_t* ph = reinterpret_cast<const uint16_t*>(b + 128 + g * 32 + h * 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                qa[r][i] = pa[2 * i] | (static_cast<uint32_t>(pa[2 * i + 1]) << 16);
-                qb[r][i] = pb[2 * i] | (static_cast<uint32_t>(pb[2 * i + 1]) << 16);
-                qh[r][i] = ph[2 * i] | (static_cast<uint32_t>(ph[2 * i + 1]) << 16);
-            }
-            const float d = h2f(*reinterpret_cast<const uint16_t*>(b + 208));
-            const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + g * 8 + h);
-#pragma unroll
-            for (int l = 0; l < 4; ++l) dsc[r][l] = d * static_cast<float>(sc[2 * l]);
+        for (int i = 0; i < 4; ++i) {
+            w.qa[i] = pa[2 * i] | (static_cast<uint32_t>(pa[2 * i + 1]) << 16);
+            w.qb[i] = pb[2 * i] | (static_cast<uint32_t>(pb[2 * i + 1]) << 16);
+            w.qh[i] = ph[2 * i] | (static_cast<uint32_t>(ph[2 * i + 1]) << 16);
         }
+        const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + half * 8 + hg);
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
+        for (int j = 0; j < 4; ++j) w.sc[j] = sc[2 * j];
+        w.d = *reinterpret_cast<const uint16_t*>(b + 208);
+    };
+    v4f64 acc[kQ6FAcc];
 #pragma unroll
-            for (int jq = 0; jq < 4; ++jq) {  // columns 4jq .. 4jq+3 of the group
-                float4 xv[8];
+    for (int a = 0; a < kQ6FAcc; ++a) acc[a] = v4f64{0.0, 0.0, 0.0, 0.0};
+    if (s_beg < s_end) {
+        Raw cur;
+        load_unit(s_beg, cur);
+        for (int sb = s_beg; sb < s_end; ++sb) {
+            Raw nxt;
+            load_unit(min(sb + 1, s_end - 1), nxt);  // the next unit in flight (the last one loads itself again)
+            // the lane's 64 activations of the super-block, all requested at once
+            const float* xs = xt + static_cast<size_t>(sb) * 256;
+            float4 xa[4][4];
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    xv[k] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(tok0 + k) * K + sb * 256 +
-                                                             g * 128 + l * 32 + h * 16 + 4 * jq);
-                double wv[4][4];
+            for (int c4 = 0; c4 < 4; ++c4)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // the 6-bit codes u = q + 32 of the four columns as bytes
-                    // (nibble of ql, bits 2l..2l+1 of qh above it); each
-                    // weight (d*sc)*(u - 32) by one fma from its exact value
-                    const uint32_t lw = (l & 1) ? qb[r][jq] : qa[r][jq];
-                    const uint32_t hw = qh[r][jq];
-                    const uint32_t lo4 = (l >> 1) ? (lw >> 4) & 0x0f0f0f0fu : lw & 0x0f0f0f0fu;
-                    const uint32_t hi2 = (2 * l <= 4 ? hw << (4 - 2 * l) : hw >> (2 * l - 4)) & 0x30303030u;
-                    const uint32_t u = lo4 | hi2;
-                    const float off = -32.0f * dsc[r][l];  // exact (a power-of-two multiple)
+                for (int j = 0; j < 4; ++j) xa[c4][j] = reinterpret_cast<const float4*>(xs + 32 * j)[c4];
+            const float d = h2f(cur.d);
+            double dsc[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        wv[r][e] = static_cast<double>(fmaf(static_cast<float>((u >> (8 * e)) & 0xffu), dsc[r][l], off));
-                }
+            for (int j = 0; j < 4; ++j) dsc[j] = static_cast<double>(d * static_cast<float>(cur.sc[j]));
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const double xd[4] = {static_cast<double>(xv[k].x), static_cast<double>(xv[k].y),
-                                          static_cast<double>(xv[k].z), static_cast<double>(xv[k].w)};
+            for (int c4 = 0; c4 < 4; ++c4) {  // columns 4c4 .. 4c4+3 of the unit's four groups
+                const float4* xv = xa[c4];
+                // 6-bit codes q + 32 four to a dword, bit 5 flipped (bits 6..7 ignored by the extract)
+                const uint32_t qa = cur.qa[c4], qb = cur.qb[c4], hx = cur.qh[c4] ^ 0xaaaaaaaau;
+                constexpr uint32_t kLo = 0x0f0f0f0fu;
+                const uint32_t u[4] = {(qa & kLo) | ((hx << 4) & ~kLo), (qb & kLo) | ((hx << 2) & ~kLo),
+                                       ((qa >> 4) & kLo) | (hx & ~kLo), ((qb >> 4) & kLo) | ((hx >> 2) & ~kLo)};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
+                for (int e = 0; e < 4; ++e) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) acc[r][k] = fma(wv[r][e], xd[e], acc[r][k]);
+                    for (int j = 0; j < 4; ++j) {
+                        const int q = static_cast<int>(u[j] << (26 - 8 * e)) >> 26;
+                        const double a = static_cast<double>(q) * dsc[j];  // w, exact
+                        const float xe = e == 0 ? xv[j].x : e == 1 ? xv[j].y : e == 2 ? xv[j].z : xv[j].w;
+                        const double bx = static_cast<double>(xe);
+                        v4f64& ac = acc[(4 * e + j) % kQ6FAcc];
+                        ac = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bx, ac, 0, 0, 0);
+                    }
                 }
             }
+            cur = nxt;
         }
     }
+    v4f64 part = acc[0];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) s_part[slot][(4 * rq + r) * kQ6BTok + 8 * th + k] = acc[r][k];
+    for (int a = 1; a < kQ6FAcc; ++a) part += acc[a];
+    s_red[wave][lane] = part;
     __syncthreads();
-    const int orow = blockIdx.x * kQ6BRows + t / kQ6BTok, otok = blockIdx.y * kQ6BTok + t % kQ6BTok;
-    double tot = 0.0;
+    if (wave == 0) {
+        v4f64 tot = s_red[0][lane];
 #pragma unroll
-    for (int s2 = 0; s2 < kQ6BSlots; ++s2) tot += s_part[s2][t];
-    if (orow < N) y[static_cast<size_t>(otok) * N + orow] = static_cast<float>(tot);
+        for (int w = 1; w < kQ6FWaves; ++w) tot += s_red[w][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = r0 + 4 * r + g;
+            if (row < N) y[static_cast<size_t>(t0 + li) * N + row] = static_cast<float>(tot[r]);
+        }
+    }
 }
+
+// rows x tokens of the Q6_K token-group tile
+constexpr int kQ6BRows = 16, kQ6BTok = 16;
 
 // F32 weights (dot_f32_simd, src/gguf_kernels.cpp:228-234, as tensor_matvec
 // and tensor_matmul_batch call it): per (row, token) eight accumulators
@@ -1472,7 +1487,8 @@ hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t r
         // whole groups of kQ6BTok tokens on the batch kernel, the rest per token below
         const size_t groups = batch / kQ6BTok;
         const dim3 bgrid(static_cast<unsigned>((rows + kQ6BRows - 1) / kQ6BRows), static_cast<unsigned>(groups));
-        gemv_q6_k_batch_kernel<<<bgrid, 256, 0, st>>>(W, x, y, static_cast<int>(rows), static_cast<int>(cols));
+        gemv_q6_k_batch_f64_kernel<<<bgrid, 64 * kQ6FWaves, 0, st>>>(W, x, y, static_cast<int>(rows),
+                                                                     static_cast<int>(cols));
         const size_t done = groups * kQ6BTok;
         if (done == batch) return hipGetLastError();
         x += done * cols;
