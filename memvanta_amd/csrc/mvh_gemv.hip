@@ -506,6 +506,66 @@ __global__ __launch_bounds__(256) void gemv_f32act_persistent_q8_0(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
     gemv_f32act_persistent<kQ8_0, 4>(W, x, y, N, nb, ntiles);
 }
+// dot_q8_0_fp32 for one token (src/gguf_kernels.cpp:111-120), K = 16 * UB
+// blocks: the row-group layout of the Q4_0 x Q8 decode GEMV.  A wave holds 4
+// rows, one per 16-lane group; lane g of a group owns the row's blocks
+// UB*g .. UB*g + UB - 1 (UB * 34 contiguous bytes, 8-byte loads issued before
+// the activation staging), turns them into (d_b, s_b) pairs (s_b the block's
+// exact eight-lane sum, f32act_block_sum), and the row's chain
+// sum = fma(d_b, s_b, sum) walks the group's lanes in block order: at stage st
+// every lane redoes its UB fmas from its left neighbour's value (DPP
+// row_ror:1), lane g's value being final from stage g on.  The activation is
+// staged once per workgroup (4 waves, 16 rows), block b at float
+// 32b + 4*(b / UB): the 16 lanes of a group then read 16 different bank
+// quads at every step.
+__device__ __forceinline__ float dpp_row_ror1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false));
+}
+
+template <int UB>
+__global__ __launch_bounds__(256) void gemv_q8_0_f32act_rows16(const uint8_t* __restrict__ W,
+                                                                const float* __restrict__ x, float* __restrict__ y,
+                                                                int N) {
+    constexpr int nb = 16 * UB, kW2 = UB * 34 / 8;  // blocks per row, 8-byte words per lane
+    __shared__ __align__(16) float s_x[32 * nb + 4 * 16];
+    const int t = threadIdx.x, lane = t & 63, g = lane & 15;
+    const int row = blockIdx.x * 16 + (t >> 6) * 4 + (lane >> 4);
+    // rows past N read row N - 1 and are not written
+    const uint2* src = reinterpret_cast<const uint2*>(W + static_cast<size_t>(min(row, N - 1)) * (nb * 34) +
+                                                      static_cast<size_t>(g) * (UB * 34));
+    uint32_t w[2 * kW2];
+#pragma unroll
+    for (int k = 0; k < kW2; ++k) {
+        const uint2 v = src[k];
+        w[2 * k] = v.x;
+        w[2 * k + 1] = v.y;
+    }
+    for (int c = t; c < nb * 8; c += 256) {
+        const int b = c >> 3;
+        *reinterpret_cast<float4*>(s_x + 32 * b + 4 * (b / UB) + 4 * (c & 7)) = reinterpret_cast<const float4*>(x)[c];
+    }
+    __syncthreads();
+    float pd[UB], ps[UB];
+#pragma unroll
+    for (int j = 0; j < UB; ++j) {
+        uint32_t dbits, qs[Blk<kQ8_0>::kQdw];
+        unit_block<kQ8_0>(w, j, dbits, qs);
+        const int b = UB * g + j;
+        pd[j] = Blk<kQ8_0>::scale(dbits);
+        ps[j] = f32act_block_sum<kQ8_0>(qs, s_x + 32 * b + 4 * g);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+        const float in = dpp_row_ror1(sum);
+        float acc = g == 0 ? 0.0f : in;
+#pragma unroll
+        for (int j = 0; j < UB; ++j) acc = fmaf(pd[j], ps[j], acc);
+        sum = acc;
+    }
+    if (g == 15 && row < N) y[row] = sum;
+}
+
 __global__ __launch_bounds__(256) void gemv_f32act_persistent_nq4_0(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int N, int nb, int ntiles) {
     gemv_f32act_persistent<kNQ4_0, 4>(W, x, y, N, nb, ntiles);
@@ -1361,6 +1421,17 @@ template <uint32_t TYPE>
 static hipError_t launch_f32act_any(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols,
                                     size_t batch, hipStream_t st) {
     if (!rows || !batch) return hipSuccess;
+    if constexpr (TYPE == kQ8_0) {
+        // one token at K = 2048 / 4096: the row-group kernel
+        if (batch == 1 && (cols == 2048 || cols == 4096) && (reinterpret_cast<uintptr_t>(W) & 7) == 0) {
+            const unsigned grid = static_cast<unsigned>((rows + 15) / 16);
+            if (cols == 2048)
+                gemv_q8_0_f32act_rows16<4><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows));
+            else
+                gemv_q8_0_f32act_rows16<8><<<grid, 256, 0, st>>>(W, x, y, static_cast<int>(rows));
+            return hipGetLastError();
+        }
+    }
     if (batch == 1 && cols % 256 == 0 && cols / 128 <= 64) {
         static const int cus = [] {
             int dev = 0;

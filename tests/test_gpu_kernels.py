@@ -139,8 +139,12 @@ def test_gemv_q4_0_prequantized_bitexact(ctx, oracle, k, n):
     t.free()
 
 
+# one token at K = 2048 / 4096 runs the row-group kernel (16 rows per
+# workgroup; ragged last workgroups at 37 and 1001 rows), other K the
+# persistent or per-token kernels
 @pytest.mark.parametrize("k,n", [(288, 32000), (2048, 2048), (2048, 256), (5632, 2048), (4096, 4096), (288, 768),
-                                 (4096, 37), (256, 130), (8192, 33), (11008, 64), (16384, 5)])
+                                 (4096, 37), (256, 130), (8192, 33), (11008, 64), (16384, 5), (2048, 11264),
+                                 (2048, 2560), (2048, 1001)])
 def test_gemv_q8_0_bitexact(ctx, oracle, k, n):
     rng = np.random.default_rng(7 * k + n)
     w = _w(rng, synth.Q8_0, n, k)
