@@ -1551,6 +1551,22 @@ hipError_t launch_gemv_f16(const uint16_t* W, const float* x, float* y, size_t r
     return hipGetLastError();
 }
 
+size_t gemv_decode_rows_per_wg(uint32_t type, size_t rows, size_t cols) {
+    switch (type) {
+        case kQ4_0: return gemv_q4_0_rows16_ok(cols) ? 16 : 0;
+        case kQ8_0: return cols == 2048 || cols == 4096 ? 16 : 0;  // gemv_q8_0_f32act_rows16
+        case kQ6_K: {  // the one-token choice of launch_gemv_q6_k below
+            if (cols % 256) return 0;
+            const size_t units = cols / 64;
+            const bool half = units <= 64;
+            const size_t rpw1 = half ? 8 : 4;
+            const bool two = rows >= 1024 * 2 * rpw1;
+            return half ? (two ? 16 : 8) : 8;
+        }
+    }
+    return 0;
+}
+
 hipError_t launch_gemv_q6_k(const uint8_t* W, const float* x, float* y, size_t rows, size_t cols, size_t batch,
                             hipStream_t st) {
     if (!rows || !batch) return hipSuccess;

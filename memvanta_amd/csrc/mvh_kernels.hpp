@@ -45,6 +45,11 @@ hipError_t launch_gemv_f16(const uint16_t* W, const float* x, float* y, size_t r
 // x != nullptr quantizes the fp32 input inside the kernel; otherwise aq
 // (16-byte aligned) / ad are the Q8 input.
 bool gemv_q4_0_rows16_ok(size_t cols);
+// Rows each workgroup of the one-token decode GEMV of a Q4_0 (pre-quantized
+// Q8 input), Q8_0 or Q6_K (fp32 input) tensor reads: workgroup c reads rows
+// [c*r, (c+1)*r), one contiguous chunk of the tensor, and runs on XCD c % 8
+// (the L2 warm-up's map); 0 when that kernel reads no such chunks.
+size_t gemv_decode_rows_per_wg(uint32_t type, size_t rows, size_t cols);
 hipError_t launch_gemv_q4_0_rows16(const uint8_t* W, const float* x, const int8_t* aq, const float* ad, float* y,
                                    size_t rows, size_t cols, hipStream_t st);
 // the same kernel over native BlockQ4_0 x BlockQ8_0 (xq 4-byte aligned)

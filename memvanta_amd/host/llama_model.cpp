@@ -192,10 +192,14 @@ LlamaModel::LlamaModel(const std::string& path, int device, std::size_t ctx_over
     logits_.resize(c_.vocab);
     fused_attn_ = kv_type_ == mvh::kKvF16 && mvh::attn_decode_fused_ok(c_.head_dim(), c_.n_ctx, page_tokens_);
     // default shares: what the RMSNorm and attention launches can fetch while
-    // their own work runs (the SwiGLU launch warming ffn_down measured slower);
-    // MVH_L2_WARM=0 turns the warm-up off, "a,b,c,d,e" sets the five shares
-    const float defaults[kWarmSites] = {0.5f, 1.0f, 0.3f, 0.0f, 0.15f};
-    std::copy(defaults, defaults + kWarmSites, warm_frac_);
+    // their own work runs (the SwiGLU launch warming ffn_down measured
+    // slower); with Q8_0 layers (the TinyLlama shape's 5.6 MB q|k|v) the
+    // attention norm warms all of q|k|v.  MVH_L2_WARM=0 turns the warm-up
+    // off, "a,b,c,d,e" sets the five shares
+    const bool q8_layers = !layers_.empty() && (layers_[0].fused_qkv ? layers_[0].qkv : layers_[0].q).type == 8;
+    const float defaults_q4[kWarmSites] = {0.5f, 1.0f, 0.3f, 0.0f, 0.15f};
+    const float defaults_q8[kWarmSites] = {1.0f, 1.0f, 0.3f, 0.0f, 0.15f};
+    std::copy(q8_layers ? defaults_q8 : defaults_q4, (q8_layers ? defaults_q8 : defaults_q4) + kWarmSites, warm_frac_);
     if (const char* e = getenv("MVH_L2_WARM")) {
         float f[kWarmSites] = {};
         const int n = std::sscanf(e, "%f,%f,%f,%f,%f", &f[0], &f[1], &f[2], &f[3], &f[4]);
@@ -382,19 +386,21 @@ void LlamaModel::gemm(const Tensor& w, const float* x, const int8_t* q8, const f
     prof_stop(w, B);
 }
 
-// The L2 warm-up of a decode GEMV's weights (mvh::l2_warm): a Q4_0 GEMV on
-// the one-token kernel (gemv_q4_rows16: workgroup c reads rows 16c..16c+15,
-// one contiguous chunk) has its chunks from the fraction `from` to from +
-// share pulled into the L2 of the XCD that will read them; other GEMVs get
-// none.
+// The L2 warm-up of a decode GEMV's weights (mvh::l2_warm): a GEMV whose
+// one-token kernel reads one contiguous chunk of rows per workgroup
+// (mvh::gemv_decode_rows_per_wg: Q4_0, Q8_0 at K = 2048 / 4096, Q6_K) has its
+// chunks from the fraction `from` to from + share pulled into the L2 of the
+// XCD that will read them; other GEMVs get none.
 static mvh::L2Warm l2_warm_for(std::uint32_t type, std::size_t rows, std::size_t cols, const void* d, float from,
                                float share) {
     mvh::L2Warm r;
-    if (type != 2 || !mvh::gemv_q4_0_rows16_ok(cols) || share <= 0.0f) return r;
-    const float chunks = static_cast<float>((rows + 15) / 16);
-    const unsigned whole = static_cast<unsigned>(rows / 16);  // a partial last chunk is left cold
+    const std::size_t per_wg = mvh::gemv_decode_rows_per_wg(type, rows, cols);
+    const std::size_t row_bytes = type == 2 ? cols / 32 * 18 : type == 8 ? cols / 32 * 34 : cols / 256 * 210;
+    if (!per_wg || share <= 0.0f || (per_wg * row_bytes) % 16) return r;
+    const float chunks = static_cast<float>((rows + per_wg - 1) / per_wg);
+    const unsigned whole = static_cast<unsigned>(rows / per_wg);  // a partial last chunk is left cold
     r.base = static_cast<const uint8_t*>(d);
-    r.chunk = static_cast<unsigned>(16 * (cols / 32) * 18);  // cols % 256 == 0: a multiple of 16
+    r.chunk = static_cast<unsigned>(per_wg * row_bytes);
     r.c0 = std::min(whole, static_cast<unsigned>(from * chunks));
     r.c1 = std::min(whole, static_cast<unsigned>((from + share) * chunks));
     return r;
