@@ -873,14 +873,18 @@ __global__ __launch_bounds__(256) void batch_f32act_rows2_kernel(const uint8_t* 
                     const uint8_t* blk = &s_w[buf][(2 * rp + r) * kU + kB * jb];
                     const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
                     if constexpr (TYPE == kQ4_0) {
-                        const uint32_t pair =
-                            static_cast<uint32_t>(blk[2 + j]) | (static_cast<uint32_t>(blk[10 + j]) << 8);
-                        const uint32_t lo = pair & 0x0f0fu, hi = (pair >> 4) & 0x0f0fu;
-                        // float(q - 8): the nibble converted exactly, minus 8 exactly
-                        q[r][0] = (static_cast<float>(lo & 0xffu) - 8.0f) * d;
-                        q[r][1] = (static_cast<float>(lo >> 8) - 8.0f) * d;
-                        q[r][2] = (static_cast<float>(hi & 0xffu) - 8.0f) * d;
-                        q[r][3] = (static_cast<float>(hi >> 8) - 8.0f) * d;
+                        // bytes j and j + 8 of the nibbles: elements j, j + 8 (low
+                        // nibbles), j + 16, j + 24 (high).  q ^ 8 read as a signed
+                        // 4-bit field is q - 8, so one signed extract (v_bfe_i32,
+                        // written as shifts: __builtin_amdgcn_sbfe's result is
+                        // converted as unsigned by this compiler) gives it;
+                        // float(q - 8) * d is then the reference's product
+                        const uint32_t px =
+                            (static_cast<uint32_t>(blk[2 + j]) | (static_cast<uint32_t>(blk[10 + j]) << 8)) ^ 0x8888u;
+                        q[r][0] = static_cast<float>(static_cast<int>(px << 28) >> 28) * d;
+                        q[r][1] = static_cast<float>(static_cast<int>(px << 20) >> 28) * d;
+                        q[r][2] = static_cast<float>(static_cast<int>(px << 24) >> 28) * d;
+                        q[r][3] = static_cast<float>(static_cast<int>(px << 16) >> 28) * d;
                     } else {
 #pragma unroll
                         for (int m = 0; m < 4; ++m)

@@ -275,6 +275,38 @@ def test_matmul_v06_ref_mode_lanes_bitexact(ctx, oracle, ty, name, batch, k, n):
     t.free()
 
 
+def test_matmul_v06_ref_mode_special_scales(ctx, oracle):
+    """Default prefill numerics on the two-row Q4_0 kernel with block scales
+    that are +0, -0, f16 subnormals, negative, +-inf and NaN, and activations
+    holding zeros, -0 and float denormals: bit-identical to the oracle (NaN
+    exactly where it has NaN).  Rows 0..31 mix every special scale (the
+    reference's subtract-and-multiply path), rows 32..63 only signed zeros,
+    rows 64..95 only subnormal and negative scales (the fma path)."""
+    rng = np.random.default_rng(77)
+    k, n, batch = 2048, 96, 32
+    nb = k // 32
+    w = _w(rng, synth.Q4_0, n, k).reshape(n, nb, 18).copy()
+    sets = [(range(0, 32), [0x0000, 0x8000, 0x0001, 0x83FF, 0x7C00, 0xFC00, 0x7E00, 0xBC00]),
+            (range(32, 64), [0x0000, 0x8000]), (range(64, 96), [0x0001, 0x03FF, 0x8001, 0xC500, 0x8400])]
+    for rows, vals in sets:
+        for r in rows:
+            for b in rng.choice(nb, size=6, replace=False):
+                v = int(rng.choice(vals))
+                w[r, b, 0], w[r, b, 1] = v & 0xFF, v >> 8
+    w = w.reshape(-1)
+    t = ctx.upload("blk.0.attn_q.weight", synth.Q4_0, k, n, w)
+    x = synth.activations(rng, batch, k)
+    x[:, ::97] = 0.0
+    x[:, 5::101] = -0.0
+    x[:, 7::89] = np.float32(1e-40) * np.sign(x[:, 7::89] + np.float32(0.5))
+    got = ctx.matmul_batch_v06(t, x, capi.MVH_ACT_REF)
+    want = oracle.matmul_batch_v06(w, synth.Q4_0, n, k, x, is_ffn=False, force_q8=False)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(bits(got[fin]), bits(want[fin]))
+    t.free()
+
+
 @pytest.mark.parametrize("ty", [synth.Q4_0, synth.Q8_0])
 @pytest.mark.parametrize("batch,k,n", [(2, 1024, 96), (32, 4096, 512), (7, 288, 768)])
 def test_matmul_v06_q8_mode_bitexact(ctx, oracle, ty, batch, k, n):
