@@ -397,7 +397,10 @@ hipError_t launch_gemm_q4_0_q8_mfma(const uint8_t* W, const int8_t* aq, const fl
             W, aq, ad, y, N, nb, Bn);
         return hipGetLastError();
     }
-    if ((batch <= 32 && gx < tg2_min) || gx * g32 <= 1024) {
+    // (17..32 tokens: the row-tile count alone decides -- the fused q|k|v's
+    // 768 row tiles on 32-token tiles, pp512 11.84 -> 11.95-12.03 K tok/s;
+    // up to 16 tokens a 32-token tile would be half empty)
+    if (batch <= 32 ? batch <= 16 || gx < tg2_min : gx * g32 <= 1024) {
         if (gx * g16 <= 1024)
             gemm_q4_0_q8_mfma_kernel<1, 4><<<dim3(gx, static_cast<unsigned>(g16)), 64, 0, st>>>(W, aq, ad, y, N, nb, Bn);
         else
