@@ -188,7 +188,7 @@ def test_gemv_q6_k(ctx, oracle, k, n):
     t.free()
 
 
-@pytest.mark.parametrize("k,n", [(4096, 16400), (2048, 300)])
+@pytest.mark.parametrize("k,n", [(4096, 16400), (2048, 300), (5632, 300)])
 def test_gemv_q6_k_nonfinite(ctx, oracle, k, n):
     """An infinite or NaN activation: the rows' double sums give inf, -inf or
     NaN (a zero weight times inf) exactly where the oracle's do, on both the
