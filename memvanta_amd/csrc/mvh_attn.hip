@@ -832,7 +832,9 @@ __global__ __launch_bounds__(kHT) void attn_decode_head_kernel(
         } else {
             out[o] = acc[0];
         }
-        if (q8) {  // quantize_q8 of each 32-element block of the output (32 / DPL lanes)
+        // quantize_q8 of each 32-element block of the output (32 / DPL lanes;
+        // a slice narrower than a block is launched without q8)
+        if (SW % 32 == 0 && q8) {
             constexpr int L = 32 / DPL;
             float m = fabsf(acc[0]);
             if constexpr (DPL == 2) m = fmaxf(m, fabsf(acc[DPL - 1]));
@@ -1338,8 +1340,10 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
         return e ? atoi(e) : -1;
     }();
     // default: four slices per head at head_dim 128 (tg128 562.9 against
-    // 561.8 tok/s with two, 543 with one), two at 64
-    const int ns = ns_env >= 0 ? ns_env : hd == 128 ? 4 : 2;
+    // 561.8 tok/s with two, 543 with one); at 64 four when no Q8 output is
+    // written (16-element slices; the TinyLlama shape 1256.6 against 1250.9
+    // tok/s with two), else two
+    const int ns = ns_env >= 0 ? ns_env : hd == 128 || !q8 ? 4 : 2;
     // the LDS-staged kernel takes q, k and v as one buffer (the decode step's q|k|v)
     const bool qkv_one = k == q + n_head * hd && v == k + n_head_kv * hd && page_stride <= INT32_MAX;
     if ((hd == 128 || hd == 64) && max_ctx <= static_cast<size_t>(kHMaxCtx) && ns > 0 && qkv_one) {
@@ -1356,6 +1360,7 @@ hipError_t launch_attn_decode_fused(const float* q, const float* k, const float*
         else if (hd == 128 && ns == 4) MVH_ATTN_HEAD(128, 4);
         else if (hd == 128) MVH_ATTN_HEAD(128, 2);
         else if (ns == 1) MVH_ATTN_HEAD(64, 1);
+        else if (ns == 4 && !q8) MVH_ATTN_HEAD(64, 4);  // 16-element slices: no Q8 blocks of the output
         else MVH_ATTN_HEAD(64, 2);
 #undef MVH_ATTN_HEAD
         return hipGetLastError();

@@ -443,10 +443,11 @@ def test_attention_variants_vs_oracle(tmp_path, override):
     """The kernels the tuning overrides select, in a child process that sets
     the override before any GPU call: the fused F16 decode attention with 1 or
     2 slices per head (LDS-staged kernel) or 0 (the register-staged one) --
-    the default, 4 at head_dim 128 and 2 at 64, runs in every other model
+    the default, 4 at head_dim 128 and at 64 without a Q8 output (the GQA
+    model's Q8_0 o projection), 2 at 64 otherwise, runs in every other model
     test --, the per-(head, token) prefill scores kernel in place of the
     K-tile one for F16 chunks of 8..32 tokens, and the decode step's L2
-    warm-up of the Q4_0 GEMV weights off or at every site in full (the norm,
+    warm-up of the GEMV weights off or at every site in full (the norm,
     attention and SwiGLU launches then carry warm-up workgroups over whole
     tensors).  Head dims 128 (MHA) and 64 (GQA 32/4), prefill chunks of 32
     ending in ragged ones (12 and 14 tokens), decode positions past 256 (a
