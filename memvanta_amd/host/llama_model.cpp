@@ -214,6 +214,7 @@ LlamaModel::~LlamaModel() {
     for (Lane& l : lanes_)
         if (l.st) (void)hipStreamSynchronize(l.st);
     if (graph_) (void)hipGraphExecDestroy(graph_);
+    if (graphk_) (void)hipGraphExecDestroy(graphk_);
     for (hipEvent_t e : kv_done_)
         if (e) (void)hipEventDestroy(e);
     for (void* p : allocs_) (void)hipFree(p);
@@ -699,21 +700,38 @@ std::vector<int> LlamaModel::generate_greedy(int token, std::size_t n) {
     } else if (!graph_) {
         // the step reads token and position from device memory and its argmax
         // writes the next token and advances the position: one graph serves
-        // every step
-        hipGraph_t g{};
-        check(hipStreamBeginCapture(ln_->st, hipStreamCaptureModeThreadLocal), "begin capture");
-        try {
-            decode_step(d_tok_, true, true);
-        } catch (...) {  // leave the stream out of capture mode for the calls that follow
-            if (hipStreamEndCapture(ln_->st, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
-            throw;
-        }
-        check(hipStreamEndCapture(ln_->st, &g), "end capture");
-        check(hipGraphInstantiate(&graph_, g, nullptr, nullptr, 0), "graph instantiate");
-        (void)hipGraphDestroy(g);
+        // every step; a second graph of gsteps_ consecutive steps is launched
+        // while at least that many tokens remain (one graph launch per 8
+        // tokens instead of per token: 7B-shape tg128 666.0 -> 670.2 tok/s with
+        // 4 steps, 670.5 with 16; MVH_GRAPH_STEPS overrides, 1 = per token)
+        static const int gsteps = [] {
+            const char* e = getenv("MVH_GRAPH_STEPS");
+            return e ? std::max(1, atoi(e)) : kGraphSteps;
+        }();
+        gsteps_ = gsteps;
+        auto capture = [&](int steps, hipGraphExec_t* exec) {
+            hipGraph_t g{};
+            check(hipStreamBeginCapture(ln_->st, hipStreamCaptureModeThreadLocal), "begin capture");
+            try {
+                for (int i = 0; i < steps; ++i) decode_step(d_tok_, true, true);
+            } catch (...) {  // leave the stream out of capture mode for the calls that follow
+                if (hipStreamEndCapture(ln_->st, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            check(hipStreamEndCapture(ln_->st, &g), "end capture");
+            const hipError_t e = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            check(e, "graph instantiate");
+        };
+        capture(1, &graph_);
+        if (gsteps_ > 1) capture(gsteps_, &graphk_);
     }
-    if (!profiling_)
-        for (std::size_t i = 0; i < n; ++i) check(hipGraphLaunch(graph_, ln_->st), "graph launch");
+    if (!profiling_) {
+        std::size_t i = 0;
+        if (graphk_)
+            for (; i + gsteps_ <= n; i += gsteps_) check(hipGraphLaunch(graphk_, ln_->st), "graph launch");
+        for (; i < n; ++i) check(hipGraphLaunch(graph_, ln_->st), "graph launch");
+    }
     check(hipMemcpyAsync(pin_, d_hist_ + pos_, n * 4, hipMemcpyDeviceToHost, ln_->st), "token copy");
     check(hipStreamSynchronize(ln_->st), "sync");
     std::memcpy(out.data(), pin_, n * 4);

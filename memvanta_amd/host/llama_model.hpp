@@ -136,7 +136,10 @@ private:
     int* d_prompt_{};                       // token ids of a prefill call, chunk i's at d_prompt_ + i
     int* pin_{};         // pinned host staging
     std::vector<float> logits_;
-    hipGraphExec_t graph_{};
+    hipGraphExec_t graph_{};   // one decode step (token and position read from device memory)
+    hipGraphExec_t graphk_{};  // gsteps_ consecutive decode steps (gsteps_ > 1)
+    static constexpr int kGraphSteps = 8;
+    int gsteps_ = 1;
     bool fused_attn_{};  // decode attention in one launch (launch_attn_decode_fused; F16 pages)
     // L2 warm-up during a decode step (l2_warm), as shares of a GEMV's
     // weights: q|k|v by the RMSNorm before it, o by the attention, gate|up by
