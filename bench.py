@@ -9,8 +9,8 @@ reference's real_model_bench (benchmarks/real_model_bench.cpp:20-27):
 
 * tg128: reset, prefill a 128-token seed (untimed), then 128 greedy decode
   tokens from token 17, timed -- the reference's tg rep.  One step = one whole
-  tg128 rep; the 128 tokens run as the device-resident greedy loop (one
-  captured HIP graph per token, argmax on the device) at positions 128..255.
+  tg128 rep; the 128 tokens run as the device-resident greedy loop (captured
+  HIP graphs of eight decode steps, argmax on the device) at positions 128..255.
   `value` = 128 * K / (the K reps' decode seconds) (tok/s); `ms_per_step` =
   the mean decode time of one rep.  The per-call API rate (forward() + host
   argmax, as the reference's loop does) is reported beside it.
@@ -1043,7 +1043,7 @@ def main():
             "greedy_ids_head": ids[:8],
             "model_write_s": round(t_write, 1),
             "model_load_s": round(t_load, 2),
-            "timing": "tg: device-resident greedy loop (one HIP graph per token), wall clock between "
+            "timing": "tg: device-resident greedy loop (HIP graphs of eight decode steps), wall clock between "
                       "device synchronizations; pp: host-driven chunks, wall clock",
             "vs_baseline_basis": "published reference tg128 1.52 tok/s (real OpenLLaMA-7B-v2 Q4_0, CPU, 4 threads); "
                                  "decode numerics do not depend on the prefill mode",
